@@ -1,0 +1,118 @@
+/* lvattn: MI355X (gfx950) continuous-batching attention path -- the C ABI.
+ *
+ * Every entry point takes plain device pointers, element strides and sizes, enqueues its kernels on `stream`
+ * (a hipStream_t passed as void*; NULL is the default stream), never synchronises the host, never allocates,
+ * and returns LV_OK or an error status whose message lv_last_error() returns (thread-local). No C++ exception
+ * crosses the ABI. Buffers are owned by the caller. Strides are in elements, not bytes.
+ *
+ * Element formats: LV_DTYPE_BF16 and LV_DTYPE_F16 for attention; the store kernels copy bytes and take any
+ * element size.
+ */
+#ifndef LVATTN_H_
+#define LVATTN_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LV_OK 0
+#define LV_EINVAL 1 /* bad argument: shape, stride, alignment or size */
+#define LV_EHIP 2   /* a HIP runtime call or kernel launch failed */
+
+#define LV_DTYPE_BF16 0
+#define LV_DTYPE_F16 1
+
+#define LV_ABI_VERSION 1
+
+/* The last error message of the calling thread ("" if none). */
+const char* lv_last_error(void);
+
+/* LV_ABI_VERSION of the built library. */
+int lv_abi_version(void);
+
+/* ---------------------------------------------------------------------------------------------------------
+ * Ragged-batch packing. Replaces the host packing of ModelRunner.prepare_batch
+ * (lean_vllm/engine/model_runner.py:356-446, context dict :448-462) with one kernel.
+ *
+ * Inputs, in scheduler order, one entry per row: num_cached[B], num_new[B] (int32), and the rows' block lists
+ * as CSR: blk_indptr[B+1], blk_ids[blk_indptr[B]] (int32). query_len is the length whose rows lead the batch
+ * (decode_query_len, model_runner.py:51-63). table_width = the longest list; num_tokens = sum(num_new).
+ * Outputs, in batch order (rows of length query_len first, scheduler order kept within each group):
+ *   order[B]            batch row -> scheduler row
+ *   cu_seqlens_q[B+1]   int32 prefix sums of num_new
+ *   cu_seqlens_k[B+1]   int32 prefix sums of num_cached + num_new
+ *   positions[T]        int64, num_cached + offset within the row
+ *   slot_mapping[<=T]   int32, block_list[pos / bs] * bs + pos % bs, only for rows whose list is non-empty
+ *                       (compacted, as model_runner.py:442-445)
+ *   context_lens[B]     int32 num_cached + num_new
+ *   block_tables[B*W]   int32 block lists padded with -1 (may be NULL when table_width == 0)
+ * Limit: num_rows <= LV_PACK_MAX_ROWS. */
+#define LV_PACK_MAX_ROWS 4096
+int lv_pack(const int32_t* num_cached, const int32_t* num_new, const int32_t* blk_indptr, const int32_t* blk_ids,
+            int32_t num_rows, int32_t query_len, int32_t block_size, int32_t table_width, int32_t num_tokens,
+            int32_t* order, int32_t* cu_seqlens_q, int32_t* cu_seqlens_k, int64_t* positions,
+            int32_t* slot_mapping, int32_t* context_lens, int32_t* block_tables, void* stream);
+
+/* ---------------------------------------------------------------------------------------------------------
+ * Scatter new keys/values into the paged cache. Replaces AttentionBackend.store_kvcache
+ * (lean_vllm/attention/abstract.py:107-116; Triton store_kvcache_kernel, lean_vllm/attention/triton_cache.py:9-37,58-81).
+ * key/value: [T, Hkv, D] with unit dim stride and head stride D; row strides key_stride_t / value_stride_t.
+ * Caches: logical (block, token, head, dim) addressed by their strides (an HND cache's transposed view works),
+ * unit dim stride. slot_mapping[T]: slot = block * block_size + offset; -1 skips the token. Bit-exact copy. */
+int lv_store_kvcache(const void* key, const void* value, int64_t key_stride_t, int64_t value_stride_t,
+                     int32_t num_tokens, int32_t num_kv_heads, int32_t head_dim, void* k_cache, void* v_cache,
+                     int64_t cache_stride_block, int64_t cache_stride_token, int64_t cache_stride_head,
+                     int32_t block_size, const int32_t* slot_mapping, int32_t elem_bytes, void* stream);
+
+/* Scatter MLA latents [T, dim] (row stride latent_stride_t, unit dim stride) into a cache whose token rows are
+ * `dim` elements apart (cache.view(-1, dim)[slot] = latent[t]); -1 skips. Replaces
+ * AttentionBackend.store_latents (lean_vllm/attention/abstract.py:178-185; triton_cache.py:39-55,84-91). */
+int lv_store_latents(const void* latent, int64_t latent_stride_t, int32_t num_tokens, int32_t dim, void* cache,
+                     const int32_t* slot_mapping, int32_t elem_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------------------------------
+ * Paged attention over a step: pure decode, chunked prefill, or a mixed batch in one kernel.
+ * Replaces AttentionBackend.decode / prefill / forward for this backend (lean_vllm/attention/abstract.py:118-176;
+ * math of TorchAttention.decode/prefill, lean_vllm/attention/torch_backend.py:62-103).
+ *
+ * q: [T, Hq, D] (strides q_stride_t, q_stride_h; unit dim stride). out: same shape, own strides.
+ * Caches as lv_store_kvcache. block_tables: [B, *] int32 with row stride table_stride.
+ * cu_seqlens_q: [B+1], or NULL for one query per row (decode; T == B).
+ * Key length of row b: seqlens_k[b] if seqlens_k is non-NULL, else cu_seqlens_k[b+1] - cu_seqlens_k[b].
+ * Query j of a row with lq queries and lk keys sees keys 0 .. lk-lq+j (bottom-right causal).
+ * A row with no keys gets a zero output.
+ * max_seqlen_k bounds every row's key length (block-table width * block_size will do); it sizes the split-K grid
+ * so a captured graph needs no length read back. num_tokens_upper bounds T for the work list (use T).
+ * workspace: caller-owned device memory of at least lv_paged_attention_workspace_bytes(...) bytes for the same
+ * arguments; its contents need no initialisation. */
+size_t lv_paged_attention_workspace_bytes(int32_t num_rows, int32_t num_tokens, int32_t num_heads,
+                                          int32_t num_kv_heads, int32_t head_dim, int32_t max_seqlen_k,
+                                          int32_t decode_only);
+int lv_paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_cache,
+                       const void* v_cache, int64_t cache_stride_block, int64_t cache_stride_token,
+                       int64_t cache_stride_head, int32_t block_size, const int32_t* block_tables,
+                       int64_t table_stride, const int32_t* cu_seqlens_q, const int32_t* seqlens_k,
+                       const int32_t* cu_seqlens_k, int32_t num_rows, int32_t num_tokens, int32_t num_heads,
+                       int32_t num_kv_heads, int32_t head_dim, float scale, int32_t max_seqlen_q,
+                       int32_t max_seqlen_k, void* out, int64_t out_stride_t, int64_t out_stride_h,
+                       void* workspace, size_t workspace_bytes, int32_t dtype, void* stream);
+
+/* ---------------------------------------------------------------------------------------------------------
+ * Merge two partial attentions over disjoint key sets by log-sum-exp. Replaces merge_attention_
+ * (lean_vllm/attention/merge.py:18-28; Triton merge_attn_states_kernel, lean_vllm/attention/triton_merge.py:14-82).
+ * o_*: [T, H, D] (unit dim stride, own token/head strides), lse_*: [T, H] fp32 natural log (own strides).
+ * Writes out (may alias o_a) and overwrites lse_a with the merged lse. */
+int lv_merge_attn_states(void* out, int64_t out_stride_t, int64_t out_stride_h, const void* o_a,
+                         int64_t oa_stride_t, int64_t oa_stride_h, float* lse_a, int64_t lsea_stride_t,
+                         int64_t lsea_stride_h, const void* o_b, int64_t ob_stride_t, int64_t ob_stride_h,
+                         const float* lse_b, int64_t lseb_stride_t, int64_t lseb_stride_h, int32_t num_tokens,
+                         int32_t num_heads, int32_t head_dim, int32_t dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LVATTN_H_ */

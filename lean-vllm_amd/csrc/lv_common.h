@@ -1,0 +1,173 @@
+// Shared helpers for the lvattn HIP kernels (gfx950 / CDNA4, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cmath>
+#include <string>
+
+#include "lvattn.h"
+
+namespace lv {
+
+// ---------------------------------------------------------------------------------------------------------
+// Errors: every C entry point returns a status and leaves a message in a thread-local string.
+
+void set_error(const char* fmt, ...);
+const char* last_error();
+
+#define LV_REQUIRE(cond, ...)                 \
+  do {                                        \
+    if (!(cond)) {                            \
+      ::lv::set_error(__VA_ARGS__);           \
+      return LV_EINVAL;                       \
+    }                                         \
+  } while (0)
+
+#define LV_HIP_CHECK(expr)                                                              \
+  do {                                                                                  \
+    hipError_t lv_err_ = (expr);                                                        \
+    if (lv_err_ != hipSuccess) {                                                        \
+      ::lv::set_error("%s failed: %s", #expr, hipGetErrorString(lv_err_));              \
+      return LV_EHIP;                                                                   \
+    }                                                                                   \
+  } while (0)
+
+#define LV_LAUNCH_CHECK(name)                                                           \
+  do {                                                                                  \
+    hipError_t lv_err_ = hipGetLastError();                                             \
+    if (lv_err_ != hipSuccess) {                                                        \
+      ::lv::set_error("launch of %s failed: %s", name, hipGetErrorString(lv_err_));     \
+      return LV_EHIP;                                                                   \
+    }                                                                                   \
+  } while (0)
+
+inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// ---------------------------------------------------------------------------------------------------------
+// Vector types and element conversion.
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+struct BF16 {};  // tag types for the two 16-bit element formats
+struct F16 {};
+
+template <typename T> struct Elem;
+
+template <> struct Elem<BF16> {
+  // Two packed elements -> two floats.
+  __device__ static inline float lo(uint32_t x) { return __uint_as_float(x << 16); }
+  __device__ static inline float hi(uint32_t x) { return __uint_as_float(x & 0xffff0000u); }
+  // acc + a.x*b.x + a.y*b.y, fp32 accumulation.
+  __device__ static inline float dot2(uint32_t a, uint32_t b, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), acc, false);
+  }
+  // Two floats -> packed pair, round to nearest even.
+  __device__ static inline uint32_t pack(float a, float b) {
+    bf16x2 v = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+  __device__ static inline f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+  }
+};
+
+template <> struct Elem<F16> {
+  __device__ static inline float lo(uint32_t x) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(x & 0xffffu));
+  }
+  __device__ static inline float hi(uint32_t x) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(x >> 16)); }
+  __device__ static inline float dot2(uint32_t a, uint32_t b, float acc) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), acc, false);
+  }
+  __device__ static inline uint32_t pack(float a, float b) {
+    f16x2 v = {(_Float16)a, (_Float16)b};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+  __device__ static inline f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+  }
+};
+
+// ---------------------------------------------------------------------------------------------------------
+// Wave-level reductions. DPP within a row of 16 lanes; cross-row through the LDS crossbar (ds_bpermute).
+
+__device__ inline float dpp_xor1(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0xB1, 0xf, 0xf, false));
+}
+__device__ inline float dpp_xor2(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x4E, 0xf, 0xf, false));
+}
+__device__ inline float dpp_half_mirror(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x141, 0xf, 0xf, false));
+}
+__device__ inline float dpp_mirror(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x140, 0xf, 0xf, false));
+}
+
+// Sum over aligned groups of N lanes (N = 4, 8 or 16); every lane of a group ends with the group's sum.
+template <int N>
+__device__ inline float group_sum(float x) {
+  static_assert(N == 4 || N == 8 || N == 16, "group of 4, 8 or 16 lanes");
+  x += dpp_xor1(x);
+  x += dpp_xor2(x);
+  if constexpr (N >= 8) x += dpp_half_mirror(x);
+  if constexpr (N >= 16) x += dpp_mirror(x);
+  return x;
+}
+
+__device__ inline float shfl_xor(float x, int mask) { return __shfl_xor(x, mask, 64); }
+
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ inline float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+// Exclusive prefix sum of a[0, n) in LDS, in place, by a block of kScanThreads threads; a[n] receives the total.
+// wave_tot holds kScanThreads / 64 + 1 ints of LDS. Every thread of the block must call it.
+constexpr int kScanThreads = 1024;
+__device__ inline void block_scan(int* a, int n, int* wave_tot) {
+  const int tid = threadIdx.x;
+  const int per = (n + kScanThreads - 1) / kScanThreads;
+  const int lo = min(tid * per, n), hi = min(lo + per, n);
+  int local = 0;
+  for (int i = lo; i < hi; ++i) local += a[i];
+  const int lane = tid & 63, wave = tid >> 6;
+  int x = local;  // inclusive scan of the chunk totals across the wave
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(x, d, 64);
+    if (lane >= d) x += y;
+  }
+  if (lane == 63) wave_tot[wave] = x;
+  __syncthreads();
+  if (tid == 0) {
+    int run = 0;
+    for (int w = 0; w < kScanThreads / 64; ++w) {
+      const int v = wave_tot[w];
+      wave_tot[w] = run;
+      run += v;
+    }
+    wave_tot[kScanThreads / 64] = run;
+  }
+  __syncthreads();
+  int run = wave_tot[wave] + x - local;  // exclusive prefix of this thread's chunk
+  for (int i = lo; i < hi; ++i) {
+    const int v = a[i];
+    a[i] = run;
+    run += v;
+  }
+  if (tid == 0) a[n] = wave_tot[kScanThreads / 64];
+  __syncthreads();
+}
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+}  // namespace lv

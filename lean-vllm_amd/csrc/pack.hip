@@ -1,0 +1,126 @@
+// Ragged-batch packing on the GPU: per-row (num_cached, num_new, block list) -> the step's attention metadata.
+//
+// One kernel. Every workgroup first rebuilds the row-level prefix sums in LDS (the rows are few: a few thousand
+// ints), then fills its share of the per-token outputs (positions, slot_mapping) and of the padded block table.
+// Workgroup 0 also writes the row-level outputs. No grid-wide synchronisation, no atomics, no host read back.
+// The integer arithmetic mirrors ModelRunner.prepare_batch (lean_vllm/engine/model_runner.py:367-446).
+#include "lv_common.h"
+
+namespace lv {
+
+constexpr int kPackThreads = kScanThreads;
+constexpr int kPackMaxRows = 4096;  // LDS holds three (rows + 1)-int arrays
+
+__global__ __launch_bounds__(kPackThreads) void pack_kernel(
+    const int32_t* __restrict__ num_cached, const int32_t* __restrict__ num_new, const int32_t* __restrict__ indptr,
+    const int32_t* __restrict__ blk_ids, int32_t rows, int32_t query_len, int32_t bs, int32_t width, int32_t tokens,
+    int32_t* __restrict__ order, int32_t* __restrict__ cu_q_out, int32_t* __restrict__ cu_k_out,
+    int64_t* __restrict__ positions, int32_t* __restrict__ slots, int32_t* __restrict__ context_lens,
+    int32_t* __restrict__ tables) {
+  __shared__ int src[kPackMaxRows];       // batch row -> scheduler row
+  __shared__ int cu_q[kPackMaxRows + 1];  // token offsets, batch order
+  __shared__ int cu_s[kPackMaxRows + 1];  // slot_mapping offsets (rows with a block list only), batch order
+  __shared__ int wave_tot[kPackThreads / 64 + 1];
+  const int tid = threadIdx.x;
+
+  // 1. Stable partition: rows of query_len first, scheduler order kept in each group (model_runner.py:367-374).
+  for (int i = tid; i < rows; i += kPackThreads) cu_q[i] = num_new[i] == query_len ? 1 : 0;
+  __syncthreads();
+  block_scan(cu_q, rows, wave_tot);
+  const int leading = cu_q[rows];
+  for (int i = tid; i < rows; i += kPackThreads) {
+    const int before = cu_q[i];  // leading rows before i
+    const bool lead = num_new[i] == query_len;
+    src[lead ? before : leading + (i - before)] = i;
+  }
+  __syncthreads();
+
+  // 2. Row prefix sums in batch order (model_runner.py:393-397).
+  for (int r = tid; r < rows; r += kPackThreads) {
+    const int s = src[r];
+    cu_q[r] = num_new[s];
+    cu_s[r] = indptr[s + 1] > indptr[s] ? num_new[s] : 0;
+  }
+  __syncthreads();
+  block_scan(cu_q, rows, wave_tot);
+  block_scan(cu_s, rows, wave_tot);
+
+  // 3. Row-level outputs, from one workgroup (cu_seqlens_k last, once cu_q is free to reuse).
+  if (blockIdx.x == 0) {
+    for (int r = tid; r < rows; r += kPackThreads) {
+      const int s = src[r];
+      order[r] = s;
+      cu_q_out[r] = cu_q[r];
+      context_lens[r] = num_cached[s] + num_new[s];
+    }
+    if (tid == 0) cu_q_out[rows] = cu_q[rows];
+  }
+
+  // 4. Per-token outputs (model_runner.py:398-400, :440-445).
+  const int stride = gridDim.x * kPackThreads;
+  for (int t = blockIdx.x * kPackThreads + tid; t < tokens; t += stride) {
+    int lo = 0, hi = rows - 1;  // last row whose start <= t
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (cu_q[mid] <= t) lo = mid; else hi = mid - 1;
+    }
+    const int r = lo, s = src[r];
+    const int offset = t - cu_q[r];
+    const int64_t pos = (int64_t)num_cached[s] + offset;
+    positions[t] = pos;
+    const int list = indptr[s], len = indptr[s + 1] - list;
+    if (len > 0) {
+      const int64_t block = blk_ids[list + (int)(pos / bs)];
+      slots[cu_s[r] + offset] = (int32_t)(block * bs + pos % bs);
+    }
+  }
+
+  // 5. Padded block tables (model_runner.py:437-439).
+  const int64_t cells = (int64_t)rows * width;
+  for (int64_t e = (int64_t)blockIdx.x * kPackThreads + tid; e < cells; e += stride) {
+    const int r = (int)(e / width), j = (int)(e - (int64_t)r * width);
+    const int s = src[r];
+    const int list = indptr[s], len = indptr[s + 1] - list;
+    tables[e] = j < len ? blk_ids[list + j] : -1;
+  }
+
+  // 6. cu_seqlens_k (model_runner.py:395-397), in workgroup 0, reusing cu_q's LDS now that its tokens are done.
+  if (blockIdx.x == 0) {
+    __syncthreads();
+    for (int r = tid; r < rows; r += kPackThreads) {
+      const int s = src[r];
+      cu_q[r] = num_cached[s] + num_new[s];
+    }
+    __syncthreads();
+    block_scan(cu_q, rows, wave_tot);
+    for (int r = tid; r <= rows; r += kPackThreads) cu_k_out[r] = cu_q[r];
+  }
+}
+
+}  // namespace lv
+
+using namespace lv;
+
+extern "C" int lv_pack(const int32_t* num_cached, const int32_t* num_new, const int32_t* blk_indptr,
+                       const int32_t* blk_ids, int32_t num_rows, int32_t query_len, int32_t block_size,
+                       int32_t table_width, int32_t num_tokens, int32_t* order, int32_t* cu_seqlens_q,
+                       int32_t* cu_seqlens_k, int64_t* positions, int32_t* slot_mapping, int32_t* context_lens,
+                       int32_t* block_tables, void* stream) {
+  LV_REQUIRE(num_rows > 0 && num_rows <= kPackMaxRows, "pack: %d rows; 1 to %d are supported", num_rows,
+             kPackMaxRows);
+  LV_REQUIRE(block_size > 0, "pack: block_size must be positive, got %d", block_size);
+  LV_REQUIRE(table_width >= 0 && num_tokens >= 0, "pack: negative table width or token count");
+  LV_REQUIRE(num_cached && num_new && blk_indptr && order && cu_seqlens_q && cu_seqlens_k && context_lens,
+             "pack: null row pointer");
+  LV_REQUIRE(num_tokens == 0 || positions, "pack: null positions");
+  LV_REQUIRE(table_width == 0 || (block_tables && blk_ids && slot_mapping), "pack: null table pointer");
+  const int64_t work = (int64_t)num_tokens + (int64_t)num_rows * table_width;
+  int grid = (int)((work + kPackThreads * 4 - 1) / (kPackThreads * 4));
+  grid = grid < 1 ? 1 : (grid > 64 ? 64 : grid);
+  hipLaunchKernelGGL(pack_kernel, dim3(grid), dim3(kPackThreads), 0, reinterpret_cast<hipStream_t>(stream),
+                     num_cached, num_new, blk_indptr, blk_ids, num_rows, query_len, block_size, table_width,
+                     num_tokens, order, cu_seqlens_q, cu_seqlens_k, positions, slot_mapping, context_lens,
+                     block_tables);
+  LV_LAUNCH_CHECK("pack_kernel");
+  return LV_OK;
+}

@@ -1,0 +1,642 @@
+// Paged attention for a continuous-batching step on gfx950: pure decode, chunked prefill, or both in one launch.
+//
+// Work items (one workgroup of 4 waves each):
+//   decode item  = (row, split, kv head, query-head group): a row with one query, keys [split*S, (split+1)*S).
+//                  Streaming, bandwidth-bound: each wave takes every 4th 16-token tile of the range; a token's
+//                  head row (D elements) is spread over 16 lanes as 16-byte loads; q.k by v_dot2 with a DPP
+//                  butterfly inside the 16-lane row; online softmax per tile; p.v on the VALU in fp32. The four
+//                  waves and, for long rows, the splits are merged by log-sum-exp.
+//   prefill item = (row, q tile, kv head): a row with several queries. 64 (position, head) query rows of one GQA
+//                  group against 64-key tiles staged in LDS: S^T = K Q^T and O^T += V^T P^T on MFMA 16x16x32,
+//                  bottom-right causal mask, online softmax per query row.
+// A pure-decode launch maps blockIdx.x to (row, split) directly; a mixed launch reads a work list built on the
+// device by plan_kernel from cu_seqlens_q and the key lengths (prefill items first). Rows whose keys were split
+// are combined by splitk_merge_kernel.
+//
+// Math: TorchAttention.decode / prefill (lean_vllm/attention/torch_backend.py:62-103,159-181): query head h reads
+// key head h / (Hq/Hkv); query j of a row with lq queries and lk keys sees keys 0..lk-lq+j.
+#include "lv_common.h"
+
+namespace lv {
+
+constexpr int kTile = 16;          // decode tokens per tile; block sizes are multiples of 16, so a tile sits in one block
+constexpr int kWaves = 4;          // waves per workgroup
+constexpr int kPrefillKeys = 64;   // keys per prefill tile
+constexpr int kPrefillRows = 64;   // (position, head) query rows per prefill item, 16 per wave
+constexpr int kPlanMaxRows = 4096;  // rows of a step with prompts (the work-list scan lives in LDS)
+
+struct AttnParams {
+  const char* q;
+  int64_t q_st, q_sh;  // bytes
+  const char* k_cache;
+  const char* v_cache;
+  int64_t c_sb, c_st, c_sh;  // bytes
+  int32_t bs;
+  const int32_t* tables;
+  int64_t t_stride;  // elements
+  const int32_t* cu_q;
+  const int32_t* lens_k;
+  const int32_t* cu_k;
+  int32_t rows, hq, hkv, group, qgroups;
+  float scale_log2;  // softmax scale * log2(e): scores live in the exp2 domain
+  char* out;
+  int64_t o_st, o_sh;  // bytes
+  int32_t split;       // S: keys per decode item
+  int32_t max_splits;
+  float* part_o;    // [rows][hq][max_splits][D] normalised partial outputs
+  float* part_lse;  // [rows][hq][max_splits] log2-sum-exp2 of the partials
+  const int2* items;
+  const int32_t* n_items;
+};
+
+__device__ inline int key_len(const AttnParams& p, int row) {
+  return p.lens_k ? p.lens_k[row] : p.cu_k[row + 1] - p.cu_k[row];
+}
+
+__device__ inline u32x4 ld16(const char* ptr) { return *reinterpret_cast<const u32x4*>(ptr); }
+__device__ inline void st16(char* ptr, u32x4 v) { *reinterpret_cast<u32x4*>(ptr) = v; }
+
+// ---------------------------------------------------------------------------------------------------------
+// Decode item.
+
+template <typename T, int D, int GS>
+__device__ void decode_item(const AttnParams& p, int row, int split, int kvh, int qg, char* smem) {
+  using E = Elem<T>;
+  constexpr int LPT = D >= 128 ? 16 : D / 8;  // lanes per token head row
+  constexpr int VPL = D / (LPT * 8);          // 16-byte vectors per lane per row
+  constexpr int EPL = VPL * 8;                // elements per lane
+  constexpr int TPI = 64 / LPT;               // tokens per wave step
+  constexpr int U = kTile / TPI;              // steps per tile
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int grp = lane / LPT, part = lane % LPT;
+
+  const int lk = key_len(p, row);
+  const int kbeg = split * p.split;
+  // Past the row's end (the grid is sized for the longest row), or past the bound the caller gave.
+  if ((split > 0 && kbeg >= lk) || split >= p.max_splits) return;
+  const int kend = min(lk, kbeg + p.split);
+  const int nsplit = min((lk + p.split - 1) / p.split, p.max_splits);
+  const int tok = p.cu_q ? p.cu_q[row] : row;
+  const int head0 = kvh * p.group + qg * GS;
+
+  u32x4 qv[GS][VPL];
+#pragma unroll
+  for (int g = 0; g < GS; ++g)
+#pragma unroll
+    for (int v = 0; v < VPL; ++v)
+      qv[g][v] = ld16(p.q + tok * p.q_st + (head0 + g) * p.q_sh + (int64_t)(v * LPT + part) * 16);
+
+  float m[GS], l[GS], acc[GS][EPL];
+#pragma unroll
+  for (int g = 0; g < GS; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[g][e] = 0.f;
+  }
+
+  const int32_t* table = p.tables + (int64_t)row * p.t_stride;
+  for (int t0 = kbeg + kTile * wave; t0 < kend; t0 += kTile * kWaves) {
+    const int64_t blk = table[t0 / p.bs];
+    const int64_t base = blk * p.c_sb + (int64_t)(t0 % p.bs) * p.c_st + (int64_t)kvh * p.c_sh;
+    u32x4 kv[U][VPL], vv[U][VPL];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) {
+        const int64_t off = base + (int64_t)(u * TPI + grp) * p.c_st + (int64_t)(v * LPT + part) * 16;
+        kv[u][v] = ld16(p.k_cache + off);
+        vv[u][v] = ld16(p.v_cache + off);
+      }
+    float s[U][GS];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int g = 0; g < GS; ++g) {
+        float d = 0.f;
+#pragma unroll
+        for (int v = 0; v < VPL; ++v)
+#pragma unroll
+          for (int w = 0; w < 4; ++w) d = E::dot2(qv[g][v][w], kv[u][v][w], d);
+        s[u][g] = group_sum<LPT>(d) * p.scale_log2;
+      }
+    // Tokens past the range: no weight, and their (possibly NaN) values must not reach the sums.
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (t0 + u * TPI + grp >= kend) {
+#pragma unroll
+        for (int g = 0; g < GS; ++g) s[u][g] = -INFINITY;
+#pragma unroll
+        for (int v = 0; v < VPL; ++v) vv[u][v] = u32x4{0, 0, 0, 0};
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < GS; ++g) {
+      float mx = s[0][g];
+#pragma unroll
+      for (int u = 1; u < U; ++u) mx = fmaxf(mx, s[u][g]);
+#pragma unroll
+      for (int d = LPT; d < 64; d <<= 1) mx = fmaxf(mx, shfl_xor(mx, d));
+      const float mnew = fmaxf(m[g], mx);  // finite: every tile holds at least one token in range
+      const float alpha = fast_exp2(m[g] - mnew);
+      m[g] = mnew;
+      float pu[U];
+      float psum = 0.f;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        pu[u] = fast_exp2(s[u][g] - mnew);
+        psum += pu[u];
+      }
+      l[g] = l[g] * alpha + psum;
+#pragma unroll
+      for (int v = 0; v < VPL; ++v)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          float lo = acc[g][v * 8 + 2 * w] * alpha, hi = acc[g][v * 8 + 2 * w + 1] * alpha;
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            lo = fmaf(pu[u], E::lo(vv[u][v][w]), lo);
+            hi = fmaf(pu[u], E::hi(vv[u][v][w]), hi);
+          }
+          acc[g][v * 8 + 2 * w] = lo;
+          acc[g][v * 8 + 2 * w + 1] = hi;
+        }
+    }
+  }
+
+  // Sum the token groups of the wave (they share m).
+#pragma unroll
+  for (int g = 0; g < GS; ++g) {
+#pragma unroll
+    for (int d = LPT; d < 64; d <<= 1) {
+      l[g] += shfl_xor(l[g], d);
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) acc[g][e] += shfl_xor(acc[g][e], d);
+    }
+  }
+
+  // Merge the waves through LDS: wm/wl [kWaves][GS], wacc [kWaves][GS][D].
+  float* wm = reinterpret_cast<float*>(smem);
+  float* wl = wm + kWaves * GS;
+  float* wacc = wl + kWaves * GS;
+  if (lane < LPT) {
+#pragma unroll
+    for (int g = 0; g < GS; ++g) {
+#pragma unroll
+      for (int v = 0; v < VPL; ++v)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) wacc[(wave * GS + g) * D + (v * LPT + part) * 8 + e] = acc[g][v * 8 + e];
+      if (lane == 0) {
+        wm[wave * GS + g] = m[g];
+        wl[wave * GS + g] = l[g];
+      }
+    }
+  }
+  __syncthreads();
+  // One thread per 8 output elements.
+  for (int c = threadIdx.x; c < GS * D / 8; c += blockDim.x) {
+    const int g = c / (D / 8), d0 = (c % (D / 8)) * 8;
+    float mmax = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) mmax = fmaxf(mmax, wm[w * GS + g]);
+    float o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    float den = 0.f;
+    if (mmax != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const float wt = fast_exp2(wm[w * GS + g] - mmax);
+        den += wt * wl[w * GS + g];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] += wt * wacc[(w * GS + g) * D + d0 + e];
+      }
+      const float inv = 1.f / den;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] *= inv;
+    }
+    const int head = head0 + g;
+    if (nsplit <= 1) {
+      u32x4 packed;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) packed[w] = E::pack(o[2 * w], o[2 * w + 1]);
+      st16(p.out + tok * p.o_st + head * p.o_sh + (int64_t)d0 * 2, packed);
+    } else {
+      const int64_t slot = ((int64_t)row * p.hq + head) * p.max_splits + split;
+      float* dst = p.part_o + slot * D + d0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dst[e] = o[e];
+      if (d0 == 0) p.part_lse[slot] = mmax == -INFINITY ? -INFINITY : mmax + fast_log2(den);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// Prefill item (MFMA).
+
+// LDS swizzle of the transposed value tile: key k of dim row d sits at k ^ (4 * vt_swz(d)). Conflict-free for
+// both the transposing 16-bit writes (fixed d % 8, varying d / 8) and the 8-byte MFMA operand reads
+// (fixed d % 2 and d / 16, varying d / 2 % 8).
+__device__ inline int vt_swz(int d) {
+  return ((d >> 4) & 1) | ((((d >> 1) ^ (d >> 5)) & 1) << 1) | ((((d >> 2) ^ (d >> 6)) & 1) << 2) |
+         (((d >> 3) & 1) << 3);
+}
+
+template <int D>
+struct PrefillSmem {
+  static constexpr int kRow = D + 8;  // key tile row, elements (pad: conflict-free operand reads)
+  static constexpr int kBytes = kPrefillKeys * kRow * 2 + D * kPrefillKeys * 2;
+};
+
+template <typename T, int D>
+__device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, char* smem) {
+  using E = Elem<T>;
+  constexpr int KS = D / 32;  // MFMA k-steps over the head dim
+  constexpr int DB = D / 16;  // 16-dim blocks of the output
+  constexpr int ROW = PrefillSmem<D>::kRow;
+  uint16_t* ks_lds = reinterpret_cast<uint16_t*>(smem);          // [64 keys][ROW]
+  uint16_t* vt_lds = ks_lds + kPrefillKeys * ROW;                // [D][64 keys], swizzled
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = lane & 15, j4 = lane >> 4;
+  const int G = p.group;
+  const int qp = kPrefillRows / G;  // positions per item
+  const int q0 = p.cu_q[row], lq = p.cu_q[row + 1] - q0;
+  const int lk = key_len(p, row);
+  const int p0 = qtile * qp;
+
+  const int mrow = wave * 16 + n;
+  const int qi = p0 + mrow / G;
+  const int head = kvh * G + mrow % G;
+  const bool qvalid = mrow < qp * G && qi < lq;
+  u32x4 qb[KS];
+#pragma unroll
+  for (int k = 0; k < KS; ++k)
+    qb[k] = qvalid ? ld16(p.q + (int64_t)(q0 + qi) * p.q_st + head * p.q_sh + (int64_t)(32 * k + 8 * j4) * 2)
+                   : u32x4{0, 0, 0, 0};
+  const int lim = qvalid ? lk - lq + qi + 1 : lk;  // this query row sees keys < lim
+  const int kmax = min(lk, lk - lq + min(p0 + qp, lq));
+
+  float mrun = -INFINITY, lrun = 0.f;
+  f32x4 o[DB];
+#pragma unroll
+  for (int b = 0; b < DB; ++b) o[b] = f32x4{0, 0, 0, 0};
+
+  const int32_t* table = p.tables + (int64_t)row * p.t_stride;
+  constexpr int CPK = D / 8;  // 16-byte chunks per key head row
+  for (int kt = 0; kt < kmax; kt += kPrefillKeys) {
+    __syncthreads();  // the previous tile's operand reads are done
+    for (int c = tid; c < kPrefillKeys * CPK; c += blockDim.x) {
+      const int key = c / CPK, part = c % CPK;
+      const int jk = kt + key;
+      u32x4 kk = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
+      if (jk < lk) {
+        const int64_t blk = table[jk / p.bs];
+        const int64_t off = blk * p.c_sb + (int64_t)(jk % p.bs) * p.c_st + (int64_t)kvh * p.c_sh + part * 16;
+        kk = ld16(p.k_cache + off);
+        vv = ld16(p.v_cache + off);
+      }
+      st16(reinterpret_cast<char*>(ks_lds + key * ROW + part * 8), kk);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int d = part * 8 + e;
+        const uint16_t x = (uint16_t)(vv[e >> 1] >> ((e & 1) * 16));
+        vt_lds[d * kPrefillKeys + (key ^ (4 * vt_swz(d)))] = x;
+      }
+    }
+    __syncthreads();
+
+    // S^T (keys x query rows): lane holds keys kt + 16*kb + 4*j4 + r of query row n.
+    f32x4 st[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      st[kb] = f32x4{0, 0, 0, 0};
+#pragma unroll
+      for (int k = 0; k < KS; ++k) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(ks_lds + (kb * 16 + n) * ROW + 32 * k + 8 * j4);
+        st[kb] = E::mfma16x16x32(a, qb[k], st[kb]);
+      }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = kt + kb * 16 + 4 * j4 + r;
+        const float s = key < lim ? st[kb][r] * p.scale_log2 : -INFINITY;
+        st[kb][r] = s;
+        mx = fmaxf(mx, s);
+      }
+    mx = fmaxf(mx, shfl_xor(mx, 16));
+    mx = fmaxf(mx, shfl_xor(mx, 32));
+    const float mnew = fmaxf(mrun, mx);
+    const float mref = mnew == -INFINITY ? 0.f : mnew;
+    const float alpha = fast_exp2(mrun - mref);
+    mrun = mnew;
+    float psum = 0.f;
+    u32x4 pb[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float pr[8];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        pr[r] = fast_exp2(st[2 * h][r] - mref);
+        pr[4 + r] = fast_exp2(st[2 * h + 1][r] - mref);
+      }
+#pragma unroll
+      for (int r = 0; r < 8; ++r) psum += pr[r];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) pb[h][w] = E::pack(pr[2 * w], pr[2 * w + 1]);
+    }
+    lrun = lrun * alpha + psum;
+#pragma unroll
+    for (int b = 0; b < DB; ++b) {
+      o[b] *= alpha;
+      const int d = b * 16 + n;
+      const uint16_t* vrow = vt_lds + d * kPrefillKeys;
+      const int sw = 4 * vt_swz(d);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow + ((32 * h + 4 * j4) ^ sw));
+        const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + ((32 * h + 16 + 4 * j4) ^ sw));
+        const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
+        o[b] = E::mfma16x16x32(a, pb[h], o[b]);
+      }
+    }
+  }
+
+  lrun += shfl_xor(lrun, 16);
+  lrun += shfl_xor(lrun, 32);
+  if (qvalid) {
+    const float inv = lrun > 0.f ? 1.f / lrun : 0.f;
+    char* dst = p.out + (int64_t)(q0 + qi) * p.o_st + head * p.o_sh;
+#pragma unroll
+    for (int b = 0; b < DB; ++b) {
+      u32x2 packed = {E::pack(o[b][0] * inv, o[b][1] * inv), E::pack(o[b][2] * inv, o[b][3] * inv)};
+      *reinterpret_cast<u32x2*>(dst + (int64_t)(b * 16 + 4 * j4) * 2) = packed;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// Kernels.
+
+template <int D, int GS>
+struct SmemBytes {
+  static constexpr int kDecode = kWaves * GS * (D + 2) * 4;
+  static constexpr int kPrefill = PrefillSmem<D>::kBytes;
+  static constexpr int kMixed = kDecode > kPrefill ? kDecode : kPrefill;
+};
+
+template <typename T, int D, int GS, bool MIXED>
+__global__ __launch_bounds__(256) void paged_attention_kernel(AttnParams p) {
+  constexpr int kSmem = MIXED ? SmemBytes<D, GS>::kMixed : SmemBytes<D, GS>::kDecode;
+  __shared__ __attribute__((aligned(16))) char smem[kSmem];
+  const int kvh = blockIdx.y / p.qgroups, qg = blockIdx.y % p.qgroups;
+  if constexpr (MIXED) {
+    if ((int)blockIdx.x >= *p.n_items) return;
+    const int2 it = p.items[blockIdx.x];
+    if (it.y >= 0)
+      decode_item<T, D, GS>(p, it.x, it.y, kvh, qg, smem);
+    else if (qg == 0)
+      prefill_item<T, D>(p, it.x, -1 - it.y, kvh, smem);
+  } else {
+    decode_item<T, D, GS>(p, blockIdx.x / p.max_splits, blockIdx.x % p.max_splits, kvh, qg, smem);
+  }
+}
+
+// Work list of a mixed step: prefill items (row, -1 - tile) first, then decode items (row, split).
+__global__ __launch_bounds__(kScanThreads) void plan_kernel(const int32_t* __restrict__ cu_q,
+                                                            const int32_t* __restrict__ lens_k,
+                                                            const int32_t* __restrict__ cu_k, int32_t rows,
+                                                            int32_t split, int32_t qp, int32_t max_items,
+                                                            int2* __restrict__ items, int32_t* __restrict__ n_items) {
+  __shared__ int pre[kPlanMaxRows + 1];
+  __shared__ int dec[kPlanMaxRows + 1];
+  __shared__ int wave_tot[kScanThreads / 64 + 1];
+  const int tid = threadIdx.x;
+  for (int r = tid; r < rows; r += kScanThreads) {
+    const int lq = cu_q[r + 1] - cu_q[r];
+    const int lk = lens_k ? lens_k[r] : cu_k[r + 1] - cu_k[r];
+    const int nd = lk > 0 ? (lk + split - 1) / split : 1;
+    pre[r] = lq > 1 ? (lq + qp - 1) / qp : 0;
+    dec[r] = lq == 1 ? nd : 0;
+  }
+  __syncthreads();
+  block_scan(pre, rows, wave_tot);
+  block_scan(dec, rows, wave_tot);
+  const int npre = pre[rows];
+  for (int r = tid; r < rows; r += kScanThreads) {
+    for (int i = pre[r]; i < pre[r + 1]; ++i)
+      if (i < max_items) items[i] = make_int2(r, -1 - (i - pre[r]));
+    for (int i = dec[r]; i < dec[r + 1]; ++i)
+      if (npre + i < max_items) items[npre + i] = make_int2(r, i - dec[r]);
+  }
+  if (tid == 0) *n_items = min(npre + dec[rows], max_items);
+}
+
+// Combine a split row's partial outputs: o = sum_s 2^(lse_s - M) o_s / sum_s 2^(lse_s - M).
+template <typename T, int D>
+__global__ __launch_bounds__(64) void splitk_merge_kernel(AttnParams p) {
+  using E = Elem<T>;
+  const int row = blockIdx.x, head = blockIdx.y, lane = threadIdx.x;
+  if (p.cu_q && p.cu_q[row + 1] - p.cu_q[row] != 1) return;  // a prefill row: written by its items
+  const int lk = key_len(p, row);
+  const int nsplit = min((lk + p.split - 1) / p.split, p.max_splits);
+  if (nsplit <= 1) return;
+  const int tok = p.cu_q ? p.cu_q[row] : row;
+  const int64_t slot0 = ((int64_t)row * p.hq + head) * p.max_splits;
+  float mmax = -INFINITY;
+  for (int s = 0; s < nsplit; ++s) mmax = fmaxf(mmax, p.part_lse[slot0 + s]);
+  constexpr int PER = D / 64 > 0 ? D / 64 : 1;
+  float o[PER];
+#pragma unroll
+  for (int e = 0; e < PER; ++e) o[e] = 0.f;
+  float den = 0.f;
+  for (int s = 0; s < nsplit; ++s) {
+    const float w = fast_exp2(p.part_lse[slot0 + s] - mmax);
+    den += w;
+    const float* src = p.part_o + (slot0 + s) * D;
+#pragma unroll
+    for (int e = 0; e < PER; ++e)
+      if (lane * PER + e < D) o[e] = fmaf(w, src[lane * PER + e], o[e]);
+  }
+  const float inv = 1.f / den;
+  char* dst = p.out + tok * p.o_st + head * p.o_sh;
+#pragma unroll
+  for (int e = 0; e < PER; ++e) {
+    const int d = lane * PER + e;
+    if (d < D) {
+      const uint32_t packed = E::pack(o[e] * inv, 0.f);
+      *reinterpret_cast<uint16_t*>(dst + d * 2) = (uint16_t)(packed & 0xffffu);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// Host side.
+
+struct Shape {
+  int32_t split, max_splits, max_items, gs;
+  size_t items_off, count_off, lse_off, o_off, bytes;
+};
+
+static int pick_gs(int group) {
+  if (group % 4 == 0) return 4;
+  if (group % 2 == 0) return 2;
+  return 1;
+}
+
+static Shape plan_shape(int32_t rows, int32_t tokens, int32_t hq, int32_t hkv, int32_t d, int32_t max_k,
+                        bool decode_only) {
+  Shape s{};
+  const int group = hq / hkv;
+  s.gs = pick_gs(group);
+  const int64_t units = (int64_t)rows * hkv * (group / s.gs);
+  const int64_t keys = max_k > 0 ? max_k : 1;
+  // Keys per decode item: enough items to fill the chip several times over, at least 256 keys each.
+  const int64_t target = 8192;
+  int64_t split = 256;
+  while (split < keys && units * ((keys + split - 1) / split) > target) split *= 2;
+  s.split = (int32_t)split;
+  s.max_splits = (int32_t)((keys + split - 1) / split);
+  const int qp = kPrefillRows / (group > 0 ? group : 1);
+  s.max_items = decode_only ? 0 : rows * s.max_splits + (tokens + qp - 1) / qp + rows;
+  size_t off = 0;
+  s.items_off = off;
+  off += (size_t)s.max_items * sizeof(int2);
+  off = (off + 255) / 256 * 256;
+  s.count_off = off;
+  off += 256;
+  const size_t parts = s.max_splits > 1 ? (size_t)rows * hq * s.max_splits : 0;
+  s.lse_off = off;
+  off += parts * sizeof(float);
+  off = (off + 255) / 256 * 256;
+  s.o_off = off;
+  off += parts * d * sizeof(float);
+  s.bytes = off;
+  return s;
+}
+
+template <typename T, int D, int GS>
+static void launch(const AttnParams& p, bool mixed, int grid_x, hipStream_t stream) {
+  const dim3 grid(grid_x, p.hkv * p.qgroups);
+  if (mixed)
+    hipLaunchKernelGGL((paged_attention_kernel<T, D, GS, true>), grid, dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL((paged_attention_kernel<T, D, GS, false>), grid, dim3(256), 0, stream, p);
+  if (p.max_splits > 1)
+    hipLaunchKernelGGL((splitk_merge_kernel<T, D>), dim3(p.rows, p.hq), dim3(64), 0, stream, p);
+}
+
+template <typename T, int D>
+static void launch_gs(const AttnParams& p, int gs, bool mixed, int grid_x, hipStream_t stream) {
+  if (gs == 4) launch<T, D, 4>(p, mixed, grid_x, stream);
+  else if (gs == 2) launch<T, D, 2>(p, mixed, grid_x, stream);
+  else launch<T, D, 1>(p, mixed, grid_x, stream);
+}
+
+template <typename T>
+static int launch_d(const AttnParams& p, int d, int gs, bool mixed, int grid_x, hipStream_t stream) {
+  switch (d) {
+    case 64: launch_gs<T, 64>(p, gs, mixed, grid_x, stream); return LV_OK;
+    case 128: launch_gs<T, 128>(p, gs, mixed, grid_x, stream); return LV_OK;
+    default: set_error("paged_attention: head_dim %d is not 64 or 128", d); return LV_EINVAL;
+  }
+}
+
+}  // namespace lv
+
+using namespace lv;
+
+extern "C" size_t lv_paged_attention_workspace_bytes(int32_t num_rows, int32_t num_tokens, int32_t num_heads,
+                                                     int32_t num_kv_heads, int32_t head_dim, int32_t max_seqlen_k,
+                                                     int32_t decode_only) {
+  if (num_rows <= 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads) return 0;
+  return plan_shape(num_rows, num_tokens, num_heads, num_kv_heads, head_dim, max_seqlen_k, decode_only != 0).bytes;
+}
+
+extern "C" int lv_paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_cache,
+                                  const void* v_cache, int64_t cache_stride_block, int64_t cache_stride_token,
+                                  int64_t cache_stride_head, int32_t block_size, const int32_t* block_tables,
+                                  int64_t table_stride, const int32_t* cu_seqlens_q, const int32_t* seqlens_k,
+                                  const int32_t* cu_seqlens_k, int32_t num_rows, int32_t num_tokens,
+                                  int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float scale,
+                                  int32_t max_seqlen_q, int32_t max_seqlen_k, void* out, int64_t out_stride_t,
+                                  int64_t out_stride_h, void* workspace, size_t workspace_bytes, int32_t dtype,
+                                  void* stream) {
+  LV_REQUIRE(dtype == LV_DTYPE_BF16 || dtype == LV_DTYPE_F16, "paged_attention: dtype %d is not bf16 or fp16",
+             dtype);
+  LV_REQUIRE(num_rows >= 0 && num_tokens >= 0, "paged_attention: negative row or token count");
+  if (num_rows == 0 || num_tokens == 0) return LV_OK;
+  LV_REQUIRE(num_heads > 0 && num_kv_heads > 0 && num_heads % num_kv_heads == 0,
+             "paged_attention: %d query heads do not group over %d key heads", num_heads, num_kv_heads);
+  LV_REQUIRE(num_heads / num_kv_heads <= kPrefillRows, "paged_attention: query group %d exceeds %d",
+             num_heads / num_kv_heads, kPrefillRows);
+  LV_REQUIRE(head_dim == 64 || head_dim == 128, "paged_attention: head_dim %d is not 64 or 128", head_dim);
+  LV_REQUIRE(block_size > 0 && block_size % kTile == 0, "paged_attention: block_size %d is not a multiple of %d",
+             block_size, kTile);
+  LV_REQUIRE(q && k_cache && v_cache && out && block_tables, "paged_attention: null tensor pointer");
+  LV_REQUIRE(seqlens_k || cu_seqlens_k, "paged_attention: neither key lengths nor cu_seqlens_k given");
+  LV_REQUIRE(cu_seqlens_q || num_tokens == num_rows, "paged_attention: without cu_seqlens_q, T (%d) must equal B (%d)",
+             num_tokens, num_rows);
+  LV_REQUIRE(max_seqlen_k >= 0, "paged_attention: negative max_seqlen_k");
+  // 16-byte rows: q, out and cache head rows are read and written as 16-byte vectors.
+  LV_REQUIRE(aligned(q, 16) && aligned(out, 16) && aligned(k_cache, 16) && aligned(v_cache, 16) &&
+                 (q_stride_t * 2) % 16 == 0 && (q_stride_h * 2) % 16 == 0 && (out_stride_t * 2) % 16 == 0 &&
+                 (out_stride_h * 2) % 16 == 0 && (cache_stride_block * 2) % 16 == 0 &&
+                 (cache_stride_token * 2) % 16 == 0 && (cache_stride_head * 2) % 16 == 0,
+             "paged_attention: tensors and their strides must be 16-byte aligned");
+  const bool mixed = cu_seqlens_q != nullptr && max_seqlen_q > 1;
+  LV_REQUIRE(!mixed || num_rows <= kPlanMaxRows, "paged_attention: a step with prompts holds at most %d rows, got %d",
+             kPlanMaxRows, num_rows);
+  const Shape s = plan_shape(num_rows, num_tokens, num_heads, num_kv_heads, head_dim, max_seqlen_k, !mixed);
+  LV_REQUIRE(workspace_bytes >= s.bytes && (s.bytes == 0 || workspace),
+             "paged_attention: workspace of %zu bytes given, %zu needed", workspace_bytes, s.bytes);
+  LV_REQUIRE(aligned(workspace, 256), "paged_attention: workspace must be 256-byte aligned");
+
+  AttnParams p{};
+  p.q = (const char*)q;
+  p.q_st = q_stride_t * 2;
+  p.q_sh = q_stride_h * 2;
+  p.k_cache = (const char*)k_cache;
+  p.v_cache = (const char*)v_cache;
+  p.c_sb = cache_stride_block * 2;
+  p.c_st = cache_stride_token * 2;
+  p.c_sh = cache_stride_head * 2;
+  p.bs = block_size;
+  p.tables = block_tables;
+  p.t_stride = table_stride;
+  p.cu_q = cu_seqlens_q;
+  p.lens_k = seqlens_k;
+  p.cu_k = cu_seqlens_k;
+  p.rows = num_rows;
+  p.hq = num_heads;
+  p.hkv = num_kv_heads;
+  p.group = num_heads / num_kv_heads;
+  p.qgroups = p.group / s.gs;
+  p.scale_log2 = scale * kLog2e;
+  p.out = (char*)out;
+  p.o_st = out_stride_t * 2;
+  p.o_sh = out_stride_h * 2;
+  p.split = s.split;
+  p.max_splits = s.max_splits;
+  char* ws = (char*)workspace;
+  p.part_lse = s.max_splits > 1 ? reinterpret_cast<float*>(ws + s.lse_off) : nullptr;
+  p.part_o = s.max_splits > 1 ? reinterpret_cast<float*>(ws + s.o_off) : nullptr;
+  p.items = mixed ? reinterpret_cast<const int2*>(ws + s.items_off) : nullptr;
+  p.n_items = mixed ? reinterpret_cast<const int32_t*>(ws + s.count_off) : nullptr;
+
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  int grid_x = num_rows * s.max_splits;
+  if (mixed) {
+    const int qp = kPrefillRows / p.group;
+    hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kScanThreads), 0, st, cu_seqlens_q, seqlens_k, cu_seqlens_k,
+                       num_rows, s.split, qp, s.max_items, reinterpret_cast<int2*>(ws + s.items_off),
+                       reinterpret_cast<int32_t*>(ws + s.count_off));
+    LV_LAUNCH_CHECK("plan_kernel");
+    grid_x = s.max_items;
+  }
+  const int rc = dtype == LV_DTYPE_BF16 ? launch_d<BF16>(p, head_dim, s.gs, mixed, grid_x, st)
+                                        : launch_d<F16>(p, head_dim, s.gs, mixed, grid_x, st);
+  if (rc != LV_OK) return rc;
+  LV_LAUNCH_CHECK("paged_attention_kernel");
+  return LV_OK;
+}

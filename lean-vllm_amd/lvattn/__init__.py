@@ -1,0 +1,30 @@
+"""lvattn: lean-vLLM's continuous-batching attention path, MI355X-native (gfx950 HIP kernels behind a C ABI).
+
+- ``MI355XAttention``: the per-layer attention backend (store_kvcache, decode, prefill, mixed steps).
+- ``Packer``: the ragged-batch packing of a step on the GPU.
+- ``Context``, ``LayerSpec``, ``AttentionBackend``, ``get_attention_backend``: the reference's interface.
+"""
+
+from .abstract import AttentionBackend, LayerSpec, write_into
+from .backend import MI355XAttention
+from .context import Context, get_context, reset_context, set_context, split_decodes_and_prefills, use_context
+from .pack import Packer, StagingBuffers, decode_query_len
+from .selector import BACKENDS, get_attention_backend
+
+__all__ = [
+    "BACKENDS",
+    "AttentionBackend",
+    "Context",
+    "LayerSpec",
+    "MI355XAttention",
+    "Packer",
+    "StagingBuffers",
+    "decode_query_len",
+    "get_attention_backend",
+    "get_context",
+    "reset_context",
+    "set_context",
+    "split_decodes_and_prefills",
+    "use_context",
+    "write_into",
+]

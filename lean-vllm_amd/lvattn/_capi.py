@@ -1,0 +1,99 @@
+"""ctypes binding of ``liblvattn.so``: the C ABI declared in ``include/lvattn.h``.
+
+Loading order matters: torch is imported first, so the library's ``libamdhip64.so.7`` dependency binds to the
+HIP runtime torch already loaded (both carry that soname) and torch's streams and allocations are valid here.
+There is no fallback: if the library is missing or fails to load, every call raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from ctypes import c_float, c_int32, c_int64, c_size_t, c_void_p
+from pathlib import Path
+
+import torch  # noqa: F401  -- loads the HIP runtime this library must share
+
+LIBRARY = Path(__file__).resolve().parent / "liblvattn.so"
+
+# name -> (restype, argtypes), exactly the prototypes of include/lvattn.h
+_P = c_void_p
+_PROTOTYPES = {
+    "lv_last_error": (ctypes.c_char_p, []),
+    "lv_abi_version": (ctypes.c_int, []),
+    "lv_pack": (ctypes.c_int, [_P, _P, _P, _P, c_int32, c_int32, c_int32, c_int32, c_int32,
+                               _P, _P, _P, _P, _P, _P, _P, _P]),
+    "lv_store_kvcache": (ctypes.c_int, [_P, _P, c_int64, c_int64, c_int32, c_int32, c_int32, _P, _P,
+                                        c_int64, c_int64, c_int64, c_int32, _P, c_int32, _P]),
+    "lv_store_latents": (ctypes.c_int, [_P, c_int64, c_int32, c_int32, _P, _P, c_int32, _P]),
+    "lv_paged_attention_workspace_bytes": (c_size_t, [c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,
+                                                      c_int32]),
+    "lv_paged_attention": (ctypes.c_int, [_P, c_int64, c_int64, _P, _P, c_int64, c_int64, c_int64, c_int32, _P,
+                                          c_int64, _P, _P, _P, c_int32, c_int32, c_int32, c_int32, c_int32,
+                                          c_float, c_int32, c_int32, _P, c_int64, c_int64, _P, c_size_t,
+                                          c_int32, _P]),
+    "lv_merge_attn_states": (ctypes.c_int, [_P, c_int64, c_int64, _P, c_int64, c_int64, _P, c_int64, c_int64,
+                                            _P, c_int64, c_int64, _P, c_int64, c_int64, c_int32, c_int32,
+                                            c_int32, c_int32, _P]),
+    "lv_mla_decode_workspace_bytes": (c_size_t, [c_int32, c_int32, c_int32, c_int32, c_int32, c_int32]),
+    "lv_mla_decode": (ctypes.c_int, [_P, c_int64, c_int64, _P, c_int64, c_int32, _P, c_int64, _P, c_int32,
+                                     c_int32, c_int32, c_int32, c_int32, c_float, c_int32, _P, c_int64, c_int64,
+                                     _P, c_size_t, c_int32, _P]),
+}
+
+LV_OK, LV_EINVAL, LV_EHIP = 0, 1, 2
+DTYPES = {torch.bfloat16: 0, torch.float16: 1}
+
+_lib: ctypes.CDLL | None = None
+
+
+class LvError(RuntimeError):
+    """A non-zero status from the C ABI, with the library's message."""
+
+
+def library_path() -> Path:
+    return LIBRARY
+
+
+def load() -> ctypes.CDLL:
+    """The loaded library; raises if it is not built."""
+    global _lib
+    if _lib is None:
+        if not LIBRARY.exists():
+            raise LvError(f"{LIBRARY} is not built; run __graft_entry__.build() (or python -m lvattn._build)")
+        lib = ctypes.CDLL(str(LIBRARY))
+        for name, (restype, argtypes) in _PROTOTYPES.items():
+            fn = getattr(lib, name, None)
+            if fn is None:
+                continue  # reported by exported_symbols / the tests, not at load
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _lib = lib
+    return _lib
+
+
+def exported_symbols() -> dict[str, bool]:
+    lib = load()
+    return {name: hasattr(lib, name) for name in _PROTOTYPES}
+
+
+def call(name: str, *args):
+    """Call ``name`` and raise ``LvError`` with the library's message on a non-zero status."""
+    fn = getattr(load(), name)
+    rc = fn(*args)
+    if rc != LV_OK:
+        msg = load().lv_last_error().decode(errors="replace")
+        raise LvError(f"{name}: {msg} (status {rc})")
+    return rc
+
+
+def query(name: str, *args):
+    """Call a function returning a value (no status)."""
+    return getattr(load(), name)(*args)
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream

@@ -1,0 +1,165 @@
+"""The MI355X attention backend: lean-vLLM's per-layer backend contract on hand-written gfx950 kernels.
+
+Drop-in for ``lean_vllm/attention/abstract.py:29-224``: same constructor, capability flags, cache shape and
+methods; registered ahead of ``TorchAttention`` in the selector's ``BACKENDS``. Differences in behaviour, all
+allowed by the contract:
+- ``split_decodes()`` is False: a step with prompts goes to ``prefill`` whole, and one kernel launch serves its
+  decode rows (streaming) and prompt chunks (MFMA tiles) together, as the FA3 backend's single call does
+  (``lean_vllm/attention/flash_backend.py:75-89``).
+- Nothing syncs the host: slot -1 is skipped on the device, no length is read back, and split-K is sized from
+  host bounds (``max_seqlen_k`` or the block-table width), so decode can be captured in a full graph.
+- A row with no keys returns zeros (the torch backend returns NaN there; such rows are graph padding).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _capi
+from .abstract import AttentionBackend
+from .context import Context
+
+
+def _arch_ok() -> bool:
+    if not torch.cuda.is_available():
+        return False
+    try:
+        return torch.cuda.get_device_properties(0).gcnArchName.split(":")[0] == "gfx950"
+    except Exception:
+        return False
+
+
+class _Workspace:
+    """One growing device buffer per device for split-K partials and work lists. Its contents need no
+    initialisation, so a captured graph replays with whatever the last call left."""
+
+    def __init__(self):
+        self._buf: dict[torch.device, torch.Tensor] = {}
+
+    def get(self, device: torch.device, nbytes: int) -> torch.Tensor | None:
+        if nbytes == 0:
+            return None
+        buf = self._buf.get(device)
+        if buf is None or buf.numel() < nbytes:
+            size = max(nbytes, 2 * (buf.numel() if buf is not None else 0), 1 << 20)
+            buf = torch.empty(size, dtype=torch.uint8, device=device)
+            self._buf[device] = buf
+        return buf
+
+
+_WORKSPACE = _Workspace()
+
+
+class MI355XAttention(AttentionBackend):
+    """Paged attention, cache stores and MLA latent decode on MI355X (gfx950) HIP kernels."""
+
+    supported_dtypes = (torch.float16, torch.bfloat16)
+    supported_kinds = ("decoder",)
+
+    @staticmethod
+    def get_name() -> str:
+        return "mi355x"
+
+    @staticmethod
+    def is_available() -> bool:
+        return _arch_ok() and _capi.LIBRARY.exists()
+
+    @staticmethod
+    def supports_cuda_graph() -> bool:
+        return True
+
+    @staticmethod
+    def supports_full_cudagraph() -> bool:
+        return True
+
+    @staticmethod
+    def split_decodes() -> bool:
+        return False
+
+    @staticmethod
+    def supports_head_size(head_size: int) -> bool:
+        return head_size in (64, 128)
+
+    @classmethod
+    def validate(cls, spec) -> list[str]:
+        reasons = super().validate(spec)
+        if spec.kind == "decoder" and spec.num_kv_heads and spec.num_heads // max(spec.num_kv_heads, 1) > 64:
+            reasons.append(f"{spec.num_heads // spec.num_kv_heads} query heads per key head exceed 64")
+        return reasons
+
+    @staticmethod
+    def supports_mla_decode() -> bool:
+        return False
+
+    @staticmethod
+    def mla_block_size() -> int | None:
+        return None
+
+    # -- cache writes --------------------------------------------------------------------------------------
+    def store_kvcache(self, key, value, k_cache, v_cache, slot_mapping) -> None:
+        num_tokens, heads, dim = key.shape
+        assert key.stride(-1) == 1 and value.stride(-1) == 1, "unit dim stride"
+        assert key.stride(1) == dim and value.stride(1) == dim, "head stride must equal head_dim"
+        assert k_cache.stride() == v_cache.stride() and k_cache.stride(-1) == 1
+        assert slot_mapping.numel() == num_tokens
+        assert key.dtype == value.dtype == k_cache.dtype == v_cache.dtype
+        slot_mapping = slot_mapping if slot_mapping.dtype == torch.int32 else slot_mapping.to(torch.int32)
+        sb, st, sh, _ = k_cache.stride()
+        _capi.call("lv_store_kvcache", key.data_ptr(), value.data_ptr(), key.stride(0), value.stride(0), num_tokens,
+                   heads, dim, k_cache.data_ptr(), v_cache.data_ptr(), sb, st, sh, k_cache.size(1),
+                   slot_mapping.data_ptr(), key.element_size(), _capi.stream_of(key.device))
+
+    def store_latents(self, latent, latent_cache, slot_mapping) -> None:
+        num_tokens, dim = latent.shape
+        assert latent.stride(-1) == 1 and latent_cache.stride(-2) == dim and latent_cache.stride(-1) == 1
+        assert slot_mapping.numel() == num_tokens and latent.dtype == latent_cache.dtype
+        slot_mapping = slot_mapping if slot_mapping.dtype == torch.int32 else slot_mapping.to(torch.int32)
+        _capi.call("lv_store_latents", latent.data_ptr(), latent.stride(0), num_tokens, dim, latent_cache.data_ptr(),
+                   slot_mapping.data_ptr(), latent.element_size(), _capi.stream_of(latent.device))
+
+    # -- attention -----------------------------------------------------------------------------------------
+    def _attend(self, q, k_cache, v_cache, out, *, block_tables, cu_seqlens_q, seqlens_k, cu_seqlens_k, rows,
+                max_seqlen_q, max_seqlen_k):
+        assert q.dtype in _capi.DTYPES and k_cache.dtype == q.dtype == v_cache.dtype
+        assert q.stride(-1) == 1 and k_cache.stride() == v_cache.stride() and k_cache.stride(-1) == 1
+        assert block_tables is not None and block_tables.dtype == torch.int32 and block_tables.stride(-1) == 1
+        if out is None:
+            out = torch.empty_like(q)
+        assert out.shape == q.shape and out.stride(-1) == 1 and out.dtype == q.dtype
+        tokens, heads, dim = q.shape
+        decode_only = cu_seqlens_q is None or max_seqlen_q == 1
+        nbytes = _capi.query("lv_paged_attention_workspace_bytes", rows, tokens, heads, self.num_kv_heads, dim,
+                             max_seqlen_k, int(decode_only))
+        ws = _WORKSPACE.get(q.device, nbytes)
+        sb, st, sh, _ = k_cache.stride()
+        _capi.call("lv_paged_attention", q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(),
+                   v_cache.data_ptr(), sb, st, sh, k_cache.size(1), block_tables.data_ptr(), block_tables.stride(0),
+                   _capi.ptr(cu_seqlens_q), _capi.ptr(seqlens_k), _capi.ptr(cu_seqlens_k), rows, tokens, heads,
+                   self.num_kv_heads, dim, float(self.scale), max_seqlen_q, max_seqlen_k, out.data_ptr(),
+                   out.stride(0), out.stride(1), _capi.ptr(ws), 0 if ws is None else ws.numel(),
+                   _capi.DTYPES[q.dtype], _capi.stream_of(q.device))
+        return out
+
+    def decode(self, q, k_cache, v_cache, context: Context, out=None):
+        """One query per row against its ``context_lens[b]`` cached keys; q ``[B, Hq, D]``."""
+        bt, lens = context.block_tables, context.context_lens
+        assert bt is not None and lens is not None
+        lens = lens if lens.dtype == torch.int32 else lens.to(torch.int32)
+        # The table's width bounds every length, so nothing is read back (torch_backend.py:98).
+        max_k = bt.size(1) * k_cache.size(1)
+        return self._attend(q, k_cache, v_cache, out, block_tables=bt, cu_seqlens_q=None, seqlens_k=lens,
+                            cu_seqlens_k=None, rows=q.size(0), max_seqlen_q=1, max_seqlen_k=max_k)
+
+    def prefill(self, q, k, v, k_cache, v_cache, context: Context, out=None):
+        """Varlen causal attention over the step's rows, bottom-right aligned, every key read from the pages;
+        rows of one query take the streaming decode path inside the same launch."""
+        cu_q, cu_k = context.cu_seqlens_q, context.cu_seqlens_k
+        assert cu_q is not None and cu_k is not None
+        if context.block_tables is None:
+            raise NotImplementedError("the mi355x backend reads keys from the paged cache; pass block_tables")
+        bt = context.block_tables
+        max_k = context.max_seqlen_k or bt.size(1) * k_cache.size(1)
+        max_q = context.max_seqlen_q or q.size(0)
+        return self._attend(q, k_cache, v_cache, out, block_tables=bt, cu_seqlens_q=cu_q.to(torch.int32),
+                            seqlens_k=None, cu_seqlens_k=cu_k.to(torch.int32), rows=cu_q.numel() - 1,
+                            max_seqlen_q=max_q, max_seqlen_k=max_k)

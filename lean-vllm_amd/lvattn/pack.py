@@ -1,0 +1,166 @@
+"""Ragged-batch packing on the GPU: the attention half of ``ModelRunner.prepare_batch``
+(``lean_vllm/engine/model_runner.py:349-519``) as one kernel.
+
+The host hands over only per-row integers -- ``num_cached``, ``num_new`` and each row's block list (CSR) -- in one
+pinned buffer and one copy. The kernel produces the per-token ``positions`` and ``slot_mapping``, the ``-1``-padded
+``block_tables`` and the row prefix sums, in the decode-first row order the reference uses. The host keeps the
+row-level ints the ``Context`` carries as host lists (``cu_seqlens_*_host``, ``max_seqlen_*``), which it derives
+from the same per-row ints without touching per-token data.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import _capi
+
+MIN_CAPACITY = 256
+
+
+def decode_query_len(lens: np.ndarray, num_speculative_tokens: int = 0) -> int:
+    """The most common query length not above ``1 + num_speculative_tokens``, shorter on ties, else 1
+    (``model_runner.py:51-63``)."""
+    short = lens[lens <= 1 + num_speculative_tokens]
+    if short.size == 0:
+        return 1
+    return int(np.argmax(np.bincount(short)))
+
+
+class StagingBuffers:
+    """Named device buffers fed from reusable pinned host buffers (``lean_vllm/engine/input_buffers.py:17-56``):
+    grow to at least twice their size, copy asynchronously, and fence the host buffers with an event so a step
+    never overwrites what the previous step's copy is still reading."""
+
+    def __init__(self, device: torch.device):
+        self.device = torch.device(device)
+        self._pinned: dict[str, torch.Tensor] = {}
+        self._device: dict[str, torch.Tensor] = {}
+        self._copied: torch.cuda.Event | None = None
+
+    def begin(self):
+        if self._copied is not None:
+            self._copied.synchronize()
+            self._copied = None
+
+    def end(self):
+        self._copied = torch.cuda.Event()
+        self._copied.record(torch.cuda.current_stream(self.device))
+
+    def device_buffer(self, name: str, n: int, dtype: torch.dtype) -> torch.Tensor:
+        """A device buffer of at least ``n`` elements for a kernel to fill."""
+        buf = self._device.get(name)
+        if buf is None or buf.numel() < n or buf.dtype != dtype:
+            cap = max(n, 2 * (buf.numel() if buf is not None else 0), MIN_CAPACITY)
+            buf = torch.empty(cap, dtype=dtype, device=self.device)
+            self._device[name] = buf
+        return buf[:n]
+
+    def put(self, name: str, values: np.ndarray, dtype: torch.dtype) -> torch.Tensor:
+        """Copy host values into this name's device buffer through its pinned buffer."""
+        n = values.size
+        host = self._pinned.get(name)
+        if host is None or host.numel() < n:
+            cap = max(n, 2 * (host.numel() if host is not None else 0), MIN_CAPACITY)
+            host = torch.empty(cap, dtype=dtype, pin_memory=True)
+            self._pinned[name] = host
+        host[:n].numpy()[:] = values.reshape(-1)
+        dev = self.device_buffer(name, n, dtype)
+        dev.copy_(host[:n], non_blocking=True)
+        return dev
+
+
+class PackPlan:
+    """One step's staged packing inputs (device) and the row-level host ints derived from them."""
+
+    __slots__ = ("rows", "tokens", "width", "slot_count", "query_len", "inputs", "host")
+
+    def __init__(self, rows, tokens, width, slot_count, query_len, inputs, host):
+        self.rows, self.tokens, self.width, self.slot_count = rows, tokens, width, slot_count
+        self.query_len, self.inputs, self.host = query_len, inputs, host
+
+
+class Packer:
+    """Builds a step's attention ``Context`` fields on the GPU from per-row scheduler state."""
+
+    def __init__(self, device, block_size: int):
+        self.block_size = block_size
+        self.buffers = StagingBuffers(device)
+
+    def pack(self, num_cached, num_new, block_lists, num_speculative_tokens: int = 0,
+             is_prompt=None) -> tuple[torch.Tensor, dict]:
+        """Per-row ``num_cached``, ``num_new`` (scheduler order) and block lists -> ``(positions, context)``.
+
+        ``context`` has the keys of ``prepare_batch``'s context dict (``model_runner.py:448-462``) that attention
+        reads, plus ``order`` (batch row -> scheduler row). ``is_prompt`` marks prompt rows (default: rows with
+        more than one new token), which makes the step ``is_prefill``. The returned tensors live in buffers the
+        next call reuses.
+        """
+        self.buffers.begin()
+        plan = self.stage(num_cached, num_new, block_lists, num_speculative_tokens, is_prompt)
+        out = self.run(plan)
+        self.buffers.end()
+        return out
+
+    def stage(self, num_cached, num_new, block_lists, num_speculative_tokens: int = 0, is_prompt=None) -> PackPlan:
+        """Copy the per-row inputs to the device (one pinned copy) and derive the host-side row ints."""
+        num_cached = np.asarray(num_cached, dtype=np.int32)
+        num_new = np.asarray(num_new, dtype=np.int32)
+        rows = num_new.size
+        if rows == 0:
+            raise ValueError("pack: a step needs at least one row")
+        lengths = np.fromiter((len(b) for b in block_lists), np.int32, rows)
+        indptr = np.zeros(rows + 1, dtype=np.int32)
+        np.cumsum(lengths, out=indptr[1:])
+        ids = np.concatenate([np.asarray(b, dtype=np.int32) for b in block_lists]) if indptr[-1] else \
+            np.zeros(0, dtype=np.int32)
+        width = int(lengths.max())
+        tokens = int(num_new.sum())
+        query_len = decode_query_len(num_new, num_speculative_tokens)
+        order = np.argsort(num_new != query_len, kind="stable")
+        lens_b, ends_b = num_new[order], (num_cached + num_new)[order]
+        if is_prompt is None:
+            is_prompt = num_new > 1
+        host = dict(
+            is_prefill=bool(np.any(is_prompt)),
+            max_seqlen_q=int(lens_b.max()),
+            max_seqlen_k=int(ends_b.max()),
+            cu_seqlens_q_host=[0, *np.cumsum(lens_b).tolist()],
+            cu_seqlens_k_host=[0, *np.cumsum(ends_b).tolist()],
+            decode_query_len=query_len,
+        )
+        staged = np.concatenate([num_cached, num_new, indptr, ids])
+        inputs = self.buffers.put("inputs", staged, torch.int32)
+        slot_count = int(num_new[lengths > 0].sum())
+        return PackPlan(rows, tokens, width, slot_count, query_len, inputs, host)
+
+    def run(self, plan: PackPlan) -> tuple[torch.Tensor, dict]:
+        """Launch the pack kernel on staged inputs; returns ``(positions, context)``."""
+        buf, rows, width = self.buffers, plan.rows, plan.width
+        d_cached = plan.inputs[:rows]
+        d_new = plan.inputs[rows:2 * rows]
+        d_indptr = plan.inputs[2 * rows:3 * rows + 1]
+        d_ids = plan.inputs[3 * rows + 1:]
+        has_tables = width > 0
+        out_order = buf.device_buffer("order", rows, torch.int32)
+        cu_q = buf.device_buffer("cu_seqlens_q", rows + 1, torch.int32)
+        cu_k = buf.device_buffer("cu_seqlens_k", rows + 1, torch.int32)
+        positions = buf.device_buffer("positions", plan.tokens, torch.int64)
+        slots = buf.device_buffer("slot_mapping", plan.slot_count, torch.int32)
+        context_lens = buf.device_buffer("context_lens", rows, torch.int32)
+        tables = buf.device_buffer("block_tables", rows * width, torch.int32) if has_tables else None
+        _capi.call("lv_pack", d_cached.data_ptr(), d_new.data_ptr(), d_indptr.data_ptr(),
+                   d_ids.data_ptr() if d_ids.numel() else None, rows, plan.query_len, self.block_size, width,
+                   plan.tokens, out_order.data_ptr(), cu_q.data_ptr(), cu_k.data_ptr(), positions.data_ptr(),
+                   slots.data_ptr() if has_tables else None, context_lens.data_ptr(),
+                   tables.data_ptr() if has_tables else None, _capi.stream_of(buf.device))
+        context = dict(
+            plan.host,
+            cu_seqlens_q=cu_q,
+            cu_seqlens_k=cu_k,
+            slot_mapping=slots,
+            context_lens=context_lens,
+            block_tables=tables.view(rows, width) if has_tables else None,
+            order=out_order,
+        )
+        return positions, context

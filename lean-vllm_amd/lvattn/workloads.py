@@ -1,0 +1,203 @@
+"""Synthetic continuous-batching steps of the shapes this path is measured on.
+
+Each workload is a step's per-row scheduler state -- ``num_cached``, ``num_new`` and a block list per row, in
+scheduler order -- plus the layer shape. Lengths and block lists come from ``numpy.random.default_rng(seed)``
+(identical on every machine); block lists are consecutive slices of a seeded permutation of the block pool, so
+pages are scattered. Tensor values are drawn by ``materialize`` with a seeded torch generator on the target
+device. Key lengths include the token(s) stored this step (``context_lens = num_cached + num_new``).
+
+- ``qwen3_0_6b_mixed``: 16/8 heads, d128, bs 256, pool 512; chunks 0->512 and 256->384 new, plus 30 decode rows
+  with context U[64, 2048].
+- ``qwen3_8b_decode``: 32/8 heads, d128, bs 256, pool 12,000; 256 decode rows, context U[512, 8192].
+- ``qwen3_8b_mixed``: 32/8 heads, d128, bs 256, pool 24,000; 4 chunks of 1536 new tokens on a cached prefix
+  U[0, 6144], plus 2048 decode rows with context U[256, 4096] (8192 tokens).
+- ``qwen3_8b_long``: 32/8 heads, d128, bs 256, pool 10,000; 16 decode rows, context U[32768, 131072].
+- ``deepseek_v2_lite_mla``: 16 heads, latent 576 (512 + 64 rope), values 512, bs 64, pool 34,000; 128 decode
+  rows, context U[1024, 16384]; values N(0, 0.5); scale 1/sqrt(192).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+
+@dataclass
+class Workload:
+    name: str
+    num_heads: int
+    num_kv_heads: int
+    head_dim: int
+    block_size: int
+    pool: int
+    num_cached: list[int]
+    num_new: list[int]
+    block_lists: list[list[int]]
+    scale: float
+    value_std: float = 1.0
+    latent_dim: int = 0  # MLA: cached latent width
+    v_dim: int = 0  # MLA: value width (leading entries of a latent)
+    notes: dict = field(default_factory=dict)
+
+    @property
+    def rows(self) -> int:
+        return len(self.num_new)
+
+    @property
+    def tokens(self) -> int:
+        return int(sum(self.num_new))
+
+    @property
+    def context_lens(self) -> np.ndarray:
+        return np.asarray(self.num_cached, np.int64) + np.asarray(self.num_new, np.int64)
+
+    @property
+    def is_mla(self) -> bool:
+        return self.latent_dim > 0
+
+    def kv_bytes_per_token(self, elem_bytes: int = 2) -> int:
+        """Cache bytes one attended key position costs: K and V of every kv head, or one MLA latent."""
+        if self.is_mla:
+            return self.latent_dim * elem_bytes
+        return 2 * self.num_kv_heads * self.head_dim * elem_bytes
+
+
+def _tables(rng, pool: int, ends, block_size: int) -> list[list[int]]:
+    perm = rng.permutation(pool)
+    need = [-(-int(e) // block_size) for e in ends]
+    if sum(need) > pool:
+        raise ValueError(f"pool of {pool} blocks is smaller than the {sum(need)} the step needs")
+    out, at = [], 0
+    for n in need:
+        out.append([int(x) for x in perm[at:at + n]])
+        at += n
+    return out
+
+
+def qwen3_0_6b_mixed(seed: int = 0) -> Workload:
+    rng = np.random.default_rng(seed)
+    dec = rng.integers(64, 2048 + 1, size=30)
+    num_cached = [0, 256] + [int(c) - 1 for c in dec]
+    num_new = [512, 384] + [1] * 30
+    ends = [c + n for c, n in zip(num_cached, num_new)]
+    return Workload("qwen3_0_6b_mixed", 16, 8, 128, 256, 512, num_cached, num_new, _tables(rng, 512, ends, 256),
+                    1 / math.sqrt(128))
+
+
+def qwen3_8b_decode(seed: int = 0, batch: int = 256) -> Workload:
+    rng = np.random.default_rng(seed)
+    ctx = rng.integers(512, 8192 + 1, size=batch)
+    num_cached = [int(c) - 1 for c in ctx]
+    num_new = [1] * batch
+    return Workload("qwen3_8b_decode", 32, 8, 128, 256, 12_000, num_cached, num_new,
+                    _tables(rng, 12_000, ctx, 256), 1 / math.sqrt(128))
+
+
+def qwen3_8b_mixed(seed: int = 0) -> Workload:
+    rng = np.random.default_rng(seed)
+    prefix = rng.integers(0, 6144 + 1, size=4)
+    dec = rng.integers(256, 4096 + 1, size=2048)
+    # Scheduler order: the chunks first; packing moves the one-token rows to the front.
+    num_cached = [int(p) for p in prefix] + [int(c) - 1 for c in dec]
+    num_new = [1536] * 4 + [1] * 2048
+    ends = [c + n for c, n in zip(num_cached, num_new)]
+    return Workload("qwen3_8b_mixed", 32, 8, 128, 256, 24_000, num_cached, num_new,
+                    _tables(rng, 24_000, ends, 256), 1 / math.sqrt(128))
+
+
+def qwen3_8b_long(seed: int = 0) -> Workload:
+    rng = np.random.default_rng(seed)
+    ctx = rng.integers(32768, 131072 + 1, size=16)
+    num_cached = [int(c) - 1 for c in ctx]
+    return Workload("qwen3_8b_long", 32, 8, 128, 256, 10_000, num_cached, [1] * 16,
+                    _tables(rng, 10_000, ctx, 256), 1 / math.sqrt(128))
+
+
+def deepseek_v2_lite_mla(seed: int = 0) -> Workload:
+    rng = np.random.default_rng(seed)
+    ctx = rng.integers(1024, 16384 + 1, size=128)
+    num_cached = [int(c) - 1 for c in ctx]
+    return Workload("deepseek_v2_lite_mla", 16, 1, 576, 64, 34_000, num_cached, [1] * 128,
+                    _tables(rng, 34_000, ctx, 64), 1 / math.sqrt(192), value_std=0.5, latent_dim=576, v_dim=512)
+
+
+WORKLOADS = {
+    "qwen3_0_6b_mixed": qwen3_0_6b_mixed,
+    "qwen3_8b_decode": qwen3_8b_decode,
+    "qwen3_8b_mixed": qwen3_8b_mixed,
+    "qwen3_8b_long": qwen3_8b_long,
+    "deepseek_v2_lite_mla": deepseek_v2_lite_mla,
+}
+
+
+@dataclass
+class Tensors:
+    q: torch.Tensor  # [T, Hq, D] (MLA: [T, H, latent])
+    k_new: torch.Tensor | None  # [T, Hkv, D] this step's keys (MLA: latents [T, latent])
+    v_new: torch.Tensor | None
+    k_cache: torch.Tensor  # [pool, bs, Hkv, D] (MLA: [pool, bs, latent])
+    v_cache: torch.Tensor | None
+
+
+def _randn(shape, generator, device, dtype, std: float, chunk: int = 1 << 27):
+    """N(0, std) drawn in fp32 (in chunks, so a multi-GB cache needs no multi-GB fp32 temporary), then cast."""
+    out = torch.empty(shape, dtype=dtype, device=device)
+    flat = out.view(-1)
+    for at in range(0, flat.numel(), chunk):
+        n = min(chunk, flat.numel() - at)
+        flat[at:at + n] = (torch.randn(n, generator=generator, device=device) * std).to(dtype)
+    return out
+
+
+def materialize(wl: Workload, device, dtype=torch.bfloat16, seed: int = 0) -> Tensors:
+    """Draw the step's q, new K/V and a whole cache pool of N(0, std) values (the cache is filled everywhere,
+    so unwritten pages hold finite values too)."""
+    device = torch.device(device)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    std = wl.value_std
+    if wl.is_mla:
+        q = _randn((wl.tokens, wl.num_heads, wl.latent_dim), gen, device, dtype, std)
+        lat = _randn((wl.tokens, wl.latent_dim), gen, device, dtype, std)
+        cache = _randn((wl.pool, wl.block_size, wl.latent_dim), gen, device, dtype, std)
+        return Tensors(q, lat, None, cache, None)
+    q = _randn((wl.tokens, wl.num_heads, wl.head_dim), gen, device, dtype, std)
+    k = _randn((wl.tokens, wl.num_kv_heads, wl.head_dim), gen, device, dtype, std)
+    v = _randn((wl.tokens, wl.num_kv_heads, wl.head_dim), gen, device, dtype, std)
+    shape = (wl.pool, wl.block_size, wl.num_kv_heads, wl.head_dim)
+    return Tensors(q, k, v, _randn(shape, gen, device, dtype, std), _randn(shape, gen, device, dtype, std))
+
+
+def batch_order(wl: Workload) -> np.ndarray:
+    """Scheduler row of each batch row: one-token rows first, scheduler order kept within each group."""
+    return np.argsort(np.asarray(wl.num_new) != 1, kind="stable")
+
+
+def algorithmic_bytes(wl: Workload, elem_bytes: int = 2) -> dict:
+    """Bytes the step must move at least once, from the drawn lengths: every attended key position's cache
+    bytes, q and out, the store of this step's new K/V, and the pack kernel's inputs and outputs."""
+    ctx = wl.context_lens
+    kv = int(ctx.sum()) * wl.kv_bytes_per_token(elem_bytes)
+    if wl.is_mla:
+        qo = wl.tokens * wl.num_heads * (wl.latent_dim + wl.v_dim) * elem_bytes
+        store = 2 * wl.tokens * wl.latent_dim * elem_bytes
+    else:
+        qo = 2 * wl.tokens * wl.num_heads * wl.head_dim * elem_bytes
+        store = 2 * wl.tokens * wl.kv_bytes_per_token(elem_bytes)
+    nblocks = sum(len(b) for b in wl.block_lists)
+    width = max(len(b) for b in wl.block_lists)
+    pack = 4 * (3 * wl.rows + 1 + nblocks) + 4 * (4 * wl.rows + 2) + 12 * wl.tokens + 4 * wl.rows * width
+    return dict(kv=kv, qo=qo, store=store, pack=pack, attention=kv + qo, total=kv + qo + store + pack)
+
+
+def algorithmic_flops(wl: Workload) -> int:
+    """4 * heads * D * (keys each query sees), summed over queries (QK and PV, 2 flops per MAC)."""
+    total = 0
+    for c, n in zip(wl.num_cached, wl.num_new):
+        seen = n * c + n * (n + 1) // 2  # query j of the row sees c + j + 1 keys
+        total += seen
+    d = (wl.latent_dim + wl.v_dim) // 2 if wl.is_mla else wl.head_dim
+    return 4 * wl.num_heads * d * total

@@ -1,0 +1,54 @@
+"""The C-ABI library (CPU only): it loads, exports every function include/lvattn.h declares, and rejects bad
+arguments with a message before touching the GPU."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from lvattn import _capi
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "lvattn.h"
+
+
+def declared():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(lv_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_path():
+    names = declared()
+    for name in ("lv_pack", "lv_store_kvcache", "lv_store_latents", "lv_paged_attention",
+                 "lv_paged_attention_workspace_bytes", "lv_merge_attn_states", "lv_last_error", "lv_abi_version"):
+        assert name in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _capi.load()
+    missing = [n for n in declared() if not hasattr(lib, n)]
+    assert not missing, f"declared in lvattn.h but not exported: {missing}"
+    assert lib.lv_abi_version() == 1
+    assert all(n in _capi._PROTOTYPES for n in declared()), "every declared function has a ctypes prototype"
+
+
+def test_bad_arguments_raise_with_the_library_message():
+    with pytest.raises(_capi.LvError, match="rows; 1 to 4096"):
+        _capi.call("lv_pack", None, None, None, None, 0, 1, 16, 0, 0, None, None, None, None, None, None, None, None)
+    with pytest.raises(_capi.LvError, match="block_size must be positive"):
+        _capi.call("lv_store_kvcache", None, None, 0, 0, 1, 1, 8, None, None, 0, 0, 0, 0, None, 2, None)
+    with pytest.raises(_capi.LvError, match="head_dim 96"):
+        _capi.call("lv_paged_attention", 1, 0, 0, 1, 1, 0, 0, 0, 16, 1, 0, None, 1, None, 1, 1, 8, 2, 96, 1.0, 1, 16,
+                   1, 0, 0, None, 0, 0, None)
+    with pytest.raises(_capi.LvError, match="not bf16 or fp16"):
+        _capi.call("lv_paged_attention", 1, 0, 0, 1, 1, 0, 0, 0, 16, 1, 0, None, 1, None, 1, 1, 8, 2, 64, 1.0, 1, 16,
+                   1, 0, 0, None, 0, 7, None)
+
+
+def test_workspace_query_sizes():
+    # pure decode of one short row needs no split-K partials
+    small = _capi.query("lv_paged_attention_workspace_bytes", 1, 1, 8, 2, 64, 64, 1)
+    big = _capi.query("lv_paged_attention_workspace_bytes", 16, 16, 32, 8, 128, 131072, 1)
+    assert small <= 512 and big > 1 << 20
+    assert _capi.query("lv_paged_attention_workspace_bytes", 0, 0, 8, 2, 64, 64, 1) == 0

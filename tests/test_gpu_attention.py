@@ -1,0 +1,220 @@
+"""The HIP backend against the oracle on the reference tests' cases (tests/test_attention_backends.py), through
+the C ABI. Shapes: 8 query heads over 2 key heads, head dim 64 and 128, scale 0.137, 16-token pages.
+
+Tolerances: fp16 6e-3 against fp32 (the reference's); bf16 2e-2 absolute / 1e-2 relative against an fp32
+evaluation of the same math (the path's stated bar)."""
+
+import math
+
+import pytest
+import torch
+
+from helpers import context_for, dense_expected, paged_step, randn, slots_for
+from lvattn import Context, MI355XAttention
+from oracle import attention as A
+
+pytestmark = pytest.mark.gpu
+
+H, HKV, SCALE, BS = 8, 2, 0.137, 16
+TOL = {torch.float16: dict(atol=6e-3, rtol=6e-3), torch.bfloat16: dict(atol=2e-2, rtol=1e-2)}
+
+
+@pytest.fixture(params=[(torch.float16, 64), (torch.bfloat16, 64), (torch.bfloat16, 128)],
+                ids=["fp16-d64", "bf16-d64", "bf16-d128"])
+def case(request, cuda):
+    dtype, dim = request.param
+    return MI355XAttention(H, dim, SCALE, HKV), dtype, dim, cuda
+
+
+def check(out, want, dtype):
+    torch.testing.assert_close(out.float().cpu(), want.float(), **TOL[dtype])
+
+
+def run_step(backend, dtype, dim, device, num_cached, num_new, tables, nblocks, layout="NHD", host=True):
+    qs, kf, vf, kn, vn, kc, vc, slots = paged_step(num_cached, num_new, tables, nblocks, heads=H, kv_heads=HKV,
+                                                   dim=dim, bs=BS, device=device, dtype=dtype, layout=layout)
+    backend.store_kvcache(kn, vn, kc, vc, slots)
+    ctx = context_for(num_cached, num_new, tables, device, host=host)
+    out = backend.forward(torch.cat(qs), kn, vn, kc, vc, ctx)
+    torch.cuda.synchronize()
+    return out, dense_expected(qs, kf, vf, SCALE), (qs, kf, vf, kc, vc, ctx)
+
+
+def test_prefill_of_a_cold_batch_with_pages(case):
+    b, dtype, dim, dev = case
+    out, want, _ = run_step(b, dtype, dim, dev, [0, 0], [5, BS + 3], [[0, 1, -1], [2, 3, 4]], 6)
+    check(out, want, dtype)
+
+
+def test_prefill_with_prefix_cache(case):
+    b, dtype, dim, dev = case
+    out, want, _ = run_step(b, dtype, dim, dev, [2 * BS + 2, 0], [6, 5],
+                            [[0, 1, 2, 3, 4, 5], [6, 7, -1, -1, -1, -1]], 8)
+    check(out, want, dtype)
+
+
+def test_mixed_batch_of_chunks_and_decodes(case):
+    b, dtype, dim, dev = case
+    out, want, _ = run_step(b, dtype, dim, dev, [2 * BS + 5, BS + 1, 0], [1, 7, 4],
+                            [[0, 1, 2], [3, 4, -1], [5, -1, -1]], 6)
+    check(out, want, dtype)
+
+
+def test_decode(case):
+    b, dtype, dim, dev = case
+    lens = [BS + 3, 3, 4 * BS]
+    tables = [[0, 1, 2, 3], [4, 5, -1, -1], [6, 7, 8, 9]]
+    qs, kf, vf, kn, vn, kc, vc, slots = paged_step([n - 1 for n in lens], [1, 1, 1], tables, 10, heads=H,
+                                                   kv_heads=HKV, dim=dim, bs=BS, device=dev, dtype=dtype)
+    b.store_kvcache(kn, vn, kc, vc, slots)
+    ctx = Context(is_prefill=False, context_lens=torch.tensor(lens, dtype=torch.int32, device=dev),
+                  block_tables=torch.tensor(tables, dtype=torch.int32, device=dev))
+    out = b.forward(torch.cat(qs), kn, vn, kc, vc, ctx)
+    check(out, dense_expected(qs, kf, vf, SCALE), dtype)
+
+
+def test_decode_matches_equivalent_prefill(case):
+    b, dtype, dim, dev = case
+    n = 2 * BS + 1
+    qs, kf, vf, kn, vn, kc, vc, slots = paged_step([n - 1], [1], [[0, 1, 2]], 3, heads=H, kv_heads=HKV, dim=dim,
+                                                   bs=BS, device=dev, dtype=dtype)
+    b.store_kvcache(kn, vn, kc, vc, slots)
+    bt = torch.tensor([[0, 1, 2]], dtype=torch.int32, device=dev)
+    dec = b.decode(qs[0], kc, vc, Context(context_lens=torch.tensor([n], dtype=torch.int32, device=dev), block_tables=bt))
+    pre = b.prefill(qs[0], kn, vn, kc, vc, context_for([n - 1], [1], [[0, 1, 2]], dev))
+    torch.testing.assert_close(dec, pre, **TOL[dtype])
+
+
+def test_mixed_batch_matches_running_the_rows_separately(case):
+    b, dtype, dim, dev = case
+    num_cached, num_new = [BS + 1, 3 * BS], [6, 1]  # a chunk, then a decode row
+    tables = [[0, 1, -1, -1], [2, 3, 4, 5]]
+    out, _, (qs, kf, vf, kc, vc, ctx) = run_step(b, dtype, dim, dev, num_cached, num_new, tables, 6)
+    chunk = b.prefill(qs[0], None, None, kc, vc, context_for([num_cached[0]], [6], [tables[0]], dev))
+    dec = b.decode(qs[1], kc, vc, Context(context_lens=torch.tensor([3 * BS + 1], dtype=torch.int32, device=dev),
+                                          block_tables=torch.tensor([tables[1]], dtype=torch.int32, device=dev)))
+    torch.testing.assert_close(out, torch.cat([chunk, dec]), **TOL[dtype])
+
+
+def test_top_left_causal_alignment_would_be_wrong(case):
+    b, dtype, dim, dev = case
+    lq, lk = 4, 2 * BS + 2
+    out, want, (qs, kf, vf, *_ ) = run_step(b, dtype, dim, dev, [lk - lq], [lq], [[0, 1, 2]], 3)
+    check(out, want, dtype)
+    q, k, v = qs[0].float().cpu(), kf[0].float().cpu(), vf[0].float().cpu()
+    top_left = torch.nn.functional.scaled_dot_product_attention(
+        q.transpose(0, 1), k.repeat_interleave(H // HKV, 1).transpose(0, 1),
+        v.repeat_interleave(H // HKV, 1).transpose(0, 1), is_causal=True, scale=SCALE).transpose(0, 1)
+    assert not torch.allclose(out.float().cpu(), top_left, atol=5 * TOL[dtype]["atol"])
+
+
+def test_an_hnd_cache_stores_and_attends_as_an_nhd_one(case):
+    b, dtype, dim, dev = case
+    args = ([BS + 3 - 1, 4], [1, 1], [[0, 3], [1, -1]], 4)
+    nhd, _, _ = run_step(b, dtype, dim, dev, *args, layout="NHD")
+    hnd, _, _ = run_step(b, dtype, dim, dev, *args, layout="HND")
+    torch.testing.assert_close(hnd, nhd, atol=0, rtol=0)
+
+
+def test_low_precision_no_worse_than_naive(cuda):
+    """tests/test_attention_backends.py:705-753: bf16 error against fp32 at most twice naive bf16 arithmetic's."""
+    b = MI355XAttention(H, 64, SCALE, HKV)
+    num_cached, num_new = 2 * BS + 2, 6
+    out, _, (qs, kf, vf, *_) = run_step(b, torch.bfloat16, 64, cuda, [num_cached], [num_new], [[0, 1, 2, 3]], 4)
+    q, k, v = qs[0].cpu(), kf[0].cpu(), vf[0].cpu()
+    ref = A.dense_attention(q.float(), k.float(), v.float(), SCALE)
+    naive = A.dense_attention(q, k, v, SCALE, compute_dtype=torch.bfloat16).float()
+    backend_err = (out.float().cpu() - ref).abs().max().item()
+    naive_err = (naive - ref).abs().max().item()
+    assert backend_err <= 2 * naive_err + 1e-6, (backend_err, naive_err)
+
+
+@pytest.mark.parametrize("poison", [float("nan"), float("inf")], ids=["nan", "inf"])
+def test_unwritten_cache_slots_are_ignored(cuda, poison):
+    """tests/test_attention_backends.py:142-168, at kernel shapes: poison everywhere outside the rows' keys."""
+    b = MI355XAttention(H, 64, SCALE, HKV)
+    for num_cached, num_new, tables in (([20, 3], [1, 1], [[1, 2], [0, -1]]), ([20, 0], [5, 3], [[1, 2], [0, -1]])):
+        qs, kf, vf, kn, vn, kc, vc, slots = paged_step(num_cached, num_new, tables, 3, heads=H, kv_heads=HKV, dim=64,
+                                                       bs=BS, device=cuda, dtype=torch.float16, fill=poison)
+        b.store_kvcache(kn, vn, kc, vc, slots)
+        ctx = context_for(num_cached, num_new, tables, cuda, is_prefill=max(num_new) > 1)
+        out = b.forward(torch.cat(qs), kn, vn, kc, vc, ctx)
+        assert torch.isfinite(out).all()
+        check(out, dense_expected(qs, kf, vf, SCALE), torch.float16)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_long_rows_split_over_keys(cuda, dtype):
+    """Rows long enough that decode splits them over keys, beside a one-key row and an empty-ish row."""
+    bs = 256
+    lens = [40_000, 1, 17, 9 * bs + 1, 5000]
+    nblocks = sum(-(-n // bs) for n in lens)
+    perm = torch.randperm(nblocks, generator=torch.Generator().manual_seed(1)).tolist()
+    tables, at = [], 0
+    width = max(-(-n // bs) for n in lens)
+    for n in lens:
+        k = -(-n // bs)
+        tables.append(perm[at:at + k] + [-1] * (width - k))
+        at += k
+    b = MI355XAttention(32, 128, 1 / math.sqrt(128), 8)
+    qs, kf, vf, kn, vn, kc, vc, slots = paged_step([n - 1 for n in lens], [1] * len(lens), tables, nblocks, heads=32,
+                                                   kv_heads=8, dim=128, bs=bs, device=cuda, dtype=dtype)
+    b.store_kvcache(kn, vn, kc, vc, slots)
+    ctx = Context(context_lens=torch.tensor(lens, dtype=torch.int32, device=cuda),
+                  block_tables=torch.tensor(tables, dtype=torch.int32, device=cuda))
+    out = b.decode(torch.cat(qs), kc, vc, ctx)
+    check(out, dense_expected(qs, kf, vf, 1 / math.sqrt(128)), dtype)
+
+
+def test_zero_length_rows_give_zeros(cuda):
+    """Graph padding rows (context_len 0) produce a zero output and disturb no other row."""
+    b = MI355XAttention(H, 64, SCALE, HKV)
+    qs, kf, vf, kn, vn, kc, vc, slots = paged_step([9], [1], [[0]], 2, heads=H, kv_heads=HKV, dim=64, bs=BS,
+                                                   device=cuda, dtype=torch.bfloat16)
+    b.store_kvcache(kn, vn, kc, vc, slots)
+    q = torch.cat([qs[0], torch.ones(1, H, 64, dtype=torch.bfloat16, device=cuda)])
+    ctx = Context(context_lens=torch.tensor([10, 0], dtype=torch.int32, device=cuda),
+                  block_tables=torch.tensor([[0], [1]], dtype=torch.int32, device=cuda))
+    out = b.decode(q, kc, vc, ctx)
+    assert torch.equal(out[1], torch.zeros_like(out[1]))
+    check(out[:1], dense_expected(qs, kf, vf, SCALE), torch.bfloat16)
+
+
+def test_out_is_written_in_place(cuda):
+    b = MI355XAttention(H, 64, SCALE, HKV)
+    out, want, (qs, kf, vf, kc, vc, ctx) = run_step(b, torch.float16, 64, cuda, [20, 0], [1, 7], [[0, 1], [2, -1]], 3)
+    buf = torch.empty(10, H, 64, dtype=torch.float16, device=cuda)
+    got = b.forward(torch.cat(qs), None, None, kc, vc, ctx, out=buf[2:10])
+    assert got.data_ptr() == buf[2:].data_ptr()
+    check(buf[2:10], want, torch.float16)
+
+
+def test_decode_replays_in_a_graph(cuda):
+    """A captured decode replays correctly with new queries and lengths written into its static inputs; each
+    replay is checked against an eager call, with eager work between replays."""
+    b = MI355XAttention(32, 128, 1 / math.sqrt(128), 8)
+    bs, rows, width = 256, 4, 8
+    lens = [300, 1500, 2047, 40]
+    qs, kf, vf, kn, vn, kc, vc, slots = paged_step([n - 1 for n in lens], [1] * rows,
+                                                   [[r * width + j for j in range(width)] for r in range(rows)],
+                                                   rows * width, heads=32, kv_heads=8, dim=128, bs=bs, device=cuda,
+                                                   dtype=torch.bfloat16)
+    b.store_kvcache(kn, vn, kc, vc, slots)
+    q = torch.cat(qs).clone()
+    ctx = Context(context_lens=torch.tensor(lens, dtype=torch.int32, device=cuda),
+                  block_tables=torch.arange(rows * width, dtype=torch.int32, device=cuda).view(rows, width))
+    out = torch.empty_like(q)
+    b.decode(q, kc, vc, ctx, out=out)  # warm: allocates the workspace outside capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        b.decode(q, kc, vc, ctx, out=out)
+    gen = torch.Generator().manual_seed(5)
+    for step in range(3):
+        q.copy_(torch.randn(q.shape, generator=gen).to(q.dtype))
+        ctx.context_lens.copy_(torch.tensor([max(l - 37 * step, 1) for l in lens], dtype=torch.int32))
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = b.decode(q, kc, vc, ctx)
+        torch.cuda.synchronize()
+        torch.testing.assert_close(out, eager, atol=0, rtol=0)

@@ -1,0 +1,71 @@
+"""store_kvcache / store_latents on the GPU: bit-exact against the oracle scatter, -1 skipped, HND == NHD, and at
+full config sizes by the size-independent property (written rows equal the inputs, every other byte unchanged)."""
+
+import pytest
+import torch
+
+from lvattn import MI355XAttention
+from lvattn import workloads as W
+from oracle import store as S
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("layout", ["NHD", "HND"])
+def test_store_matches_the_oracle_bit_for_bit(cuda, dtype, layout):
+    heads, dim, bs, blocks = 2, 64, 16, 6
+    gen = torch.Generator().manual_seed(0)
+    key = torch.randn(40, heads, dim, generator=gen).to(dtype)
+    value = torch.randn(40, heads, dim, generator=gen).to(dtype)
+    slots = torch.randperm(blocks * bs, generator=gen)[:40].to(torch.int32)
+    slots[[3, 17, 39]] = -1
+    if layout == "NHD":
+        kc = torch.full((blocks, bs, heads, dim), 7.0, dtype=dtype)
+    else:
+        kc = torch.full((blocks, heads, bs, dim), 7.0, dtype=dtype).transpose(1, 2)
+    vc = kc.clone() if layout == "NHD" else kc.transpose(1, 2).clone().transpose(1, 2)
+    want_k, want_v = kc.clone(), vc.clone()
+    S.store_kvcache(key, value, want_k, want_v, slots)
+    dk, dv = kc.to(cuda), vc.to(cuda)
+    if layout == "HND":  # keep the transposed storage on the device
+        dk = kc.transpose(1, 2).contiguous().to(cuda).transpose(1, 2)
+        dv = vc.transpose(1, 2).contiguous().to(cuda).transpose(1, 2)
+    MI355XAttention(4, dim, 1.0, heads).store_kvcache(key.to(cuda), value.to(cuda), dk, dv, slots.to(cuda))
+    torch.cuda.synchronize()
+    assert torch.equal(dk.cpu(), want_k) and torch.equal(dv.cpu(), want_v)
+
+
+def test_store_latents_skips_negative_slots(cuda):
+    """tests/test_attention_backends.py:439-455."""
+    b = MI355XAttention(16, 128, 1.0, 16)
+    cache = torch.full((2, 64, 576), 7.0, dtype=torch.bfloat16, device=cuda)
+    latent = torch.randn(3, 576, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
+    b.store_latents(latent.to(cuda), cache, torch.tensor([0, -1, 69], dtype=torch.int32, device=cuda))
+    want = torch.full((2, 64, 576), 7.0, dtype=torch.bfloat16)
+    S.store_latents(latent, want, [0, -1, 69])
+    assert torch.equal(cache.cpu(), want)
+
+
+@pytest.mark.parametrize("name", ["qwen3_0_6b_mixed", "qwen3_8b_decode"])
+def test_store_at_config_size(cuda, name):
+    """The step's new K/V into the full pool: written rows equal the inputs; the rest of the pool is untouched."""
+    wl = W.WORKLOADS[name]()
+    t = W.materialize(wl, cuda)
+    ends = wl.context_lens
+    slots = torch.tensor([wl.block_lists[i][(e - n + j) // wl.block_size] * wl.block_size + (e - n + j) % wl.block_size
+                          for i, (e, n) in enumerate(zip(ends, wl.num_new)) for j in range(n)],
+                         dtype=torch.int32, device=cuda)
+    before_k = t.k_cache.view(-1, wl.num_kv_heads, wl.head_dim).sum(dtype=torch.float64, dim=(1, 2))
+    before_v = t.v_cache.view(-1, wl.num_kv_heads, wl.head_dim).sum(dtype=torch.float64, dim=(1, 2))
+    MI355XAttention(wl.num_heads, wl.head_dim, wl.scale, wl.num_kv_heads).store_kvcache(
+        t.k_new, t.v_new, t.k_cache, t.v_cache, slots)
+    torch.cuda.synchronize()
+    flat_k = t.k_cache.view(-1, wl.num_kv_heads, wl.head_dim)
+    flat_v = t.v_cache.view(-1, wl.num_kv_heads, wl.head_dim)
+    assert torch.equal(flat_k[slots.long()], t.k_new) and torch.equal(flat_v[slots.long()], t.v_new)
+    after_k = flat_k.sum(dtype=torch.float64, dim=(1, 2))
+    after_v = flat_v.sum(dtype=torch.float64, dim=(1, 2))
+    other = torch.ones(flat_k.size(0), dtype=torch.bool, device=cuda)
+    other[slots.long()] = False
+    assert torch.equal(after_k[other], before_k[other]) and torch.equal(after_v[other], before_v[other])

@@ -1,0 +1,83 @@
+"""Host logic of the boundary (CPU only): the per-step Context split, backend selection, capability flags."""
+
+import pytest
+import torch
+
+from lvattn import Context, LayerSpec, MI355XAttention, get_attention_backend, split_decodes_and_prefills
+from lvattn.context import get_context, set_context, use_context
+
+BS = 16
+
+
+def host_context(num_cached, num_new, tables):
+    totals = [c + n for c, n in zip(num_cached, num_new)]
+    cu_q = [0, *torch.tensor(num_new).cumsum(0).tolist()]
+    cu_k = [0, *torch.tensor(totals).cumsum(0).tolist()]
+    return Context(
+        is_prefill=True,
+        cu_seqlens_q=torch.tensor(cu_q, dtype=torch.int32),
+        cu_seqlens_k=torch.tensor(cu_k, dtype=torch.int32),
+        max_seqlen_q=max(num_new),
+        max_seqlen_k=max(totals),
+        block_tables=torch.tensor(tables, dtype=torch.int32),
+        cu_seqlens_q_host=cu_q,
+        cu_seqlens_k_host=cu_k,
+        context_lens=torch.tensor(totals, dtype=torch.int32),
+    )
+
+
+def test_the_split_slices_the_leading_one_query_rows():
+    """Known answer of tests/test_attention_backends.py:874-889."""
+    context = host_context([9, 0, 4, 2 * BS], [1, 1, 5, 3], [[0, -1, -1], [1, -1, -1], [2, -1, -1], [3, 4, 5]])
+    n, decodes, prefills = split_decodes_and_prefills(context)
+    assert n == 2
+    assert decodes.context_lens.tolist() == [10, 1]
+    assert decodes.block_tables.tolist() == [[0, -1, -1], [1, -1, -1]]
+    assert prefills.cu_seqlens_q.tolist() == prefills.cu_seqlens_q_host == [0, 5, 8]
+    assert prefills.cu_seqlens_k.tolist() == prefills.cu_seqlens_k_host == [0, 9, 12 + 2 * BS]
+    assert (prefills.max_seqlen_q, prefills.max_seqlen_k) == (5, 3 + 2 * BS)
+    assert prefills.block_tables.tolist() == [[2, -1, -1], [3, 4, 5]]
+    assert split_decodes_and_prefills(context)[1] is decodes  # cached for every layer
+
+
+def test_a_step_split_at_no_row_is_left_whole():
+    """tests/test_attention_backends.py:892-894."""
+    context = host_context([0, 3], [4, 1], [[0], [1]])
+    assert split_decodes_and_prefills(context) == (0, None, context)
+
+
+def test_context_nesting_restores_the_previous_one():
+    outer = get_context()
+    with set_context(True, max_seqlen_q=3) as ctx:
+        assert get_context() is ctx and ctx.is_prefill and ctx.max_seqlen_q == 3
+        inner = Context()
+        with pytest.raises(ValueError):
+            with use_context(inner):
+                assert get_context() is inner
+                raise ValueError
+        assert get_context() is ctx
+    assert get_context() is outer
+
+
+def test_capabilities():
+    b = MI355XAttention
+    assert b.get_name() == "mi355x"
+    assert b.supports_cuda_graph() and b.supports_full_cudagraph() and not b.split_decodes()
+    assert b.get_kv_cache_shape(10, 256, 8, 128) == (10, 256, 8, 128)
+    assert b.validate(LayerSpec(128, 32, 8, torch.bfloat16)) == []
+    assert b.validate(LayerSpec(64, 8, 2, torch.float16)) == []
+    assert "dtype torch.float32" in b.validate(LayerSpec(128, 32, 8, torch.float32))[0]
+    assert "6 query heads do not group over 4 key heads" in b.validate(LayerSpec(128, 6, 4, torch.bfloat16))
+    assert "head size 96 is not supported" in b.validate(LayerSpec(96, 32, 8, torch.bfloat16))
+
+
+def test_selection_rules(monkeypatch):
+    """selector.py:19-39: unknown names raise ValueError; a named backend that cannot serve raises RuntimeError."""
+    monkeypatch.setattr(MI355XAttention, "is_available", staticmethod(lambda: True))
+    monkeypatch.delenv("LEAN_VLLM_ATTENTION_BACKEND", raising=False)
+    assert get_attention_backend(LayerSpec(128, 32, 8, torch.bfloat16)) is MI355XAttention
+    with pytest.raises(ValueError, match="unknown attention backend"):
+        get_attention_backend(LayerSpec(128, 32, 8, torch.bfloat16), name="nope")
+    monkeypatch.setenv("LEAN_VLLM_ATTENTION_BACKEND", "mi355x")
+    with pytest.raises(RuntimeError, match="dtype torch.float32"):
+        get_attention_backend(LayerSpec(128, 32, 8, torch.float32))

@@ -1,0 +1,94 @@
+"""Pins the packing oracle: the reference's known answers, its per-token-loop oracle on random steps, and
+closed-form invariants (CPU only)."""
+
+import random
+
+import numpy as np
+import pytest
+
+from oracle import pack as P
+
+
+def test_known_answer_single_prompt_and_decode():
+    """tests/test_model_runner.py:29-52: a 3-token prompt packs positions [0,1,2]; its next decode step [3]."""
+    got = P.pack_numpy([0], [3], [[0]], block_size=8)
+    assert got["positions"].tolist() == [0, 1, 2]
+    got = P.pack_numpy([3], [1], [[0]], block_size=8)
+    assert got["positions"].tolist() == [3]
+    assert got["cu_seqlens_q_host"] == [0, 1] and got["context_lens"].tolist() == [4]
+
+
+def test_known_answer_one_query_rows_lead_the_batch():
+    """tests/test_model_runner.py:179-195: a decoding row after a prompt in scheduler order leads the batch:
+    positions [2, 0, 1, 2] and cu_seqlens_q_host [0, 1, 4]."""
+    got = P.pack_numpy([0, 2], [3, 1], [[0], [0]], block_size=8)
+    assert got["positions"].tolist() == [2, 0, 1, 2]
+    assert got["cu_seqlens_q_host"] == [0, 1, 4]
+    assert got["order"].tolist() == [1, 0]
+    # closed forms for the rest of the row: both rows end at 3 keys, all in page 0
+    assert got["cu_seqlens_k_host"] == [0, 3, 6]
+    assert got["slot_mapping"].tolist() == [2, 0, 1, 2]
+    assert got["block_tables"].tolist() == [[0], [0]]
+
+
+def test_query_len_is_the_most_common_short_length():
+    """model_runner.py:51-63: most common length <= 1 + drafts, the shorter on ties, else 1."""
+    assert P.decode_query_len(np.array([1, 1, 5, 3])) == 1
+    assert P.decode_query_len(np.array([5, 7])) == 1
+    assert P.decode_query_len(np.array([3, 3, 2, 1]), num_speculative_tokens=2) == 3
+    assert P.decode_query_len(np.array([3, 2]), num_speculative_tokens=2) == 2
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_vectorised_packing_matches_the_per_token_loops(seed):
+    """Twenty random steps of decodes, cold prompts, resumed chunks (every fifth without tables), as the
+    reference checks prepare_batch against reference_batch (tests/test_model_runner.py:557-596)."""
+    rng = random.Random(seed)
+    bs = 8
+    for step in range(20):
+        cached, new, lists = P.random_rows(rng, bs, with_tables=step % 5 != 0)
+        got = P.pack_numpy(cached, new, lists, bs)
+        want = P.pack_loops(cached, new, lists, bs)
+        assert got["order"].tolist() == want["order"]
+        assert got["positions"].tolist() == want["positions"]
+        assert got["slot_mapping"].tolist() == want["slot_mapping"]
+        assert got["cu_seqlens_q"].tolist() == want["cu_seqlens_q"] == got["cu_seqlens_q_host"]
+        assert got["cu_seqlens_k"].tolist() == want["cu_seqlens_k"] == got["cu_seqlens_k_host"]
+        assert got["context_lens"].tolist() == want["context_lens"]
+        assert got["max_seqlen_q"] == max(np.diff(want["cu_seqlens_q"]))
+        assert got["max_seqlen_k"] == max(want["context_lens"])
+        if want["block_tables"] is None:
+            assert got["block_tables"] is None
+        else:
+            assert got["block_tables"].tolist() == want["block_tables"]
+
+
+def test_invariants_on_a_large_random_step():
+    """Each slot lies in its own row's pages at the right offset; cu differences are the lengths."""
+    rng = random.Random(7)
+    bs = 16
+    cached, new, lists = P.random_rows(rng, bs, max_rows=200)
+    got = P.pack_numpy(cached, new, lists, bs)
+    order = got["order"]
+    assert (np.diff(got["cu_seqlens_q"]) == np.asarray(new)[order]).all()
+    assert (np.diff(got["cu_seqlens_k"]) == (np.asarray(cached) + np.asarray(new))[order]).all()
+    t = 0
+    for r, s in enumerate(order):
+        for j in range(new[s]):
+            pos = cached[s] + j
+            assert got["positions"][t] == pos
+            slot = got["slot_mapping"][t]
+            assert slot // bs == lists[s][pos // bs] and slot % bs == pos % bs
+            t += 1
+
+
+def test_a_planted_off_by_one_is_caught():
+    """The loop check discriminates: an oracle with slots one page off disagrees with the loops."""
+    rng = random.Random(3)
+    cached, new, lists = P.random_rows(rng, 8)
+    got = P.pack_numpy(cached, new, lists, 8)
+    want = P.pack_loops(cached, new, lists, 8)
+    shifted = [lists[i][1:] + [0] for i in range(len(lists))]  # page index off by one
+    bad = P.pack_numpy(cached, new, shifted, 8)
+    assert got["slot_mapping"].tolist() == want["slot_mapping"]
+    assert bad["slot_mapping"].tolist() != want["slot_mapping"]
