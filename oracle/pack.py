@@ -109,7 +109,7 @@ def random_rows(rng, block_size: int, with_tables: bool = True, max_rows: int = 
 
     ``rng`` is a ``random.Random``. Returns (num_cached, num_new, block_lists).
     """
-    free = iter(rng.sample(range(pool), 2_000))  # scattered pages, so a wrong lookup shows
+    free = iter(rng.sample(range(pool), min(pool, max(2_000, 12 * max_rows))))  # scattered, so a wrong lookup shows
     num_cached, num_new, lists = [], [], []
     for _ in range(rng.randint(1, max_rows)):
         kind = rng.choice(["decode", "prompt", "chunk"])
