@@ -39,7 +39,23 @@ def parse():
     ap.add_argument("--workload", default="qwen3_8b_mixed")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run a plain device-to-device copy of MIB MiB, 5 times (the reference kernel for "
+                         "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
     return ap.parse_args()
+
+
+def calibrate_copy(mib: int):
+    """A plain copy of known size: each launch reads and writes exactly ``mib`` MiB."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    src = torch.ones(mib << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_per_launch": mib << 20, "launches": 5}), flush=True)
 
 
 def cpu_baseline(wl, t, dec_sample: int = 96):
@@ -120,6 +136,9 @@ def main():
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this path runs on a single GPU)",
               file=sys.stderr)
         sys.exit(2)
+    if args.calibrate_copy:
+        calibrate_copy(args.calibrate_copy)
+        return
     import torch
 
     from lvattn import Context, MI355XAttention, Packer, _capi

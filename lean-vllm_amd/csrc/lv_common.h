@@ -114,6 +114,11 @@ __device__ inline float dpp_mirror(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x140, 0xf, 0xf, false));
 }
 
+// Lane (i + 8) mod 16 of the same 16-lane row.
+__device__ inline float dpp_ror8(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x128, 0xf, 0xf, false));
+}
+
 // Sum over aligned groups of N lanes (N = 4, 8 or 16); every lane of a group ends with the group's sum.
 template <int N>
 __device__ inline float group_sum(float x) {

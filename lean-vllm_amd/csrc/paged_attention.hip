@@ -25,6 +25,22 @@ constexpr int kPrefillKeys = 64;   // keys per prefill tile
 constexpr int kPrefillRows = 64;   // (position, head) query rows per prefill item, 16 per wave
 constexpr int kPlanMaxRows = 4096;  // rows of a step with prompts (the work-list scan lives in LDS)
 
+#ifndef LV_DECODE_PIPE
+#define LV_DECODE_PIPE 2
+#endif
+#ifndef LV_STREAM_NT
+#define LV_STREAM_NT 1
+#endif
+#ifndef LV_SPLIT_TARGET
+#define LV_SPLIT_TARGET 4096
+#endif
+#ifndef LV_MIN_SPLIT
+#define LV_MIN_SPLIT 256
+#endif
+#ifndef LV_HEAD_FASTEST
+#define LV_HEAD_FASTEST 0
+#endif
+
 struct AttnParams {
   const char* q;
   int64_t q_st, q_sh;  // bytes
@@ -54,20 +70,67 @@ __device__ inline int key_len(const AttnParams& p, int row) {
 }
 
 __device__ inline u32x4 ld16(const char* ptr) { return *reinterpret_cast<const u32x4*>(ptr); }
+// Streaming load of cache rows that this launch reads once: the non-temporal hint keeps them from displacing
+// reusable lines in L2 and the Infinity Cache (about 7.0 vs 6.2 TB/s for a plain streaming read on MI355X).
+__device__ inline u32x4 ld16_stream(const char* ptr) {
+#if LV_STREAM_NT
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ptr));
+#else
+  return *reinterpret_cast<const u32x4*>(ptr);
+#endif
+}
 __device__ inline void st16(char* ptr, u32x4 v) { *reinterpret_cast<u32x4*>(ptr) = v; }
 
 // ---------------------------------------------------------------------------------------------------------
 // Decode item.
+//
+// Lane layout (D = 128): 16 lanes hold one token's head row, 16 bytes (8 dims) each; the wave's 4 lane groups take
+// 4 tokens at a time, 4 times per 16-token tile. Scores stay in raw q.k units; the softmax scale (positive) and
+// log2(e) are folded into the exp2 argument. The running max is wave-uniform, so rescaling the accumulators is a
+// uniform branch taken only when a tile raises the max. p.v runs as 2-term dot products over token pairs with p in
+// the 16-bit format of the cache (fp32 accumulation), as the MFMA path does with its probability tiles.
+
+// Sum / max over lanes i and i ^ 16, and over lanes i and i ^ 32, with gfx950's cross-row swaps (no LDS round trip).
+__device__ inline float xor16_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ inline float xor32_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ inline float xor16_max(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float xor32_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// Reduce over the lane groups of a wave that hold different tokens (lanes i, i + LPT, i + 2 LPT, ...).
+template <int LPT>
+__device__ inline float groups_max(float x) {
+  static_assert(LPT == 8 || LPT == 16, "8 or 16 lanes per token");
+  if constexpr (LPT == 8) x = fmaxf(x, dpp_ror8(x));  // lane i and i ^ 8 of each 16-lane row
+  return xor32_max(xor16_max(x));
+}
+template <int LPT>
+__device__ inline float groups_sum(float x) {
+  static_assert(LPT == 8 || LPT == 16, "8 or 16 lanes per token");
+  if constexpr (LPT == 8) x += dpp_ror8(x);
+  return xor32_sum(xor16_sum(x));
+}
 
 template <typename T, int D, int GS>
 __device__ void decode_item(const AttnParams& p, int row, int split, int kvh, int qg, char* smem) {
   using E = Elem<T>;
-  constexpr int LPT = D >= 128 ? 16 : D / 8;  // lanes per token head row
-  constexpr int VPL = D / (LPT * 8);          // 16-byte vectors per lane per row
-  constexpr int EPL = VPL * 8;                // elements per lane
-  constexpr int TPI = 64 / LPT;               // tokens per wave step
-  constexpr int U = kTile / TPI;              // steps per tile
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  static_assert(D == 64 || D == 128, "head_dim 64 or 128");
+  constexpr int LPT = D / 8;      // lanes per token head row, 16 bytes each
+  constexpr int TPI = 64 / LPT;   // tokens per wave step
+  constexpr int U = kTile / TPI;  // steps per 16-token tile
+  static_assert(U % 2 == 0, "token pairs");
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int grp = lane / LPT, part = lane % LPT;
 
   const int lk = key_len(p, row);
@@ -78,102 +141,185 @@ __device__ void decode_item(const AttnParams& p, int row, int split, int kvh, in
   const int nsplit = min((lk + p.split - 1) / p.split, p.max_splits);
   const int tok = p.cu_q ? p.cu_q[row] : row;
   const int head0 = kvh * p.group + qg * GS;
+  const float c = p.scale_log2;
 
-  u32x4 qv[GS][VPL];
+  u32x4 qv[GS];
 #pragma unroll
-  for (int g = 0; g < GS; ++g)
-#pragma unroll
-    for (int v = 0; v < VPL; ++v)
-      qv[g][v] = ld16(p.q + tok * p.q_st + (head0 + g) * p.q_sh + (int64_t)(v * LPT + part) * 16);
+  for (int g = 0; g < GS; ++g) qv[g] = ld16(p.q + tok * p.q_st + (head0 + g) * p.q_sh + part * 16);
 
-  float m[GS], l[GS], acc[GS][EPL];
+  float m[GS], l[GS], acc[GS][8];
 #pragma unroll
   for (int g = 0; g < GS; ++g) {
     m[g] = -INFINITY;
     l[g] = 0.f;
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) acc[g][e] = 0.f;
+    for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
   }
 
+  // Byte offset of this lane's 16 bytes of step u inside a tile (tile rows are p.c_st apart; fits 32 bits).
+  uint32_t loff[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) loff[u] = (uint32_t)((u * TPI + grp) * p.c_st + part * 16);
   const int32_t* table = p.tables + (int64_t)row * p.t_stride;
-  for (int t0 = kbeg + kTile * wave; t0 < kend; t0 += kTile * kWaves) {
-    const int64_t blk = table[t0 / p.bs];
-    const int64_t base = blk * p.c_sb + (int64_t)(t0 % p.bs) * p.c_st + (int64_t)kvh * p.c_sh;
-    u32x4 kv[U][VPL], vv[U][VPL];
+
+  auto tile_base = [&](int t0) {
+    return (int64_t)table[t0 / p.bs] * p.c_sb + (int64_t)(t0 % p.bs) * p.c_st + (int64_t)kvh * p.c_sh;
+  };
+  auto load_rows = [&](const char* cache, int64_t base, u32x4 (&x)[U]) {
+    const char* b = cache + base;
 #pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int v = 0; v < VPL; ++v) {
-        const int64_t off = base + (int64_t)(u * TPI + grp) * p.c_st + (int64_t)(v * LPT + part) * 16;
-        kv[u][v] = ld16(p.k_cache + off);
-        vv[u][v] = ld16(p.v_cache + off);
-      }
+    for (int u = 0; u < U; ++u) x[u] = ld16_stream(b + loff[u]);
+  };
+  // Scores of a tile -> online-softmax update -> probabilities packed in token pairs, per query head.
+  auto qk = [&](int t0, const u32x4 (&kv)[U], uint32_t (&pp)[GS][U / 2]) {
     float s[U][GS];
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
       for (int g = 0; g < GS; ++g) {
-        float d = 0.f;
+        float d = E::dot2(qv[g][0], kv[u][0], 0.f);
 #pragma unroll
-        for (int v = 0; v < VPL; ++v)
-#pragma unroll
-          for (int w = 0; w < 4; ++w) d = E::dot2(qv[g][v][w], kv[u][v][w], d);
-        s[u][g] = group_sum<LPT>(d) * p.scale_log2;
+        for (int w = 1; w < 4; ++w) d = E::dot2(qv[g][w], kv[u][w], d);
+        s[u][g] = group_sum<LPT>(d);
       }
-    // Tokens past the range: no weight, and their (possibly NaN) values must not reach the sums.
+    if (t0 + kTile > kend) {  // wave-uniform: the row's last tile; tokens past it get no weight
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (t0 + u * TPI + grp >= kend) {
+      for (int u = 0; u < U; ++u) {
+        const bool in = t0 + u * TPI + grp < kend;
 #pragma unroll
-        for (int g = 0; g < GS; ++g) s[u][g] = -INFINITY;
+        for (int g = 0; g < GS; ++g) s[u][g] = in ? s[u][g] : -INFINITY;
+      }
+    }
+    float mt[GS];
+    int grow = 0;
 #pragma unroll
-        for (int v = 0; v < VPL; ++v) vv[u][v] = u32x4{0, 0, 0, 0};
+    for (int g = 0; g < GS; ++g) {
+      float x = s[0][g];
+#pragma unroll
+      for (int u = 1; u < U; ++u) x = fmaxf(x, s[u][g]);
+      mt[g] = groups_max<LPT>(x);  // finite: every tile holds a token in range
+      grow |= mt[g] > m[g];
+    }
+    if (__builtin_amdgcn_readfirstlane(grow)) {
+#pragma unroll
+      for (int g = 0; g < GS; ++g) {
+        const float mn = fmaxf(m[g], mt[g]);
+        const float alpha = fast_exp2((m[g] - mn) * c);
+        m[g] = mn;
+        l[g] *= alpha;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[g][e] *= alpha;
       }
     }
 #pragma unroll
     for (int g = 0; g < GS; ++g) {
-      float mx = s[0][g];
+      const float mc = m[g] * c;
 #pragma unroll
-      for (int u = 1; u < U; ++u) mx = fmaxf(mx, s[u][g]);
-#pragma unroll
-      for (int d = LPT; d < 64; d <<= 1) mx = fmaxf(mx, shfl_xor(mx, d));
-      const float mnew = fmaxf(m[g], mx);  // finite: every tile holds at least one token in range
-      const float alpha = fast_exp2(m[g] - mnew);
-      m[g] = mnew;
-      float pu[U];
-      float psum = 0.f;
+      for (int u = 0; u < U; u += 2) {
+        const float p0 = fast_exp2(fmaf(s[u][g], c, -mc));
+        const float p1 = fast_exp2(fmaf(s[u + 1][g], c, -mc));
+        l[g] += p0 + p1;
+        pp[g][u / 2] = E::pack(p0, p1);
+      }
+    }
+  };
+  // acc += p . V over the tile: value rows of token pairs interleaved per dim, 2-term dot products.
+  auto pv = [&](int t0, u32x4 (&vv)[U], const uint32_t (&pp)[GS][U / 2]) {
+    if (t0 + kTile > kend) {  // values past the range may be NaN: zero them (their p is 0)
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        pu[u] = fast_exp2(s[u][g] - mnew);
-        psum += pu[u];
+        const bool in = t0 + u * TPI + grp < kend;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) vv[u][w] = in ? vv[u][w] : 0u;
       }
-      l[g] = l[g] * alpha + psum;
-#pragma unroll
-      for (int v = 0; v < VPL; ++v)
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          float lo = acc[g][v * 8 + 2 * w] * alpha, hi = acc[g][v * 8 + 2 * w + 1] * alpha;
-#pragma unroll
-          for (int u = 0; u < U; ++u) {
-            lo = fmaf(pu[u], E::lo(vv[u][v][w]), lo);
-            hi = fmaf(pu[u], E::hi(vv[u][v][w]), hi);
-          }
-          acc[g][v * 8 + 2 * w] = lo;
-          acc[g][v * 8 + 2 * w + 1] = hi;
-        }
     }
+#pragma unroll
+    for (int u = 0; u < U; u += 2)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t lo = __builtin_amdgcn_perm(vv[u + 1][w], vv[u][w], 0x05040100u);
+        const uint32_t hi = __builtin_amdgcn_perm(vv[u + 1][w], vv[u][w], 0x07060302u);
+#pragma unroll
+        for (int g = 0; g < GS; ++g) {
+          acc[g][2 * w] = E::dot2(pp[g][u / 2], lo, acc[g][2 * w]);
+          acc[g][2 * w + 1] = E::dot2(pp[g][u / 2], hi, acc[g][2 * w + 1]);
+        }
+      }
+  };
+
+  constexpr int kStride = kTile * kWaves;
+  int t0 = kbeg + kTile * wave;
+  if (t0 < kend) {
+#if LV_DECODE_PIPE == 1
+    // Two register buffers: the next tile's loads are in flight while this one is consumed.
+    u32x4 ka[U], va[U], kb[U], vb[U];
+    uint32_t pp[GS][U / 2];
+    int64_t base = tile_base(t0);
+    load_rows(p.k_cache, base, ka);
+    load_rows(p.v_cache, base, va);
+    while (true) {
+      const int t1 = t0 + kStride;
+      if (t1 < kend) {
+        base = tile_base(t1);
+        load_rows(p.k_cache, base, kb);
+        load_rows(p.v_cache, base, vb);
+      }
+      qk(t0, ka, pp);
+      pv(t0, va, pp);
+      if (t1 >= kend) break;
+      const int t2 = t1 + kStride;
+      if (t2 < kend) {
+        base = tile_base(t2);
+        load_rows(p.k_cache, base, ka);
+        load_rows(p.v_cache, base, va);
+      }
+      qk(t1, kb, pp);
+      pv(t1, vb, pp);
+      if (t2 >= kend) break;
+      t0 = t2;
+    }
+#elif LV_DECODE_PIPE == 2
+    // Staggered: the next tile's keys load during this tile's p.v, its values during its own q.k.
+    u32x4 kv[U], vv[U];
+    uint32_t pp[GS][U / 2];
+    int64_t base = tile_base(t0);
+    load_rows(p.k_cache, base, kv);
+    load_rows(p.v_cache, base, vv);
+    while (true) {
+      qk(t0, kv, pp);
+      const int t1 = t0 + kStride;
+      int64_t next = 0;
+      if (t1 < kend) {
+        next = tile_base(t1);
+        load_rows(p.k_cache, next, kv);
+      }
+      pv(t0, vv, pp);
+      if (t1 >= kend) break;
+      load_rows(p.v_cache, next, vv);
+      t0 = t1;
+    }
+#else
+    for (; t0 < kend; t0 += kStride) {
+      u32x4 kv[U], vv[U];
+      uint32_t pp[GS][U / 2];
+      const int64_t base = tile_base(t0);
+      load_rows(p.k_cache, base, kv);
+      load_rows(p.v_cache, base, vv);
+      qk(t0, kv, pp);
+      pv(t0, vv, pp);
+    }
+#endif
   }
 
-  // Sum the token groups of the wave (they share m).
+  // Sum the token groups of the wave (they share m); m moves to the log2 domain of the merges.
 #pragma unroll
   for (int g = 0; g < GS; ++g) {
+    l[g] = groups_sum<LPT>(l[g]);
 #pragma unroll
-    for (int d = LPT; d < 64; d <<= 1) {
-      l[g] += shfl_xor(l[g], d);
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) acc[g][e] += shfl_xor(acc[g][e], d);
-    }
+    for (int e = 0; e < 8; ++e) acc[g][e] = groups_sum<LPT>(acc[g][e]);
+    m[g] *= c;
   }
+  constexpr int VPL = 1;
 
   // Merge the waves through LDS: wm/wl [kWaves][GS], wacc [kWaves][GS][D].
   float* wm = reinterpret_cast<float*>(smem);
@@ -389,16 +535,22 @@ template <typename T, int D, int GS, bool MIXED>
 __global__ __launch_bounds__(256) void paged_attention_kernel(AttnParams p) {
   constexpr int kSmem = MIXED ? SmemBytes<D, GS>::kMixed : SmemBytes<D, GS>::kDecode;
   __shared__ __attribute__((aligned(16))) char smem[kSmem];
-  const int kvh = blockIdx.y / p.qgroups, qg = blockIdx.y % p.qgroups;
+#if LV_HEAD_FASTEST
+  const int ny = p.hkv * p.qgroups;
+  const int by = blockIdx.x % ny, bx = blockIdx.x / ny;
+#else
+  const int by = blockIdx.y, bx = blockIdx.x;
+#endif
+  const int kvh = by / p.qgroups, qg = by % p.qgroups;
   if constexpr (MIXED) {
-    if ((int)blockIdx.x >= *p.n_items) return;
-    const int2 it = p.items[blockIdx.x];
+    if (bx >= *p.n_items) return;
+    const int2 it = p.items[bx];
     if (it.y >= 0)
       decode_item<T, D, GS>(p, it.x, it.y, kvh, qg, smem);
     else if (qg == 0)
       prefill_item<T, D>(p, it.x, -1 - it.y, kvh, smem);
   } else {
-    decode_item<T, D, GS>(p, blockIdx.x / p.max_splits, blockIdx.x % p.max_splits, kvh, qg, smem);
+    decode_item<T, D, GS>(p, bx / p.max_splits, bx % p.max_splits, kvh, qg, smem);
   }
 }
 
@@ -492,8 +644,8 @@ static Shape plan_shape(int32_t rows, int32_t tokens, int32_t hq, int32_t hkv, i
   const int64_t units = (int64_t)rows * hkv * (group / s.gs);
   const int64_t keys = max_k > 0 ? max_k : 1;
   // Keys per decode item: enough items to fill the chip several times over, at least 256 keys each.
-  const int64_t target = 8192;
-  int64_t split = 256;
+  const int64_t target = LV_SPLIT_TARGET;
+  int64_t split = LV_MIN_SPLIT;
   while (split < keys && units * ((keys + split - 1) / split) > target) split *= 2;
   s.split = (int32_t)split;
   s.max_splits = (int32_t)((keys + split - 1) / split);
@@ -517,7 +669,11 @@ static Shape plan_shape(int32_t rows, int32_t tokens, int32_t hq, int32_t hkv, i
 
 template <typename T, int D, int GS>
 static void launch(const AttnParams& p, bool mixed, int grid_x, hipStream_t stream) {
+#if LV_HEAD_FASTEST
+  const dim3 grid(grid_x * p.hkv * p.qgroups, 1);
+#else
   const dim3 grid(grid_x, p.hkv * p.qgroups);
+#endif
   if (mixed)
     hipLaunchKernelGGL((paged_attention_kernel<T, D, GS, true>), grid, dim3(256), 0, stream, p);
   else
@@ -584,6 +740,10 @@ extern "C" int lv_paged_attention(const void* q, int64_t q_stride_t, int64_t q_s
                  (out_stride_h * 2) % 16 == 0 && (cache_stride_block * 2) % 16 == 0 &&
                  (cache_stride_token * 2) % 16 == 0 && (cache_stride_head * 2) % 16 == 0,
              "paged_attention: tensors and their strides must be 16-byte aligned");
+  // A decode lane addresses its rows inside a 16-token tile with 32-bit byte offsets.
+  LV_REQUIRE(cache_stride_token >= 0 && (int64_t)kTile * cache_stride_token * 2 < (int64_t)1 << 30,
+             "paged_attention: cache token stride %lld is negative or too large", (long long)cache_stride_token);
+  LV_REQUIRE(scale > 0.f, "paged_attention: the softmax scale must be positive, got %g", (double)scale);
   const bool mixed = cu_seqlens_q != nullptr && max_seqlen_q > 1;
   LV_REQUIRE(!mixed || num_rows <= kPlanMaxRows, "paged_attention: a step with prompts holds at most %d rows, got %d",
              kPlanMaxRows, num_rows);
