@@ -101,6 +101,29 @@ int lv_paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h, co
                        void* workspace, size_t workspace_bytes, int32_t dtype, void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------
+ * MLA absorbed decode. Replaces AttentionBackend.mla_decode (lean_vllm/attention/abstract.py:206-219; math of
+ * TorchAttention.mla_decode, lean_vllm/attention/torch_backend.py:105-119; FlashMLA in the FlashMLA backend,
+ * lean_vllm/attention/flashmla_backend.py:52-68).
+ *
+ * Each of num_rows rows has queries_per_row queries, its last positions: query j of a row with L = context_lens[b]
+ * cached latents sees latents 0 .. L - queries_per_row + j. The latents are one key head shared by all num_heads
+ * query heads; the values are their leading v_dim entries.
+ * q: [num_rows * queries_per_row, num_heads, latent_dim] (strides q_stride_t, q_stride_h; unit dim stride), row b's
+ * queries consecutive. latent_cache: [blocks, block_size, latent_dim] with block stride cache_stride_block and token
+ * stride cache_stride_token (elements), unit dim stride. block_tables: [num_rows, *] int32, row stride table_stride.
+ * out: [num_rows * queries_per_row, num_heads, v_dim]. latent_dim must be 576 and v_dim 512 (DeepSeek's
+ * kv_lora_rank 512 + rope 64). max_seqlen_k bounds every row's latent count and sizes the split grid.
+ * workspace: at least lv_mla_decode_workspace_bytes(...) bytes for the same arguments; no initialisation needed. */
+size_t lv_mla_decode_workspace_bytes(int32_t num_rows, int32_t queries_per_row, int32_t num_heads,
+                                     int32_t max_seqlen_k);
+int lv_mla_decode(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* latent_cache,
+                  int64_t cache_stride_block, int64_t cache_stride_token, int32_t block_size,
+                  const int32_t* block_tables, int64_t table_stride, const int32_t* context_lens, int32_t num_rows,
+                  int32_t queries_per_row, int32_t num_heads, int32_t latent_dim, int32_t v_dim, float scale,
+                  int32_t max_seqlen_k, void* out, int64_t out_stride_t, int64_t out_stride_h, void* workspace,
+                  size_t workspace_bytes, int32_t dtype, void* stream);
+
+/* ---------------------------------------------------------------------------------------------------------
  * Merge two partial attentions over disjoint key sets by log-sum-exp. Replaces merge_attention_
  * (lean_vllm/attention/merge.py:18-28; Triton merge_attn_states_kernel, lean_vllm/attention/triton_merge.py:14-82).
  * o_*: [T, H, D] (unit dim stride, own token/head strides), lse_*: [T, H] fp32 natural log (own strides).

@@ -1,0 +1,344 @@
+// MLA absorbed decode on gfx950: each row's last queries attend its paged latents as one key head shared by all
+// query heads; values are the latents' leading v_dim entries.
+//
+// Math of TorchAttention.mla_decode (lean_vllm/attention/torch_backend.py:105-119), called by
+// MLAAttention._decode_latents (lean_vllm/layers/attention.py:319-335) with q = [q_nope W_UK_T | q_pe] of width
+// 576 (kv_lora_rank 512 + rope 64) and v_dim 512: query j of a row with lq queries and L cached latents sees
+// latents 0 .. L - lq + j.
+//
+// Work item = (row, query, 16-head tile, split of the row's latents); one workgroup of 4 waves. Per iteration a
+// 32-latent tile (36 KB) is staged row-major in LDS while the next tile's loads are in flight in registers.
+//   S^T = Lat Q^T     (32 latents x 16 heads, K = 576) on MFMA 16x16x32: wave (token half th, k half kh) takes
+//                     9 k-steps of one 16-latent half; the two k halves are summed through LDS.
+//   online softmax    per head over the tile; every wave holds the same P^T.
+//   O^T += V^T P^T    (512 dims x 16 heads, K = 32 latents) on MFMA 16x16x32: wave w owns dims [128 w, 128 w + 128).
+//                     V^T operands come from the row-major tile by gfx950's transposing LDS read (ds_read_b64_tr_b16).
+// Rows whose latents were split are combined by log-sum-exp in mla_merge_kernel.
+#include "lv_common.h"
+
+namespace lv {
+
+constexpr int kLatent = 576;              // latent width served: kv_lora_rank 512 + rope 64
+constexpr int kVDim = 512;                // value width: the latents' leading entries
+constexpr int kMlaTile = 32;              // latents per iteration
+constexpr int kMlaPitch = kLatent + 8;    // LDS row pitch in elements (1168 bytes): conflict-free operand reads
+constexpr int kLatChunks = kLatent / 8;   // 16-byte chunks per latent row
+constexpr int kMlaKHalf = kLatent / 64;   // MFMA k-steps (32 wide) per k half: 9
+constexpr int kStageLoads = kMlaTile * kLatChunks / 256;  // 16-byte chunks each thread stages per tile: 9
+static_assert(kMlaTile * kLatChunks % 256 == 0, "tile chunks split evenly over 256 threads");
+
+#ifndef LV_MLA_SPLIT_TARGET
+#define LV_MLA_SPLIT_TARGET 4096
+#endif
+
+struct MlaParams {
+  const char* q;
+  int64_t q_st, q_sh;  // bytes
+  const char* cache;
+  int64_t c_sb, c_st;  // bytes
+  int32_t bs;
+  const int32_t* tables;
+  int64_t t_stride;  // elements
+  const int32_t* lens;
+  int32_t rows, lq, heads, htiles;
+  float scale_log2;
+  char* out;
+  int64_t o_st, o_sh;  // bytes
+  int32_t split, max_splits;
+  float* part_o;    // [rows * lq][heads][max_splits][kVDim]
+  float* part_lse;  // [rows * lq][heads][max_splits], log2 domain
+};
+
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+// Column (lane % 16) of the 4 x 16 tile of 16-bit values whose rows the 16 lanes of the group address, 4
+// consecutive elements per lane (lane = 4 * row + column quad).
+__device__ inline u32x2 lds_read_tr16(const uint16_t* p) {
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+  return __builtin_bit_cast(u32x2, v);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
+  using E = Elem<T>;
+  __shared__ __attribute__((aligned(16))) uint16_t lat[kMlaTile * kMlaPitch];
+  __shared__ __attribute__((aligned(16))) f32x4 spart[4][64];
+  const int row = blockIdx.x / p.max_splits, split = blockIdx.x % p.max_splits;
+  const int qj = blockIdx.y / p.htiles, ht = blockIdx.y % p.htiles;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 15, g = lane >> 4;
+
+  const int lk = p.lens[row] - p.lq + qj + 1;  // latents this query sees
+  const int kbeg = split * p.split;
+  if ((split > 0 && kbeg >= lk) || split >= p.max_splits) return;
+  const int kend = min(lk, kbeg + p.split);
+  const int nsplit = lk > 0 ? min((lk + p.split - 1) / p.split, p.max_splits) : 0;
+  const int tokq = row * p.lq + qj;
+  const int head = ht * 16 + n;  // the head of this lane's S / O columns
+  const bool hvalid = head < p.heads;
+  const float c = p.scale_log2;
+
+  // Q^T operand for this wave's k half: lane holds dims 32 s + 8 g .. + 7 of head n.
+  const int th = wave >> 1, kh = wave & 1;
+  u32x4 qb[kMlaKHalf];
+  {
+    const char* qrow = p.q + tokq * p.q_st + (int64_t)head * p.q_sh;
+#pragma unroll
+    for (int s = 0; s < kMlaKHalf; ++s)
+      qb[s] = hvalid ? ld16(qrow + (int64_t)(32 * (kMlaKHalf * kh + s) + 8 * g) * 2) : u32x4{0, 0, 0, 0};
+  }
+
+  float m = -INFINITY, lsum = 0.f;
+  f32x4 o[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) o[j] = f32x4{0, 0, 0, 0};
+
+  const int32_t* table = p.tables + (int64_t)row * p.t_stride;
+  // Latents past the range are staged as zeros: their weight is 0 and 0 * NaN must not happen.
+  auto fetch = [&](int t0, u32x4 (&st)[kStageLoads]) {
+#pragma unroll
+    for (int i = 0; i < kStageLoads; ++i) {
+      const int ch = tid + 256 * i;
+      const int tt = ch / kLatChunks, part = ch - tt * kLatChunks;
+      const int tok = t0 + tt;
+      u32x4 v = {0, 0, 0, 0};
+      if (tok < kend) {
+        const int64_t off = (int64_t)table[tok / p.bs] * p.c_sb + (int64_t)(tok % p.bs) * p.c_st + part * 16;
+        v = ld16_stream(p.cache + off);
+      }
+      st[i] = v;
+    }
+  };
+  auto stash = [&](const u32x4 (&st)[kStageLoads]) {
+#pragma unroll
+    for (int i = 0; i < kStageLoads; ++i) {
+      const int ch = tid + 256 * i;
+      const int tt = ch / kLatChunks, part = ch - tt * kLatChunks;
+      *reinterpret_cast<u32x4*>(lat + tt * kMlaPitch + part * 8) = st[i];
+    }
+  };
+
+  const int ntiles = kend > kbeg ? (kend - kbeg + kMlaTile - 1) / kMlaTile : 0;
+  u32x4 st[kStageLoads];
+  if (ntiles > 0) fetch(kbeg, st);
+  for (int it = 0; it < ntiles; ++it) {
+    const int t0 = kbeg + it * kMlaTile;
+    __syncthreads();  // the previous tile's LDS reads are done
+    stash(st);
+    __syncthreads();
+    if (it + 1 < ntiles) fetch(t0 + kMlaTile, st);
+
+    // Partial S^T over this wave's k half: lane holds latents 16 th + 4 g + r of head n.
+    f32x4 sacc = {0, 0, 0, 0};
+    const uint16_t* arow = lat + (16 * th + n) * kMlaPitch + 8 * g;
+#pragma unroll
+    for (int s = 0; s < kMlaKHalf; ++s) {
+      const u32x4 a = *reinterpret_cast<const u32x4*>(arow + 32 * (kMlaKHalf * kh + s));
+      sacc = E::mfma16x16x32(a, qb[s], sacc);
+    }
+    spart[wave][lane] = sacc;
+    __syncthreads();
+    f32x4 s0 = spart[0][lane] + spart[1][lane];  // latents t0 + 4 g + r
+    f32x4 s1 = spart[2][lane] + spart[3][lane];  // latents t0 + 16 + 4 g + r
+    if (t0 + kMlaTile > kend) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        s0[r] = t0 + 4 * g + r < kend ? s0[r] : -INFINITY;
+        s1[r] = t0 + 16 + 4 * g + r < kend ? s1[r] : -INFINITY;
+      }
+    }
+    float mx = fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])), fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3])));
+    mx = xor32_max(xor16_max(mx));  // over the 32 latents of head n (finite: the tile holds one in range)
+    const float mn = fmaxf(m, mx);
+    const float alpha = fast_exp2((m - mn) * c);
+    m = mn;
+    const float mc = m * c;
+    float pr[8];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      pr[r] = fast_exp2(fmaf(s0[r], c, -mc));
+      pr[4 + r] = fast_exp2(fmaf(s1[r], c, -mc));
+    }
+    float ps = 0.f;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) ps += pr[r];
+    lsum = lsum * alpha + ps;
+    // P^T operand: k slots 8 g .. 8 g + 7 = latents 4 g + 0..3, then 16 + 4 g + 0..3, of head n.
+    const u32x4 pb = {E::pack(pr[0], pr[1]), E::pack(pr[2], pr[3]), E::pack(pr[4], pr[5]), E::pack(pr[6], pr[7])};
+
+    // O^T tiles of this wave's dims: V^T operand rows (dims) 128 w + 16 j + n, k slots as pb.
+    const uint16_t* v0 = lat + (4 * g + (n >> 2)) * kMlaPitch + 128 * wave + 4 * (n & 3);
+    const uint16_t* v1 = v0 + 16 * kMlaPitch;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const u32x2 lo = lds_read_tr16(v0 + 16 * j);
+      const u32x2 hi = lds_read_tr16(v1 + 16 * j);
+      o[j] = o[j] * alpha;
+      o[j] = E::mfma16x16x32(u32x4{lo[0], lo[1], hi[0], hi[1]}, pb, o[j]);
+    }
+  }
+
+  // Row sums of head n: each lane summed its own latents; add the four lane groups.
+  lsum = xor32_sum(xor16_sum(lsum));
+  if (!hvalid) return;
+  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+  if (nsplit <= 1) {
+    char* dst = p.out + tokq * p.o_st + (int64_t)head * p.o_sh;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int d = 128 * wave + 16 * j + 4 * g;
+      const u32x2 v = {E::pack(o[j][0] * inv, o[j][1] * inv), E::pack(o[j][2] * inv, o[j][3] * inv)};
+      *reinterpret_cast<u32x2*>(dst + d * 2) = v;
+    }
+  } else {
+    const int64_t slot = ((int64_t)tokq * p.heads + head) * p.max_splits + split;
+    float* dst = p.part_o + slot * kVDim;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int d = 128 * wave + 16 * j + 4 * g;
+      *reinterpret_cast<f32x4*>(dst + d) = o[j] * inv;
+    }
+    if (wave == 0 && g == 0) p.part_lse[slot] = lsum > 0.f ? m * c + fast_log2(lsum) : -INFINITY;
+  }
+}
+
+// Combine a split query's partials: o = sum_s 2^(lse_s - M) o_s / sum_s 2^(lse_s - M).
+template <typename T>
+__global__ __launch_bounds__(64) void mla_merge_kernel(MlaParams p) {
+  using E = Elem<T>;
+  const int tokq = blockIdx.x, head = blockIdx.y, lane = threadIdx.x;
+  const int row = tokq / p.lq, qj = tokq - row * p.lq;
+  const int lk = p.lens[row] - p.lq + qj + 1;
+  const int nsplit = lk > 0 ? min((lk + p.split - 1) / p.split, p.max_splits) : 0;
+  if (nsplit <= 1) return;
+  const int64_t slot0 = ((int64_t)tokq * p.heads + head) * p.max_splits;
+  float mmax = -INFINITY;
+  for (int s = 0; s < nsplit; ++s) mmax = fmaxf(mmax, p.part_lse[slot0 + s]);
+  constexpr int PER = kVDim / 64;
+  float o[PER];
+#pragma unroll
+  for (int e = 0; e < PER; ++e) o[e] = 0.f;
+  float den = 0.f;
+  if (mmax != -INFINITY) {
+    for (int s = 0; s < nsplit; ++s) {
+      const float w = fast_exp2(p.part_lse[slot0 + s] - mmax);
+      den += w;
+      const f32x4* src = reinterpret_cast<const f32x4*>(p.part_o + (slot0 + s) * kVDim + lane * PER);
+#pragma unroll
+      for (int e = 0; e < PER / 4; ++e) {
+        const f32x4 x = src[e];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[4 * e + r] = fmaf(w, x[r], o[4 * e + r]);
+      }
+    }
+  }
+  const float inv = den > 0.f ? 1.f / den : 0.f;
+  u32x4 packed;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) packed[w] = E::pack(o[2 * w] * inv, o[2 * w + 1] * inv);
+  *reinterpret_cast<u32x4*>(p.out + tokq * p.o_st + (int64_t)head * p.o_sh + lane * PER * 2) = packed;
+}
+
+struct MlaShape {
+  int32_t split, max_splits;
+  size_t lse_off, o_off, bytes;
+};
+
+static MlaShape mla_shape(int32_t rows, int32_t lq, int32_t heads, int32_t max_k) {
+  MlaShape s{};
+  const int64_t units = (int64_t)rows * lq * ((heads + 15) / 16);
+  const int64_t keys = max_k > 0 ? max_k : 1;
+  int64_t split = 256;
+  while (split < keys && units * ((keys + split - 1) / split) > LV_MLA_SPLIT_TARGET) split *= 2;
+  s.split = (int32_t)split;
+  s.max_splits = (int32_t)((keys + split - 1) / split);
+  const size_t parts = s.max_splits > 1 ? (size_t)rows * lq * heads * s.max_splits : 0;
+  s.lse_off = 0;
+  s.o_off = (parts * sizeof(float) + 255) / 256 * 256;
+  s.bytes = s.o_off + parts * kVDim * sizeof(float);
+  return s;
+}
+
+}  // namespace lv
+
+using namespace lv;
+
+extern "C" size_t lv_mla_decode_workspace_bytes(int32_t num_rows, int32_t queries_per_row, int32_t num_heads,
+                                                int32_t max_seqlen_k) {
+  if (num_rows <= 0 || queries_per_row <= 0 || num_heads <= 0) return 0;
+  return mla_shape(num_rows, queries_per_row, num_heads, max_seqlen_k).bytes;
+}
+
+extern "C" int lv_mla_decode(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* latent_cache,
+                             int64_t cache_stride_block, int64_t cache_stride_token, int32_t block_size,
+                             const int32_t* block_tables, int64_t table_stride, const int32_t* context_lens,
+                             int32_t num_rows, int32_t queries_per_row, int32_t num_heads, int32_t latent_dim,
+                             int32_t v_dim, float scale, int32_t max_seqlen_k, void* out, int64_t out_stride_t,
+                             int64_t out_stride_h, void* workspace, size_t workspace_bytes, int32_t dtype,
+                             void* stream) {
+  LV_REQUIRE(dtype == LV_DTYPE_BF16 || dtype == LV_DTYPE_F16, "mla_decode: dtype %d is not bf16 or fp16", dtype);
+  LV_REQUIRE(num_rows >= 0 && queries_per_row > 0 && num_heads > 0, "mla_decode: bad sizes B=%d Lq=%d H=%d",
+             num_rows, queries_per_row, num_heads);
+  LV_REQUIRE(latent_dim == kLatent && v_dim == kVDim, "mla_decode: latent %d / values %d; %d / %d are served",
+             latent_dim, v_dim, kLatent, kVDim);
+  if (num_rows == 0) return LV_OK;
+  LV_REQUIRE(block_size > 0, "mla_decode: block_size must be positive, got %d", block_size);
+  LV_REQUIRE(q && latent_cache && block_tables && context_lens && out, "mla_decode: null tensor pointer");
+  LV_REQUIRE(max_seqlen_k >= 0, "mla_decode: negative max_seqlen_k");
+  LV_REQUIRE(scale > 0.f, "mla_decode: the softmax scale must be positive, got %g", (double)scale);
+  LV_REQUIRE(aligned(q, 16) && aligned(out, 16) && aligned(latent_cache, 16) && (q_stride_t * 2) % 16 == 0 &&
+                 (q_stride_h * 2) % 16 == 0 && (out_stride_t * 2) % 16 == 0 && (out_stride_h * 2) % 16 == 0 &&
+                 (cache_stride_block * 2) % 16 == 0 && (cache_stride_token * 2) % 16 == 0,
+             "mla_decode: tensors and their strides must be 16-byte aligned");
+  const MlaShape s = mla_shape(num_rows, queries_per_row, num_heads, max_seqlen_k);
+  LV_REQUIRE(workspace_bytes >= s.bytes && (s.bytes == 0 || workspace),
+             "mla_decode: workspace of %zu bytes given, %zu needed", workspace_bytes, s.bytes);
+  LV_REQUIRE(aligned(workspace, 256), "mla_decode: workspace must be 256-byte aligned");
+  LV_REQUIRE((int64_t)num_rows * s.max_splits < ((int64_t)1 << 31) &&
+                 (int64_t)queries_per_row * ((num_heads + 15) / 16) < 65536,
+             "mla_decode: launch grid too large");
+
+  MlaParams p{};
+  p.q = (const char*)q;
+  p.q_st = q_stride_t * 2;
+  p.q_sh = q_stride_h * 2;
+  p.cache = (const char*)latent_cache;
+  p.c_sb = cache_stride_block * 2;
+  p.c_st = cache_stride_token * 2;
+  p.bs = block_size;
+  p.tables = block_tables;
+  p.t_stride = table_stride;
+  p.lens = context_lens;
+  p.rows = num_rows;
+  p.lq = queries_per_row;
+  p.heads = num_heads;
+  p.htiles = (num_heads + 15) / 16;
+  p.scale_log2 = scale * kLog2e;
+  p.out = (char*)out;
+  p.o_st = out_stride_t * 2;
+  p.o_sh = out_stride_h * 2;
+  p.split = s.split;
+  p.max_splits = s.max_splits;
+  char* ws = (char*)workspace;
+  p.part_lse = s.max_splits > 1 ? reinterpret_cast<float*>(ws + s.lse_off) : nullptr;
+  p.part_o = s.max_splits > 1 ? reinterpret_cast<float*>(ws + s.o_off) : nullptr;
+
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid(num_rows * s.max_splits, queries_per_row * p.htiles);
+  if (dtype == LV_DTYPE_BF16)
+    hipLaunchKernelGGL(mla_decode_kernel<BF16>, grid, dim3(256), 0, st, p);
+  else
+    hipLaunchKernelGGL(mla_decode_kernel<F16>, grid, dim3(256), 0, st, p);
+  LV_LAUNCH_CHECK("mla_decode_kernel");
+  if (s.max_splits > 1) {
+    const dim3 mgrid(num_rows * queries_per_row, num_heads);
+    if (dtype == LV_DTYPE_BF16)
+      hipLaunchKernelGGL(mla_merge_kernel<BF16>, mgrid, dim3(64), 0, st, p);
+    else
+      hipLaunchKernelGGL(mla_merge_kernel<F16>, mgrid, dim3(64), 0, st, p);
+    LV_LAUNCH_CHECK("mla_merge_kernel");
+  }
+  return LV_OK;
+}

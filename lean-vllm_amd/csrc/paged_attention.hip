@@ -28,9 +28,6 @@ constexpr int kPlanMaxRows = 4096;  // rows of a step with prompts (the work-lis
 #ifndef LV_DECODE_PIPE
 #define LV_DECODE_PIPE 2
 #endif
-#ifndef LV_STREAM_NT
-#define LV_STREAM_NT 1
-#endif
 #ifndef LV_SPLIT_TARGET
 #define LV_SPLIT_TARGET 4096
 #endif
@@ -69,17 +66,6 @@ __device__ inline int key_len(const AttnParams& p, int row) {
   return p.lens_k ? p.lens_k[row] : p.cu_k[row + 1] - p.cu_k[row];
 }
 
-__device__ inline u32x4 ld16(const char* ptr) { return *reinterpret_cast<const u32x4*>(ptr); }
-// Streaming load of cache rows that this launch reads once: the non-temporal hint keeps them from displacing
-// reusable lines in L2 and the Infinity Cache (about 7.0 vs 6.2 TB/s for a plain streaming read on MI355X).
-__device__ inline u32x4 ld16_stream(const char* ptr) {
-#if LV_STREAM_NT
-  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ptr));
-#else
-  return *reinterpret_cast<const u32x4*>(ptr);
-#endif
-}
-__device__ inline void st16(char* ptr, u32x4 v) { *reinterpret_cast<u32x4*>(ptr) = v; }
 
 // ---------------------------------------------------------------------------------------------------------
 // Decode item.
@@ -90,23 +76,6 @@ __device__ inline void st16(char* ptr, u32x4 v) { *reinterpret_cast<u32x4*>(ptr)
 // uniform branch taken only when a tile raises the max. p.v runs as 2-term dot products over token pairs with p in
 // the 16-bit format of the cache (fp32 accumulation), as the MFMA path does with its probability tiles.
 
-// Sum / max over lanes i and i ^ 16, and over lanes i and i ^ 32, with gfx950's cross-row swaps (no LDS round trip).
-__device__ inline float xor16_sum(float x) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-__device__ inline float xor32_sum(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-__device__ inline float xor16_max(float x) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ inline float xor32_max(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
 // Reduce over the lane groups of a wave that hold different tokens (lanes i, i + LPT, i + 2 LPT, ...).
 template <int LPT>
 __device__ inline float groups_max(float x) {

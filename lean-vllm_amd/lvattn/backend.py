@@ -89,7 +89,7 @@ class MI355XAttention(AttentionBackend):
 
     @staticmethod
     def supports_mla_decode() -> bool:
-        return False
+        return True
 
     @staticmethod
     def mla_block_size() -> int | None:
@@ -163,3 +163,30 @@ class MI355XAttention(AttentionBackend):
         return self._attend(q, k_cache, v_cache, out, block_tables=bt, cu_seqlens_q=cu_q.to(torch.int32),
                             seqlens_k=None, cu_seqlens_k=cu_k.to(torch.int32), rows=cu_q.numel() - 1,
                             max_seqlen_q=max_q, max_seqlen_k=max_k)
+
+    def mla_decode(self, q, latent_cache, v_dim, context: Context):
+        """Each row's last ``Lq`` queries against its paged latents, read as one key head shared by every query
+        head; values are the latents' first ``v_dim`` entries (``abstract.py:206-219``). q ``[B * Lq, H, 576]``,
+        latent_cache ``[N, bs, 576]`` -> ``[B * Lq, H, v_dim]``. Nothing is read back: ``Lq`` comes from the
+        shapes and the split-K grid from the block-table width."""
+        bt, lens = context.block_tables, context.context_lens
+        assert bt is not None and lens is not None and bt.dtype == torch.int32 and bt.stride(-1) == 1
+        lens = lens if lens.dtype == torch.int32 else lens.to(torch.int32)
+        if latent_cache.dim() == 4:  # [1, N, bs, latent] as MLA layers allocate it
+            latent_cache = latent_cache[0]
+        assert q.dtype in _capi.DTYPES and latent_cache.dtype == q.dtype
+        assert q.stride(-1) == 1 and latent_cache.stride(-1) == 1
+        rows = lens.numel()
+        tokens, heads, dim = q.shape
+        assert tokens % rows == 0, "every row has the same number of queries"
+        lq = tokens // rows
+        max_k = bt.size(1) * latent_cache.size(1)
+        out = torch.empty(tokens, heads, v_dim, dtype=q.dtype, device=q.device)
+        nbytes = _capi.query("lv_mla_decode_workspace_bytes", rows, lq, heads, max_k)
+        ws = _WORKSPACE.get(q.device, nbytes)
+        _capi.call("lv_mla_decode", q.data_ptr(), q.stride(0), q.stride(1), latent_cache.data_ptr(),
+                   latent_cache.stride(0), latent_cache.stride(1), latent_cache.size(1), bt.data_ptr(), bt.stride(0),
+                   lens.data_ptr(), rows, lq, heads, dim, v_dim, float(self.scale), max_k, out.data_ptr(),
+                   out.stride(0), out.stride(1), _capi.ptr(ws), 0 if ws is None else ws.numel(),
+                   _capi.DTYPES[q.dtype], _capi.stream_of(q.device))
+        return out

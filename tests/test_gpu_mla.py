@@ -1,0 +1,112 @@
+"""MLA absorbed decode on the GPU against the oracle, through the C ABI.
+
+Cases of the reference's check_mla_decode (tests/test_attention_backends.py:378-436): 8 heads, 576-wide latents
+whose first 512 entries are the values, scale 0.137, pages of 16 and 64 tokens; mid-page, part-page and full rows;
+rows long enough to be split over their latents beside a one-latent row; four queries per row (a row verifying
+drafts). The expected output is the textbook dense attention of each row (fp32). Tolerances: fp16 6e-3 (the
+reference's), bf16 2e-2 absolute / 1e-2 relative (the path's stated bar). At DeepSeek-V2-Lite's full decode
+shape (16 heads, 128 rows, context U[1024, 16384], 64-token pages) a sample of rows, the shortest and longest
+among them, is checked against the oracle's TorchAttention restatement.
+"""
+
+import math
+
+import pytest
+import torch
+
+from helpers import slots_for
+from lvattn import Context, MI355XAttention
+from lvattn import workloads as W
+from oracle import attention as A
+
+pytestmark = pytest.mark.gpu
+
+HEADS, LATENT, VDIM, SCALE = 8, 576, 512, 0.137
+TOL = {torch.float16: dict(atol=6e-3, rtol=6e-3), torch.bfloat16: dict(atol=2e-2, rtol=1e-2)}
+
+
+def check_mla(device, dtype, block_size, context_lens, tables, queries=1, heads=HEADS, seed=0):
+    gen = torch.Generator().manual_seed(seed)
+    nblocks = max(max(t) for t in tables) + 1
+    cache = torch.zeros(nblocks, block_size, LATENT, dtype=dtype)
+    latents = [torch.randn(n, LATENT, generator=gen).to(dtype) for n in context_lens]
+    for lat, table in zip(latents, tables):
+        slots = torch.tensor(slots_for(table, block_size, 0, lat.size(0)))
+        cache.view(-1, LATENT)[slots] = lat
+    q = torch.randn(len(context_lens) * queries, heads, LATENT, generator=gen).to(dtype)
+    ctx = Context(context_lens=torch.tensor(context_lens, dtype=torch.int32, device=device),
+                  block_tables=torch.tensor(tables, dtype=torch.int32, device=device))
+    out = MI355XAttention(heads, LATENT, SCALE, heads).mla_decode(q.to(device), cache.to(device), VDIM, ctx)
+    torch.cuda.synchronize()
+    want = torch.cat([
+        (A.dense_scores(q[i * queries:(i + 1) * queries], lat.unsqueeze(1), SCALE).softmax(-1)
+         @ lat[:, :VDIM].float()).transpose(0, 1)
+        for i, lat in enumerate(latents)])
+    assert out.shape == (len(context_lens) * queries, heads, VDIM) and out.dtype == dtype
+    torch.testing.assert_close(out.float().cpu(), want, **TOL[dtype])
+
+
+CASES = [(dtype, bs) for dtype in (torch.float16, torch.bfloat16) for bs in (16, 64)]
+IDS = [f"{'fp16' if d == torch.float16 else 'bf16'}-bs{bs}" for d, bs in CASES]
+
+
+@pytest.mark.parametrize("dtype, bs", CASES, ids=IDS)
+def test_mla_decode(cuda, dtype, bs):
+    check_mla(cuda, dtype, bs, [bs + 3, 3, 2 * bs], [[2, 0], [3, -1], [1, 4]])
+
+
+@pytest.mark.parametrize("dtype, bs", CASES, ids=IDS)
+def test_mla_decode_of_long_rows(cuda, dtype, bs):
+    pages = torch.randperm(32, generator=torch.Generator().manual_seed(3)).tolist()
+    check_mla(cuda, dtype, bs, [21 * bs - 5, 1, 9 * bs + 1],
+              [pages[:21], pages[21:22] + [-1] * 20, pages[22:] + [-1] * 11])
+
+
+@pytest.mark.parametrize("dtype, bs", CASES, ids=IDS)
+def test_mla_decode_of_rows_verifying_drafts(cuda, dtype, bs):
+    check_mla(cuda, dtype, bs, [bs + 3, 4, 2 * bs], [[2, 0], [3, -1], [1, 4]], queries=4)
+
+
+@pytest.mark.parametrize("heads", [16, 20, 32])
+def test_mla_decode_over_several_head_tiles(cuda, heads):
+    """16 heads fill one MFMA tile; 20 and 32 take two, the last one partly empty for 20."""
+    check_mla(cuda, torch.bfloat16, 64, [700, 65, 3000], [list(range(0, 11)) + [-1] * 36, [11, 12] + [-1] * 45,
+                                                         list(range(13, 60))], heads=heads)
+
+
+def test_mla_rows_with_no_latents_give_zeros(cuda):
+    b = MI355XAttention(16, LATENT, SCALE, 16)
+    cache = torch.randn(2, 64, LATENT, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).to(cuda)
+    q = torch.randn(2, 16, LATENT, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16).to(cuda)
+    ctx = Context(context_lens=torch.tensor([0, 5], dtype=torch.int32, device=cuda),
+                  block_tables=torch.tensor([[0], [1]], dtype=torch.int32, device=cuda))
+    out = b.mla_decode(q, cache, VDIM, ctx)
+    assert torch.equal(out[0], torch.zeros_like(out[0]))
+    want = A.TorchMath(16, LATENT, SCALE, 1).mla_decode(q[1:].cpu(), cache.cpu(), VDIM, A.context(
+        context_lens=torch.tensor([5], dtype=torch.int32), block_tables=torch.tensor([[1]], dtype=torch.int32)))
+    torch.testing.assert_close(out[1:].float().cpu(), want, **TOL[torch.bfloat16])
+
+
+def test_mla_decode_at_deepseek_v2_lite_shape(cuda):
+    """The full decode step (128 rows, 16 heads, 64-token pages over a 34,000-page pool); sampled rows checked."""
+    wl = W.deepseek_v2_lite_mla()
+    t = W.materialize(wl, cuda)
+    b = MI355XAttention(wl.num_heads, wl.latent_dim, wl.scale, wl.num_heads)
+    width = max(len(x) for x in wl.block_lists)
+    bt = torch.full((wl.rows, width), -1, dtype=torch.int32)
+    for r, lst in enumerate(wl.block_lists):
+        bt[r, :len(lst)] = torch.tensor(lst, dtype=torch.int32)
+    lens = torch.tensor(wl.context_lens, dtype=torch.int32)
+    out = b.mla_decode(t.q, t.k_cache, wl.v_dim, Context(context_lens=lens.to(cuda), block_tables=bt.to(cuda)))
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    order = torch.argsort(lens)
+    sample = sorted({int(order[0]), int(order[-1]), 7, 64, 100})
+    m = A.TorchMath(wl.num_heads, wl.latent_dim, wl.scale, 1)
+    for r in sample:
+        pages = torch.tensor(wl.block_lists[r], dtype=torch.long, device=cuda)
+        cache = t.k_cache[pages].cpu()
+        ctx = A.context(context_lens=lens[r:r + 1], block_tables=torch.arange(len(pages), dtype=torch.int32)[None])
+        want = m.mla_decode(t.q[r:r + 1].cpu(), cache, wl.v_dim, ctx)
+        torch.testing.assert_close(out[r:r + 1].float().cpu(), want, **TOL[torch.bfloat16])
+    assert math.isclose(wl.scale, 1 / math.sqrt(192))
