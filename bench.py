@@ -1,16 +1,19 @@
 """Benchmark of the continuous-batching attention path on one MI355X.
 
-A step is one pass of the path over one synthetic batch, all on the GPU with inputs resident in HBM: the pack
-kernel turns the rows' (num_cached, num_new, block list) -- staged on the device before timing -- into the step's
-metadata, the store kernel scatters the step's new K/V into the paged cache, and the paged-attention kernel
-attends the whole mixed batch. Default workload: Qwen3-8B-shaped chunked-prefill mixed batch at token budget
-8192 (4 chunks of 1536 new tokens on a cached prefix U[0, 6144], plus 2048 decode rows with context
-U[256, 4096]; 32/8 heads, d128, bf16, 256-token pages).
+A step is one pass of the path over one synthetic batch, all on the GPU with inputs resident in HBM:
+- the pack kernel turns the rows' (num_cached, num_new, block list), staged on the device before timing, into the
+  step's metadata (cu_seqlens, positions, slot_mapping, context_lens, padded block_tables);
+- the store kernel scatters the step's new K/V (or MLA latents) into the paged cache;
+- the attention op attends the whole batch (one varlen launch for decode and prompt rows; MLA latent decode for
+  the DeepSeek workload).
 
-Prints one JSON line. ``value`` is the step's algorithmic HBM bytes / step time (GB/s); the line also carries
-tokens/s per layer, the fraction of the 8 TB/s peak, per-kernel times from HIP events on the launch stream,
-a ``roofline`` object for the attention kernel and a ``cpu_baseline`` (the oracle's restatement of the
-reference PyTorch backend, timed on a bounded sample on the host cores).
+The JSON line's ``value`` is the primary workload's algorithmic HBM bytes per step / step time (GB/s). Default
+primary: Qwen3-8B-shaped chunked-prefill mixed batch at token budget 8192 (4 chunks of 1536 new tokens on a
+cached prefix U[0, 6144], plus 2048 decode rows with context U[256, 4096]; 32/8 heads, d128, bf16, 256-token
+pages). The line also carries per-kernel times from HIP events on the launch stream, a ``roofline`` object for
+the attention op, a ``cpu_baseline`` (the oracle's restatement of the reference PyTorch backend timed on a bounded
+sample on the host cores) and, under ``workloads``, the same figures for the other shapes this path is measured on
+(Qwen3-8B pure decode at batch 256, long-context split-K decode, DeepSeek-V2-Lite MLA decode, Qwen3-0.6B mixed).
 """
 
 from __future__ import annotations
@@ -29,6 +32,10 @@ for _p in (ROOT, ROOT / "lean-vllm_amd"):
 
 PEAK_HBM_GBS = 8000.0
 PEAK_BF16_TFLOPS = 2500.0
+METRIC = "paged-attn HBM GB/s (% of peak) + tokens/s per layer, Qwen3-8B mixed batch"
+EXTRA = "qwen3_8b_decode,qwen3_8b_long,deepseek_v2_lite_mla,qwen3_0_6b_mixed"
+# Workloads whose whole working set fits the 256 MB Infinity Cache: each timed step starts from a flushed cache.
+FLUSHED = {"qwen3_0_6b_mixed"}
 
 
 def parse():
@@ -37,6 +44,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="qwen3_8b_mixed")
+    ap.add_argument("--extra", default=EXTRA, help="comma-separated workloads also measured ('none' for none)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -58,20 +66,98 @@ def calibrate_copy(mib: int):
     print(json.dumps({"copy_calibration_bytes_per_launch": mib << 20, "launches": 5}), flush=True)
 
 
+def measure(name: str, steps: int, warmup: int, seed: int, dev):
+    """Time ``steps`` steps of one workload; returns (figures, workload, tensors)."""
+    import torch
+
+    from lvattn import Context, MI355XAttention, Packer
+    from lvattn import workloads as W
+
+    wl = W.WORKLOADS[name](seed)
+    t = W.materialize(wl, dev, torch.bfloat16, seed=seed)
+    heads_kv = wl.num_heads if wl.is_mla else wl.num_kv_heads
+    backend = MI355XAttention(wl.num_heads, wl.latent_dim if wl.is_mla else wl.head_dim, wl.scale, heads_kv)
+    packer = Packer(dev, wl.block_size)
+    plan = packer.stage(wl.num_cached, wl.num_new, wl.block_lists)
+    out = torch.empty(wl.tokens, wl.num_heads, wl.v_dim if wl.is_mla else wl.head_dim, dtype=torch.bfloat16,
+                      device=dev)
+    flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev) if name in FLUSHED else None
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    ev = {k: [torch.cuda.Event(enable_timing=True) for _ in range(steps)] for k in ("a", "b", "c", "d")}
+
+    def step(i=None):
+        if flush is not None:
+            flush.fill_(i or 0)  # evicts the previous step's lines; outside the event brackets
+        if i is not None:
+            ev["a"][i].record(stream)
+        _, ctx = packer.run(plan)
+        if i is not None:
+            ev["b"][i].record(stream)
+        if wl.is_mla:
+            backend.store_latents(t.k_new, t.k_cache, ctx["slot_mapping"])
+        else:
+            backend.store_kvcache(t.k_new, t.v_new, t.k_cache, t.v_cache, ctx["slot_mapping"])
+        if i is not None:
+            ev["c"][i].record(stream)
+        fields = {k: v for k, v in ctx.items() if k in Context.__slots__}
+        if wl.is_mla:
+            backend.mla_decode(t.q, t.k_cache, wl.v_dim, Context(**fields), out=out)
+        else:
+            backend.forward(t.q, t.k_new, t.v_new, t.k_cache, t.v_cache, Context(**fields), out=out)
+        if i is not None:
+            ev["d"][i].record(stream)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(i)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+
+    def avg_ms(x, y):
+        return sum(ev[x][i].elapsed_time(ev[y][i]) for i in range(steps)) / steps
+
+    pack_ms, store_ms, attn_ms = avg_ms("a", "b"), avg_ms("b", "c"), avg_ms("c", "d")
+    step_ms = avg_ms("a", "d") if flush is not None else wall_ms
+    nbytes = W.algorithmic_bytes(wl)
+    flops = W.algorithmic_flops(wl)
+    attn_gbs = nbytes["attention"] / (attn_ms * 1e-3) / 1e9
+    figures = {
+        "workload": name,
+        "rows": wl.rows,
+        "tokens": wl.tokens,
+        "ms_per_step": round(step_ms, 4),
+        "GBs": round(nbytes["total"] / (step_ms * 1e-3) / 1e9, 1),
+        "pct_of_peak_hbm": round(100 * nbytes["total"] / (step_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 2),
+        "tokens_per_s_per_layer": round(wl.tokens / (step_ms * 1e-3), 1),
+        "kernel_ms": {"pack": round(pack_ms, 4), "store": round(store_ms, 4), "attention": round(attn_ms, 4)},
+        "attention_GBs": round(attn_gbs, 1),
+        "attention_frac_of_peak": round(attn_gbs / PEAK_HBM_GBS, 4),
+        "attention_TFLOPs": round(flops / (attn_ms * 1e-3) / 1e12, 2),
+        "bytes": nbytes,
+        "flops": flops,
+        "cache_flushed_each_step": flush is not None,
+    }
+    return figures, wl, t
+
+
 def cpu_baseline(wl, t, dec_sample: int = 96):
     """The oracle's TorchAttention restatement (page gather, zeroed padding, row padding, bottom-right mask,
     GQA-folded SDPA) in fp32 on the host cores, on a bounded sample of the step: every prompt chunk in full plus
-    ``dec_sample`` decode rows, the decode time scaled to all decode rows. Returns the object for the JSON line."""
+    ``dec_sample`` decode rows, the decode time scaled to all decode rows. Returns the object for the JSON line,
+    in the same algorithmic-byte GB/s as the GPU figures (and tokens/s per layer)."""
     import numpy as np
     import torch
 
-    from lvattn.workloads import batch_order
+    from lvattn import workloads as W
     from oracle import attention as A
 
     torch.set_num_threads(len(os.sched_getaffinity(0)))
     cores = torch.get_num_threads()
-    bs = wl.block_size
-    order = batch_order(wl)
+    order = W.batch_order(wl)
     num_new = np.asarray(wl.num_new)[order]
     num_cached = np.asarray(wl.num_cached)[order]
     lists = [wl.block_lists[i] for i in order]
@@ -118,123 +204,92 @@ def cpu_baseline(wl, t, dec_sample: int = 96):
             total += time.perf_counter() - t0
         timings["prefill"] = total
     seconds = sum(timings.values())
+    nbytes = W.algorithmic_bytes(wl)["attention"]
     return {
-        "value": round(wl.tokens / seconds, 1),
-        "unit": "tokens/s per layer",
+        "value": round(nbytes / seconds / 1e9, 2),
+        "unit": "GB/s",
         "cores": cores,
         "kind": "port",
-        "sample": (f"oracle TorchAttention restatement, fp32, {cores} threads: all {len(pre_rows)} prompt chunks "
-                   f"in full ({timings.get('prefill', 0):.2f} s) + {len(sample_dec)} of {len(dec_rows)} decode rows "
-                   f"scaled to all ({timings.get('decode', 0):.2f} s est.)"),
+        "sample": (f"oracle TorchAttention restatement (attention only), fp32, {cores} threads: all {len(pre_rows)} "
+                   f"prompt chunks in full ({timings.get('prefill', 0):.2f} s) + {len(sample_dec)} of "
+                   f"{len(dec_rows)} decode rows scaled to all ({timings.get('decode', 0):.2f} s est.)"),
+        "tokens_per_s_per_layer": round(wl.tokens / seconds, 1),
         "seconds_per_step": round(seconds, 3),
     }
+
+
+def traffic_of(name: str):
+    """HBM bytes per attention launch from the committed rocprofv3 counter summary, if there is one."""
+    f = ROOT / "profiles" / f"traffic_{name}.json"
+    if f.exists():
+        return json.loads(f.read_text()).get("hbm_bytes_per_launch")
+    return None
 
 
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this path runs on a single GPU)",
-              file=sys.stderr)
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: this path runs on a single GPU and "
+              "nothing in it spans GPUs", file=sys.stderr)
         sys.exit(2)
     if args.calibrate_copy:
         calibrate_copy(args.calibrate_copy)
         return
     import torch
 
-    from lvattn import Context, MI355XAttention, Packer, _capi
-    from lvattn import workloads as W
-
     dev = torch.device("cuda:0")
-    wl = W.WORKLOADS[args.workload](args.seed)
-    if wl.is_mla:
-        raise SystemExit("the MLA workload is benchmarked by bench_mla (not yet built)")
-    t = W.materialize(wl, dev, torch.bfloat16, seed=args.seed)
-    backend = MI355XAttention(wl.num_heads, wl.head_dim, wl.scale, wl.num_kv_heads)
-    packer = Packer(dev, wl.block_size)
-    plan = packer.stage(wl.num_cached, wl.num_new, wl.block_lists)
-    torch.cuda.synchronize()
-    out = torch.empty_like(t.q)
-    stream = torch.cuda.current_stream(dev)
+    primary, wl, t = measure(args.workload, args.steps, args.warmup, args.seed, dev)
+    cpu = None if args.no_cpu_baseline or wl.is_mla else cpu_baseline(wl, t)
+    del t
+    torch.cuda.empty_cache()
+    extras = []
+    for name in [n for n in args.extra.split(",") if n and n != "none" and n != args.workload]:
+        fig, _, t = measure(name, args.steps, args.warmup, args.seed, dev)
+        extras.append(fig)
+        del t
+        torch.cuda.empty_cache()
 
-    ev = {k: [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)] for k in ("a", "b", "c", "d")}
-
-    def step(i=None):
-        if i is not None:
-            ev["a"][i].record(stream)
-        _, ctx = packer.run(plan)
-        if i is not None:
-            ev["b"][i].record(stream)
-        backend.store_kvcache(t.k_new, t.v_new, t.k_cache, t.v_cache, ctx["slot_mapping"])
-        if i is not None:
-            ev["c"][i].record(stream)
-        fields = {k: v for k, v in ctx.items() if k in Context.__slots__}
-        backend.forward(t.q, t.k_new, t.v_new, t.k_cache, t.v_cache, Context(**fields), out=out)
-        if i is not None:
-            ev["d"][i].record(stream)
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(i)
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-
-    def avg_ms(x, y):
-        return sum(ev[x][i].elapsed_time(ev[y][i]) for i in range(args.steps)) / args.steps
-
-    pack_ms, store_ms, attn_ms = avg_ms("a", "b"), avg_ms("b", "c"), avg_ms("c", "d")
-    ms_per_step = elapsed * 1e3 / args.steps
-    nbytes = W.algorithmic_bytes(wl)
-    flops = W.algorithmic_flops(wl)
-    gbs = nbytes["total"] / (ms_per_step * 1e-3) / 1e9
-    attn_gbs = nbytes["attention"] / (attn_ms * 1e-3) / 1e9
-    attn_tflops = flops / (attn_ms * 1e-3) / 1e12
-    traffic = None
-    tfile = ROOT / "profiles" / f"traffic_{wl.name}.json"
-    if tfile.exists():
-        traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
     result = {
-        "metric": "paged-attn HBM GB/s (% of peak) + tokens/s per layer, Qwen3-8B mixed batch",
-        "value": round(gbs, 1),
+        "metric": METRIC,
+        "value": primary["GBs"],
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
+        "ms_per_step": primary["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
         "config": {
-            "workload": wl.name,
-            "rows": wl.rows,
-            "tokens": wl.tokens,
-            "heads": f"{wl.num_heads}/{wl.num_kv_heads}",
-            "head_dim": wl.head_dim,
+            "workload": primary["workload"],
+            "rows": primary["rows"],
+            "tokens": primary["tokens"],
+            "heads": f"{wl.num_heads}/{wl.num_heads if wl.is_mla else wl.num_kv_heads}",
+            "head_dim": wl.latent_dim if wl.is_mla else wl.head_dim,
             "block_size": wl.block_size,
             "parallelism": "single GPU",
         },
-        "pct_of_peak_hbm": round(100 * gbs / PEAK_HBM_GBS, 2),
-        "tokens_per_s_per_layer": round(wl.tokens / (ms_per_step * 1e-3), 1),
-        "kernel_ms": {"pack": round(pack_ms, 4), "store": round(store_ms, 4), "attention": round(attn_ms, 4)},
-        "bytes": nbytes,
+        "pct_of_peak_hbm": primary["pct_of_peak_hbm"],
+        "tokens_per_s_per_layer": primary["tokens_per_s_per_layer"],
+        "kernel_ms": primary["kernel_ms"],
+        "bytes": primary["bytes"],
         "roofline": {
             "bound": "hbm",
-            "achieved": round(attn_gbs, 1),
+            "achieved": primary["attention_GBs"],
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
-            "frac": round(attn_gbs / PEAK_HBM_GBS, 4),
-            "traffic": traffic,
-            "kernel": "paged_attention_kernel",
-            "algorithmic_bytes_per_launch": nbytes["attention"],
-            "tflops": round(attn_tflops, 2),
+            "frac": primary["attention_frac_of_peak"],
+            "traffic": traffic_of(primary["workload"]),
+            "kernel": "lv_paged_attention (paged_attention_kernel + work-list plan + split-K merge)",
+            "algorithmic_bytes_per_launch": primary["bytes"]["attention"],
+            "tflops": primary["attention_TFLOPs"],
         },
+        "workloads": extras,
     }
-    if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(wl, t)
+    if cpu is not None:
+        result["cpu_baseline"] = cpu
     print(json.dumps(result), flush=True)
 
 

@@ -136,6 +136,28 @@ __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ inline float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 
 // ---------------------------------------------------------------------------------------------------------
+// Division of non-negative 31-bit integers by a divisor fixed at launch (Granlund and Montgomery, "Division by
+// invariant integers using multiplication", 1994): q = (umulhi(n, m) + n) >> s with s = ceil(log2 d) and
+// m = floor(2^32 (2^s - d) / d) + 1. Exact for 0 <= n < 2^31, 1 <= d < 2^31.
+struct FastDiv {
+  uint32_t d, m, s;
+  static FastDiv make(uint32_t d) {
+    uint32_t s = 0;
+    while ((1ull << s) < d) ++s;
+    const uint64_t m = ((((uint64_t)1 << s) - d) << 32) / d + 1;
+    return FastDiv{d, (uint32_t)m, s};
+  }
+  __device__ __host__ inline uint32_t div(uint32_t n) const {
+#ifdef __HIP_DEVICE_COMPILE__
+    const uint32_t hi = __umulhi(n, m);
+#else
+    const uint32_t hi = (uint32_t)(((uint64_t)n * m) >> 32);
+#endif
+    return (hi + n) >> s;
+  }
+};
+
+// ---------------------------------------------------------------------------------------------------------
 // Global memory.
 
 #ifndef LV_STREAM_NT

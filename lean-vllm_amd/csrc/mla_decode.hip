@@ -27,6 +27,9 @@ constexpr int kMlaKHalf = kLatent / 64;   // MFMA k-steps (32 wide) per k half: 
 constexpr int kStageLoads = kMlaTile * kLatChunks / 256;  // 16-byte chunks each thread stages per tile: 9
 static_assert(kMlaTile * kLatChunks % 256 == 0, "tile chunks split evenly over 256 threads");
 
+constexpr int kMlaMaxSplit = 4096;        // latents per work item at most
+constexpr int kMlaMaxBlocks = kMlaMaxSplit / 16 + 2;  // pages one work item touches at most (pages >= 16 latents)
+
 #ifndef LV_MLA_SPLIT_TARGET
 #define LV_MLA_SPLIT_TARGET 4096
 #endif
@@ -36,7 +39,7 @@ struct MlaParams {
   int64_t q_st, q_sh;  // bytes
   const char* cache;
   int64_t c_sb, c_st;  // bytes
-  int32_t bs;
+  FastDiv bs;  // latents per page
   const int32_t* tables;
   int64_t t_stride;  // elements
   const int32_t* lens;
@@ -64,6 +67,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
   using E = Elem<T>;
   __shared__ __attribute__((aligned(16))) uint16_t lat[kMlaTile * kMlaPitch];
   __shared__ __attribute__((aligned(16))) f32x4 spart[4][64];
+  __shared__ int64_t page_off[kMlaMaxBlocks];  // byte offsets of the work item's pages, in order
   const int row = blockIdx.x / p.max_splits, split = blockIdx.x % p.max_splits;
   const int qj = blockIdx.y / p.htiles, ht = blockIdx.y % p.htiles;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -95,7 +99,14 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
 #pragma unroll
   for (int j = 0; j < 8; ++j) o[j] = f32x4{0, 0, 0, 0};
 
-  const int32_t* table = p.tables + (int64_t)row * p.t_stride;
+  // The work item's pages, looked up once: tile loads then wait on no table read.
+  const int page0 = kend > kbeg ? (int)p.bs.div(kbeg) : 0;
+  const int npages = kend > kbeg ? (int)p.bs.div(kend - 1) - page0 + 1 : 0;
+  {
+    const int32_t* table = p.tables + (int64_t)row * p.t_stride + page0;
+    for (int i = tid; i < npages; i += 256) page_off[i] = (int64_t)table[i] * p.c_sb;
+  }
+  __syncthreads();
   // Latents past the range are staged as zeros: their weight is 0 and 0 * NaN must not happen.
   auto fetch = [&](int t0, u32x4 (&st)[kStageLoads]) {
 #pragma unroll
@@ -105,7 +116,8 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
       const int tok = t0 + tt;
       u32x4 v = {0, 0, 0, 0};
       if (tok < kend) {
-        const int64_t off = (int64_t)table[tok / p.bs] * p.c_sb + (int64_t)(tok % p.bs) * p.c_st + part * 16;
+        const int pg = (int)p.bs.div(tok);
+        const int64_t off = page_off[pg - page0] + (int64_t)(tok - pg * (int)p.bs.d) * p.c_st + part * 16;
         v = ld16_stream(p.cache + off);
       }
       st[i] = v;
@@ -251,7 +263,8 @@ static MlaShape mla_shape(int32_t rows, int32_t lq, int32_t heads, int32_t max_k
   const int64_t units = (int64_t)rows * lq * ((heads + 15) / 16);
   const int64_t keys = max_k > 0 ? max_k : 1;
   int64_t split = 256;
-  while (split < keys && units * ((keys + split - 1) / split) > LV_MLA_SPLIT_TARGET) split *= 2;
+  while (split < kMlaMaxSplit && split < keys && units * ((keys + split - 1) / split) > LV_MLA_SPLIT_TARGET)
+    split *= 2;
   s.split = (int32_t)split;
   s.max_splits = (int32_t)((keys + split - 1) / split);
   const size_t parts = s.max_splits > 1 ? (size_t)rows * lq * heads * s.max_splits : 0;
@@ -284,7 +297,7 @@ extern "C" int lv_mla_decode(const void* q, int64_t q_stride_t, int64_t q_stride
   LV_REQUIRE(latent_dim == kLatent && v_dim == kVDim, "mla_decode: latent %d / values %d; %d / %d are served",
              latent_dim, v_dim, kLatent, kVDim);
   if (num_rows == 0) return LV_OK;
-  LV_REQUIRE(block_size > 0, "mla_decode: block_size must be positive, got %d", block_size);
+  LV_REQUIRE(block_size >= 16, "mla_decode: block_size must be at least 16, got %d", block_size);
   LV_REQUIRE(q && latent_cache && block_tables && context_lens && out, "mla_decode: null tensor pointer");
   LV_REQUIRE(max_seqlen_k >= 0, "mla_decode: negative max_seqlen_k");
   LV_REQUIRE(scale > 0.f, "mla_decode: the softmax scale must be positive, got %g", (double)scale);
@@ -307,7 +320,7 @@ extern "C" int lv_mla_decode(const void* q, int64_t q_stride_t, int64_t q_stride
   p.cache = (const char*)latent_cache;
   p.c_sb = cache_stride_block * 2;
   p.c_st = cache_stride_token * 2;
-  p.bs = block_size;
+  p.bs = FastDiv::make((uint32_t)block_size);
   p.tables = block_tables;
   p.t_stride = table_stride;
   p.lens = context_lens;

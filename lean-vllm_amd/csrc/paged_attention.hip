@@ -44,7 +44,7 @@ struct AttnParams {
   const char* k_cache;
   const char* v_cache;
   int64_t c_sb, c_st, c_sh;  // bytes
-  int32_t bs;
+  FastDiv bs;  // tokens per page
   const int32_t* tables;
   int64_t t_stride;  // elements
   const int32_t* cu_q;
@@ -132,7 +132,8 @@ __device__ void decode_item(const AttnParams& p, int row, int split, int kvh, in
   const int32_t* table = p.tables + (int64_t)row * p.t_stride;
 
   auto tile_base = [&](int t0) {
-    return (int64_t)table[t0 / p.bs] * p.c_sb + (int64_t)(t0 % p.bs) * p.c_st + (int64_t)kvh * p.c_sh;
+    const int pg = (int)p.bs.div(t0);
+    return (int64_t)table[pg] * p.c_sb + (int64_t)(t0 - pg * (int)p.bs.d) * p.c_st + (int64_t)kvh * p.c_sh;
   };
   auto load_rows = [&](const char* cache, int64_t base, u32x4 (&x)[U]) {
     const char* b = cache + base;
@@ -403,8 +404,9 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
       const int jk = kt + key;
       u32x4 kk = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
       if (jk < lk) {
-        const int64_t blk = table[jk / p.bs];
-        const int64_t off = blk * p.c_sb + (int64_t)(jk % p.bs) * p.c_st + (int64_t)kvh * p.c_sh + part * 16;
+        const int pg = (int)p.bs.div(jk);
+        const int64_t off = (int64_t)table[pg] * p.c_sb + (int64_t)(jk - pg * (int)p.bs.d) * p.c_st +
+                            (int64_t)kvh * p.c_sh + part * 16;
         kk = ld16(p.k_cache + off);
         vv = ld16(p.v_cache + off);
       }
@@ -730,7 +732,7 @@ extern "C" int lv_paged_attention(const void* q, int64_t q_stride_t, int64_t q_s
   p.c_sb = cache_stride_block * 2;
   p.c_st = cache_stride_token * 2;
   p.c_sh = cache_stride_head * 2;
-  p.bs = block_size;
+  p.bs = FastDiv::make((uint32_t)block_size);
   p.tables = block_tables;
   p.t_stride = table_stride;
   p.cu_q = cu_seqlens_q;

@@ -164,11 +164,11 @@ class MI355XAttention(AttentionBackend):
                             seqlens_k=None, cu_seqlens_k=cu_k.to(torch.int32), rows=cu_q.numel() - 1,
                             max_seqlen_q=max_q, max_seqlen_k=max_k)
 
-    def mla_decode(self, q, latent_cache, v_dim, context: Context):
+    def mla_decode(self, q, latent_cache, v_dim, context: Context, out=None):
         """Each row's last ``Lq`` queries against its paged latents, read as one key head shared by every query
         head; values are the latents' first ``v_dim`` entries (``abstract.py:206-219``). q ``[B * Lq, H, 576]``,
         latent_cache ``[N, bs, 576]`` -> ``[B * Lq, H, v_dim]``. Nothing is read back: ``Lq`` comes from the
-        shapes and the split-K grid from the block-table width."""
+        shapes and the split-K grid from the block-table width. ``out``, if given, receives the result."""
         bt, lens = context.block_tables, context.context_lens
         assert bt is not None and lens is not None and bt.dtype == torch.int32 and bt.stride(-1) == 1
         lens = lens if lens.dtype == torch.int32 else lens.to(torch.int32)
@@ -181,7 +181,9 @@ class MI355XAttention(AttentionBackend):
         assert tokens % rows == 0, "every row has the same number of queries"
         lq = tokens // rows
         max_k = bt.size(1) * latent_cache.size(1)
-        out = torch.empty(tokens, heads, v_dim, dtype=q.dtype, device=q.device)
+        if out is None:
+            out = torch.empty(tokens, heads, v_dim, dtype=q.dtype, device=q.device)
+        assert out.shape == (tokens, heads, v_dim) and out.dtype == q.dtype and out.stride(-1) == 1
         nbytes = _capi.query("lv_mla_decode_workspace_bytes", rows, lq, heads, max_k)
         ws = _WORKSPACE.get(q.device, nbytes)
         _capi.call("lv_mla_decode", q.data_ptr(), q.stride(0), q.stride(1), latent_cache.data_ptr(),
