@@ -34,9 +34,6 @@ constexpr int kPlanMaxRows = 4096;  // rows of a step with prompts (the work-lis
 #ifndef LV_MIN_SPLIT
 #define LV_MIN_SPLIT 256
 #endif
-#ifndef LV_HEAD_FASTEST
-#define LV_HEAD_FASTEST 0
-#endif
 
 struct AttnParams {
   const char* q;
@@ -502,57 +499,91 @@ struct SmemBytes {
   static constexpr int kMixed = kDecode > kPrefill ? kDecode : kPrefill;
 };
 
-template <typename T, int D, int GS, bool MIXED>
+// LISTED: blockIdx.x walks the device work list with the query-head groups innermost, so workgroups are
+// dispatched in list order (longest first). Otherwise (decode of more rows than the planner holds) blockIdx.x is
+// (row, split) and blockIdx.y the query-head group. MIXED: the list holds prompt items (MFMA path) too.
+template <typename T, int D, int GS, bool LISTED, bool MIXED>
 __global__ __launch_bounds__(256) void paged_attention_kernel(AttnParams p) {
   constexpr int kSmem = MIXED ? SmemBytes<D, GS>::kMixed : SmemBytes<D, GS>::kDecode;
   __shared__ __attribute__((aligned(16))) char smem[kSmem];
-#if LV_HEAD_FASTEST
-  const int ny = p.hkv * p.qgroups;
-  const int by = blockIdx.x % ny, bx = blockIdx.x / ny;
-#else
-  const int by = blockIdx.y, bx = blockIdx.x;
-#endif
-  const int kvh = by / p.qgroups, qg = by % p.qgroups;
-  if constexpr (MIXED) {
+  if constexpr (LISTED) {
+    const int ny = p.hkv * p.qgroups;
+    const int bx = blockIdx.x / ny, by = blockIdx.x - bx * ny;
+    const int kvh = by / p.qgroups, qg = by - kvh * p.qgroups;
     if (bx >= *p.n_items) return;
     const int2 it = p.items[bx];
-    if (it.y >= 0)
+    if (!MIXED || it.y >= 0)
       decode_item<T, D, GS>(p, it.x, it.y, kvh, qg, smem);
     else if (qg == 0)
       prefill_item<T, D>(p, it.x, -1 - it.y, kvh, smem);
   } else {
-    decode_item<T, D, GS>(p, bx / p.max_splits, bx % p.max_splits, kvh, qg, smem);
+    const int kvh = blockIdx.y / p.qgroups, qg = blockIdx.y % p.qgroups;
+    decode_item<T, D, GS>(p, blockIdx.x / p.max_splits, blockIdx.x % p.max_splits, kvh, qg, smem);
   }
 }
 
-// Work list of a mixed step: prefill items (row, -1 - tile) first, then decode items (row, split).
+constexpr int kLenBuckets = 64;
+// Bucket of a split of `keys` keys out of `split`: longer splits get smaller buckets (dispatched first).
+__device__ inline int len_bucket(int keys, int split) {
+  const int b = (int)(((int64_t)(split - keys) * kLenBuckets) / split);
+  return b < kLenBuckets - 1 ? b : kLenBuckets - 1;
+}
+
+// Work list of a step, longest work first: prompt items (row, -1 - tile), then every full decode split (row, s),
+// then each decode row's last split (row, n - 1) by decreasing key count (counting sort over length buckets).
+// In-order dispatch of that list approximates longest-processing-time scheduling, so the launch ends with short
+// items instead of a tail of full ones.
 __global__ __launch_bounds__(kScanThreads) void plan_kernel(const int32_t* __restrict__ cu_q,
                                                             const int32_t* __restrict__ lens_k,
                                                             const int32_t* __restrict__ cu_k, int32_t rows,
                                                             int32_t split, int32_t qp, int32_t max_items,
                                                             int2* __restrict__ items, int32_t* __restrict__ n_items) {
   __shared__ int pre[kPlanMaxRows + 1];
-  __shared__ int dec[kPlanMaxRows + 1];
+  __shared__ int full[kPlanMaxRows + 1];
+  __shared__ int bucket[kLenBuckets + 1];
   __shared__ int wave_tot[kScanThreads / 64 + 1];
   const int tid = threadIdx.x;
+  for (int b = tid; b <= kLenBuckets; b += kScanThreads) bucket[b] = 0;
+  __syncthreads();
   for (int r = tid; r < rows; r += kScanThreads) {
-    const int lq = cu_q[r + 1] - cu_q[r];
+    const int lq = cu_q ? cu_q[r + 1] - cu_q[r] : 1;
     const int lk = lens_k ? lens_k[r] : cu_k[r + 1] - cu_k[r];
-    const int nd = lk > 0 ? (lk + split - 1) / split : 1;
     pre[r] = lq > 1 ? (lq + qp - 1) / qp : 0;
-    dec[r] = lq == 1 ? nd : 0;
+    full[r] = 0;
+    if (lq == 1) {
+      const int n = lk > 0 ? (lk + split - 1) / split : 1;
+      full[r] = n - 1;
+      atomicAdd(&bucket[len_bucket(lk - (n - 1) * split, split)], 1);
+    }
   }
   __syncthreads();
   block_scan(pre, rows, wave_tot);
-  block_scan(dec, rows, wave_tot);
-  const int npre = pre[rows];
+  block_scan(full, rows, wave_tot);
+  if (tid == 0) {
+    int run = 0;
+    for (int b = 0; b < kLenBuckets; ++b) {
+      const int v = bucket[b];
+      bucket[b] = run;
+      run += v;
+    }
+    bucket[kLenBuckets] = run;
+  }
+  __syncthreads();
+  const int npre = pre[rows], nfull = full[rows], npart = bucket[kLenBuckets];
   for (int r = tid; r < rows; r += kScanThreads) {
     for (int i = pre[r]; i < pre[r + 1]; ++i)
       if (i < max_items) items[i] = make_int2(r, -1 - (i - pre[r]));
-    for (int i = dec[r]; i < dec[r + 1]; ++i)
-      if (npre + i < max_items) items[npre + i] = make_int2(r, i - dec[r]);
+    for (int i = full[r]; i < full[r + 1]; ++i)
+      if (npre + i < max_items) items[npre + i] = make_int2(r, i - full[r]);
+    const int lq = cu_q ? cu_q[r + 1] - cu_q[r] : 1;
+    if (lq == 1) {
+      const int lk = lens_k ? lens_k[r] : cu_k[r + 1] - cu_k[r];
+      const int n = lk > 0 ? (lk + split - 1) / split : 1;
+      const int pos = npre + nfull + atomicAdd(&bucket[len_bucket(lk - (n - 1) * split, split)], 1);
+      if (pos < max_items) items[pos] = make_int2(r, n - 1);
+    }
   }
-  if (tid == 0) *n_items = min(npre + dec[rows], max_items);
+  if (tid == 0) *n_items = min(npre + nfull + npart, max_items);
 }
 
 // Combine a split row's partial outputs: o = sum_s 2^(lse_s - M) o_s / sum_s 2^(lse_s - M).
@@ -608,7 +639,7 @@ static int pick_gs(int group) {
 }
 
 static Shape plan_shape(int32_t rows, int32_t tokens, int32_t hq, int32_t hkv, int32_t d, int32_t max_k,
-                        bool decode_only) {
+                        bool listed) {
   Shape s{};
   const int group = hq / hkv;
   s.gs = pick_gs(group);
@@ -621,7 +652,7 @@ static Shape plan_shape(int32_t rows, int32_t tokens, int32_t hq, int32_t hkv, i
   s.split = (int32_t)split;
   s.max_splits = (int32_t)((keys + split - 1) / split);
   const int qp = kPrefillRows / (group > 0 ? group : 1);
-  s.max_items = decode_only ? 0 : rows * s.max_splits + (tokens + qp - 1) / qp + rows;
+  s.max_items = listed ? rows * s.max_splits + (tokens + qp - 1) / qp + rows : 0;
   size_t off = 0;
   s.items_off = off;
   off += (size_t)s.max_items * sizeof(int2);
@@ -639,32 +670,32 @@ static Shape plan_shape(int32_t rows, int32_t tokens, int32_t hq, int32_t hkv, i
 }
 
 template <typename T, int D, int GS>
-static void launch(const AttnParams& p, bool mixed, int grid_x, hipStream_t stream) {
-#if LV_HEAD_FASTEST
-  const dim3 grid(grid_x * p.hkv * p.qgroups, 1);
-#else
-  const dim3 grid(grid_x, p.hkv * p.qgroups);
-#endif
-  if (mixed)
-    hipLaunchKernelGGL((paged_attention_kernel<T, D, GS, true>), grid, dim3(256), 0, stream, p);
+static void launch(const AttnParams& p, bool listed, bool mixed, int max_items, hipStream_t stream) {
+  const int ny = p.hkv * p.qgroups;
+  if (listed && mixed)
+    hipLaunchKernelGGL((paged_attention_kernel<T, D, GS, true, true>), dim3(max_items * ny), dim3(256), 0, stream, p);
+  else if (listed)
+    hipLaunchKernelGGL((paged_attention_kernel<T, D, GS, true, false>), dim3(max_items * ny), dim3(256), 0, stream,
+                       p);
   else
-    hipLaunchKernelGGL((paged_attention_kernel<T, D, GS, false>), grid, dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((paged_attention_kernel<T, D, GS, false, false>), dim3(p.rows * p.max_splits, ny), dim3(256),
+                       0, stream, p);
   if (p.max_splits > 1)
     hipLaunchKernelGGL((splitk_merge_kernel<T, D>), dim3(p.rows, p.hq), dim3(64), 0, stream, p);
 }
 
 template <typename T, int D>
-static void launch_gs(const AttnParams& p, int gs, bool mixed, int grid_x, hipStream_t stream) {
-  if (gs == 4) launch<T, D, 4>(p, mixed, grid_x, stream);
-  else if (gs == 2) launch<T, D, 2>(p, mixed, grid_x, stream);
-  else launch<T, D, 1>(p, mixed, grid_x, stream);
+static void launch_gs(const AttnParams& p, int gs, bool listed, bool mixed, int max_items, hipStream_t stream) {
+  if (gs == 4) launch<T, D, 4>(p, listed, mixed, max_items, stream);
+  else if (gs == 2) launch<T, D, 2>(p, listed, mixed, max_items, stream);
+  else launch<T, D, 1>(p, listed, mixed, max_items, stream);
 }
 
 template <typename T>
-static int launch_d(const AttnParams& p, int d, int gs, bool mixed, int grid_x, hipStream_t stream) {
+static int launch_d(const AttnParams& p, int d, int gs, bool listed, bool mixed, int max_items, hipStream_t stream) {
   switch (d) {
-    case 64: launch_gs<T, 64>(p, gs, mixed, grid_x, stream); return LV_OK;
-    case 128: launch_gs<T, 128>(p, gs, mixed, grid_x, stream); return LV_OK;
+    case 64: launch_gs<T, 64>(p, gs, listed, mixed, max_items, stream); return LV_OK;
+    case 128: launch_gs<T, 128>(p, gs, listed, mixed, max_items, stream); return LV_OK;
     default: set_error("paged_attention: head_dim %d is not 64 or 128", d); return LV_EINVAL;
   }
 }
@@ -677,7 +708,9 @@ extern "C" size_t lv_paged_attention_workspace_bytes(int32_t num_rows, int32_t n
                                                      int32_t num_kv_heads, int32_t head_dim, int32_t max_seqlen_k,
                                                      int32_t decode_only) {
   if (num_rows <= 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads) return 0;
-  return plan_shape(num_rows, num_tokens, num_heads, num_kv_heads, head_dim, max_seqlen_k, decode_only != 0).bytes;
+  const bool mixed = decode_only == 0;
+  const bool listed = mixed || num_rows <= kPlanMaxRows;
+  return plan_shape(num_rows, num_tokens, num_heads, num_kv_heads, head_dim, max_seqlen_k, listed).bytes;
 }
 
 extern "C" int lv_paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_cache,
@@ -718,7 +751,8 @@ extern "C" int lv_paged_attention(const void* q, int64_t q_stride_t, int64_t q_s
   const bool mixed = cu_seqlens_q != nullptr && max_seqlen_q > 1;
   LV_REQUIRE(!mixed || num_rows <= kPlanMaxRows, "paged_attention: a step with prompts holds at most %d rows, got %d",
              kPlanMaxRows, num_rows);
-  const Shape s = plan_shape(num_rows, num_tokens, num_heads, num_kv_heads, head_dim, max_seqlen_k, !mixed);
+  const bool listed = num_rows <= kPlanMaxRows;
+  const Shape s = plan_shape(num_rows, num_tokens, num_heads, num_kv_heads, head_dim, max_seqlen_k, listed);
   LV_REQUIRE(workspace_bytes >= s.bytes && (s.bytes == 0 || workspace),
              "paged_attention: workspace of %zu bytes given, %zu needed", workspace_bytes, s.bytes);
   LV_REQUIRE(aligned(workspace, 256), "paged_attention: workspace must be 256-byte aligned");
@@ -752,21 +786,19 @@ extern "C" int lv_paged_attention(const void* q, int64_t q_stride_t, int64_t q_s
   char* ws = (char*)workspace;
   p.part_lse = s.max_splits > 1 ? reinterpret_cast<float*>(ws + s.lse_off) : nullptr;
   p.part_o = s.max_splits > 1 ? reinterpret_cast<float*>(ws + s.o_off) : nullptr;
-  p.items = mixed ? reinterpret_cast<const int2*>(ws + s.items_off) : nullptr;
-  p.n_items = mixed ? reinterpret_cast<const int32_t*>(ws + s.count_off) : nullptr;
+  p.items = listed ? reinterpret_cast<const int2*>(ws + s.items_off) : nullptr;
+  p.n_items = listed ? reinterpret_cast<const int32_t*>(ws + s.count_off) : nullptr;
 
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  int grid_x = num_rows * s.max_splits;
-  if (mixed) {
+  if (listed) {
     const int qp = kPrefillRows / p.group;
-    hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kScanThreads), 0, st, cu_seqlens_q, seqlens_k, cu_seqlens_k,
-                       num_rows, s.split, qp, s.max_items, reinterpret_cast<int2*>(ws + s.items_off),
+    hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kScanThreads), 0, st, mixed ? cu_seqlens_q : nullptr, seqlens_k,
+                       cu_seqlens_k, num_rows, s.split, qp, s.max_items, reinterpret_cast<int2*>(ws + s.items_off),
                        reinterpret_cast<int32_t*>(ws + s.count_off));
     LV_LAUNCH_CHECK("plan_kernel");
-    grid_x = s.max_items;
   }
-  const int rc = dtype == LV_DTYPE_BF16 ? launch_d<BF16>(p, head_dim, s.gs, mixed, grid_x, st)
-                                        : launch_d<F16>(p, head_dim, s.gs, mixed, grid_x, st);
+  const int rc = dtype == LV_DTYPE_BF16 ? launch_d<BF16>(p, head_dim, s.gs, listed, mixed, s.max_items, st)
+                                        : launch_d<F16>(p, head_dim, s.gs, listed, mixed, s.max_items, st);
   if (rc != LV_OK) return rc;
   LV_LAUNCH_CHECK("paged_attention_kernel");
   return LV_OK;
