@@ -3,7 +3,7 @@
 This is the reference's ``AttentionBackend`` contract (``lean_vllm/attention/abstract.py:9-224``): the same
 ``LayerSpec``, capability flags, ``validate`` reasons, cache shape, and ``forward`` dispatch, restated so that
 this package stands alone. In a lean-vLLM checkout the MI355X backend is registered against the reference's
-own base class instead (the method set is identical); see the integration notes shipped with this package.
+own base class instead (the method set is identical).
 """
 
 from __future__ import annotations
