@@ -85,7 +85,7 @@ int lv_store_latents(const void* latent, int64_t latent_stride_t, int32_t num_to
  * Query j of a row with lq queries and lk keys sees keys 0 .. lk-lq+j (bottom-right causal).
  * A row with no keys gets a zero output.
  * max_seqlen_k bounds every row's key length (block-table width * block_size will do); it sizes the split-K grid
- * so a captured graph needs no length read back. num_tokens_upper bounds T for the work list (use T).
+ * so a captured graph needs no length read back. num_tokens is T (it sizes the work list).
  * workspace: caller-owned device memory of at least lv_paged_attention_workspace_bytes(...) bytes for the same
  * arguments; its contents need no initialisation. */
 size_t lv_paged_attention_workspace_bytes(int32_t num_rows, int32_t num_tokens, int32_t num_heads,
@@ -99,6 +99,24 @@ int lv_paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h, co
                        int32_t num_kv_heads, int32_t head_dim, float scale, int32_t max_seqlen_q,
                        int32_t max_seqlen_k, void* out, int64_t out_stride_t, int64_t out_stride_h,
                        void* workspace, size_t workspace_bytes, int32_t dtype, void* stream);
+
+/* ---------------------------------------------------------------------------------------------------------
+ * Attention over packed keys (no pages). Replaces AttentionBackend.prefill without block tables and
+ * AttentionBackend.varlen_with_lse (lean_vllm/attention/abstract.py:148-164,187-204; math of TorchAttention.prefill
+ * and varlen_with_lse, lean_vllm/attention/torch_backend.py:62-91): the warmup prefill and MLA prefill chunks.
+ *
+ * q: [T, Hq, head_dim_qk], k: [Tk, Hkv, head_dim_qk], v: [Tk, Hkv, head_dim_v], each with its own token and head
+ * strides (elements) and unit dim stride; rows given by cu_seqlens_q / cu_seqlens_k [num_rows + 1] (device).
+ * causal != 0: query j of a row with lq queries and lk keys sees keys 0 .. lk - lq + j; else all of its row's keys.
+ * out: [T, Hq, head_dim_v]. lse (optional, may be NULL): fp32 [T, Hq] natural log-sum-exp of each query row's
+ * scaled scores (-inf for a row with no keys). max_seqlen_q bounds every row's query count (it sizes the grid).
+ * (head_dim_qk, head_dim_v) in {(64, 64), (128, 128), (192, 128), (192, 192)}. No workspace. */
+int lv_varlen_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k, int64_t k_stride_t,
+                        int64_t k_stride_h, const void* v, int64_t v_stride_t, int64_t v_stride_h,
+                        const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int32_t num_rows, int32_t num_heads,
+                        int32_t num_kv_heads, int32_t head_dim_qk, int32_t head_dim_v, float scale, int32_t causal,
+                        int32_t max_seqlen_q, void* out, int64_t out_stride_t, int64_t out_stride_h, float* lse,
+                        int64_t lse_stride_t, int64_t lse_stride_h, int32_t dtype, void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------
  * MLA absorbed decode. Replaces AttentionBackend.mla_decode (lean_vllm/attention/abstract.py:206-219; math of

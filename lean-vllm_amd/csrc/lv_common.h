@@ -176,6 +176,17 @@ __device__ inline u32x4 ld16_stream(const char* ptr) {
 }
 __device__ inline void st16(char* ptr, u32x4 v) { *reinterpret_cast<u32x4*>(ptr) = v; }
 
+// Transposing LDS read (ds_read_b64_tr_b16): each group of 16 lanes reads a 4 x 16 tile of 16-bit values, lane
+// 4 * row + quad addressing 4 consecutive elements of one row; lane i of the group receives column i (4 values,
+// one per row) -- the operand layout of an MFMA whose reduction runs along the tile's rows.
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+__device__ inline u32x2 lds_read_tr16(const uint16_t* p) {
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+  return __builtin_bit_cast(u32x2, v);
+}
+
 // ---------------------------------------------------------------------------------------------------------
 // Cross-row lane exchange.
 

@@ -52,16 +52,6 @@ struct MlaParams {
   float* part_lse;  // [rows * lq][heads][max_splits], log2 domain
 };
 
-typedef short i16x4 __attribute__((ext_vector_type(4)));
-
-// Column (lane % 16) of the 4 x 16 tile of 16-bit values whose rows the 16 lanes of the group address, 4
-// consecutive elements per lane (lane = 4 * row + column quad).
-__device__ inline u32x2 lds_read_tr16(const uint16_t* p) {
-  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
-  const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
-  return __builtin_bit_cast(u32x2, v);
-}
-
 template <typename T>
 __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
   using E = Elem<T>;

@@ -6,23 +6,18 @@
 //                  head row (D elements) is spread over 16 lanes as 16-byte loads; q.k by v_dot2 with a DPP
 //                  butterfly inside the 16-lane row; online softmax per tile; p.v on the VALU in fp32. The four
 //                  waves and, for long rows, the splits are merged by log-sum-exp.
-//   prefill item = (row, q tile, kv head): a row with several queries. 64 (position, head) query rows of one GQA
-//                  group against 64-key tiles staged in LDS: S^T = K Q^T and O^T += V^T P^T on MFMA 16x16x32,
-//                  bottom-right causal mask, online softmax per query row.
-// A pure-decode launch maps blockIdx.x to (row, split) directly; a mixed launch reads a work list built on the
-// device by plan_kernel from cu_seqlens_q and the key lengths (prefill items first). Rows whose keys were split
-// are combined by splitk_merge_kernel.
+//   prompt item  = (row, q tile, kv head): a row with several queries; the MFMA tile of attn_common.h.
+// Launches read a work list built on the device by plan_kernel from the key lengths (and cu_seqlens_q), longest
+// work first. Rows whose keys were split are combined by splitk_merge_kernel.
 //
 // Math: TorchAttention.decode / prefill (lean_vllm/attention/torch_backend.py:62-103,159-181): query head h reads
 // key head h / (Hq/Hkv); query j of a row with lq queries and lk keys sees keys 0..lk-lq+j.
-#include "lv_common.h"
+#include "attn_common.h"
 
 namespace lv {
 
 constexpr int kTile = 16;          // decode tokens per tile; block sizes are multiples of 16, so a tile sits in one block
 constexpr int kWaves = 4;          // waves per workgroup
-constexpr int kPrefillKeys = 64;   // keys per prefill tile
-constexpr int kPrefillRows = 64;   // (position, head) query rows per prefill item, 16 per wave
 constexpr int kPlanMaxRows = 4096;  // rows of a step with prompts (the work-list scan lives in LDS)
 
 #ifndef LV_DECODE_PIPE
@@ -34,35 +29,6 @@ constexpr int kPlanMaxRows = 4096;  // rows of a step with prompts (the work-lis
 #ifndef LV_MIN_SPLIT
 #define LV_MIN_SPLIT 256
 #endif
-
-struct AttnParams {
-  const char* q;
-  int64_t q_st, q_sh;  // bytes
-  const char* k_cache;
-  const char* v_cache;
-  int64_t c_sb, c_st, c_sh;  // bytes
-  FastDiv bs;  // tokens per page
-  const int32_t* tables;
-  int64_t t_stride;  // elements
-  const int32_t* cu_q;
-  const int32_t* lens_k;
-  const int32_t* cu_k;
-  int32_t rows, hq, hkv, group, qgroups;
-  float scale_log2;  // softmax scale * log2(e): scores live in the exp2 domain
-  char* out;
-  int64_t o_st, o_sh;  // bytes
-  int32_t split;       // S: keys per decode item
-  int32_t max_splits;
-  float* part_o;    // [rows][hq][max_splits][D] normalised partial outputs
-  float* part_lse;  // [rows][hq][max_splits] log2-sum-exp2 of the partials
-  const int2* items;
-  const int32_t* n_items;
-};
-
-__device__ inline int key_len(const AttnParams& p, int row) {
-  return p.lens_k ? p.lens_k[row] : p.cu_k[row + 1] - p.cu_k[row];
-}
-
 
 // ---------------------------------------------------------------------------------------------------------
 // Decode item.
@@ -343,159 +309,12 @@ __device__ void decode_item(const AttnParams& p, int row, int split, int kvh, in
 }
 
 // ---------------------------------------------------------------------------------------------------------
-// Prefill item (MFMA).
-
-// LDS swizzle of the transposed value tile: key k of dim row d sits at k ^ (4 * vt_swz(d)). Conflict-free for
-// both the transposing 16-bit writes (fixed d % 8, varying d / 8) and the 8-byte MFMA operand reads
-// (fixed d % 2 and d / 16, varying d / 2 % 8).
-__device__ inline int vt_swz(int d) {
-  return ((d >> 4) & 1) | ((((d >> 1) ^ (d >> 5)) & 1) << 1) | ((((d >> 2) ^ (d >> 6)) & 1) << 2) |
-         (((d >> 3) & 1) << 3);
-}
-
-template <int D>
-struct PrefillSmem {
-  static constexpr int kRow = D + 8;  // key tile row, elements (pad: conflict-free operand reads)
-  static constexpr int kBytes = kPrefillKeys * kRow * 2 + D * kPrefillKeys * 2;
-};
-
-template <typename T, int D>
-__device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, char* smem) {
-  using E = Elem<T>;
-  constexpr int KS = D / 32;  // MFMA k-steps over the head dim
-  constexpr int DB = D / 16;  // 16-dim blocks of the output
-  constexpr int ROW = PrefillSmem<D>::kRow;
-  uint16_t* ks_lds = reinterpret_cast<uint16_t*>(smem);          // [64 keys][ROW]
-  uint16_t* vt_lds = ks_lds + kPrefillKeys * ROW;                // [D][64 keys], swizzled
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int n = lane & 15, j4 = lane >> 4;
-  const int G = p.group;
-  const int qp = kPrefillRows / G;  // positions per item
-  const int q0 = p.cu_q[row], lq = p.cu_q[row + 1] - q0;
-  const int lk = key_len(p, row);
-  const int p0 = qtile * qp;
-
-  const int mrow = wave * 16 + n;
-  const int qi = p0 + mrow / G;
-  const int head = kvh * G + mrow % G;
-  const bool qvalid = mrow < qp * G && qi < lq;
-  u32x4 qb[KS];
-#pragma unroll
-  for (int k = 0; k < KS; ++k)
-    qb[k] = qvalid ? ld16(p.q + (int64_t)(q0 + qi) * p.q_st + head * p.q_sh + (int64_t)(32 * k + 8 * j4) * 2)
-                   : u32x4{0, 0, 0, 0};
-  const int lim = qvalid ? lk - lq + qi + 1 : lk;  // this query row sees keys < lim
-  const int kmax = min(lk, lk - lq + min(p0 + qp, lq));
-
-  float mrun = -INFINITY, lrun = 0.f;
-  f32x4 o[DB];
-#pragma unroll
-  for (int b = 0; b < DB; ++b) o[b] = f32x4{0, 0, 0, 0};
-
-  const int32_t* table = p.tables + (int64_t)row * p.t_stride;
-  constexpr int CPK = D / 8;  // 16-byte chunks per key head row
-  for (int kt = 0; kt < kmax; kt += kPrefillKeys) {
-    __syncthreads();  // the previous tile's operand reads are done
-    for (int c = tid; c < kPrefillKeys * CPK; c += blockDim.x) {
-      const int key = c / CPK, part = c % CPK;
-      const int jk = kt + key;
-      u32x4 kk = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
-      if (jk < lk) {
-        const int pg = (int)p.bs.div(jk);
-        const int64_t off = (int64_t)table[pg] * p.c_sb + (int64_t)(jk - pg * (int)p.bs.d) * p.c_st +
-                            (int64_t)kvh * p.c_sh + part * 16;
-        kk = ld16(p.k_cache + off);
-        vv = ld16(p.v_cache + off);
-      }
-      st16(reinterpret_cast<char*>(ks_lds + key * ROW + part * 8), kk);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int d = part * 8 + e;
-        const uint16_t x = (uint16_t)(vv[e >> 1] >> ((e & 1) * 16));
-        vt_lds[d * kPrefillKeys + (key ^ (4 * vt_swz(d)))] = x;
-      }
-    }
-    __syncthreads();
-
-    // S^T (keys x query rows): lane holds keys kt + 16*kb + 4*j4 + r of query row n.
-    f32x4 st[4];
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      st[kb] = f32x4{0, 0, 0, 0};
-#pragma unroll
-      for (int k = 0; k < KS; ++k) {
-        const u32x4 a = *reinterpret_cast<const u32x4*>(ks_lds + (kb * 16 + n) * ROW + 32 * k + 8 * j4);
-        st[kb] = E::mfma16x16x32(a, qb[k], st[kb]);
-      }
-    }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = kt + kb * 16 + 4 * j4 + r;
-        const float s = key < lim ? st[kb][r] * p.scale_log2 : -INFINITY;
-        st[kb][r] = s;
-        mx = fmaxf(mx, s);
-      }
-    mx = fmaxf(mx, shfl_xor(mx, 16));
-    mx = fmaxf(mx, shfl_xor(mx, 32));
-    const float mnew = fmaxf(mrun, mx);
-    const float mref = mnew == -INFINITY ? 0.f : mnew;
-    const float alpha = fast_exp2(mrun - mref);
-    mrun = mnew;
-    float psum = 0.f;
-    u32x4 pb[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      float pr[8];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        pr[r] = fast_exp2(st[2 * h][r] - mref);
-        pr[4 + r] = fast_exp2(st[2 * h + 1][r] - mref);
-      }
-#pragma unroll
-      for (int r = 0; r < 8; ++r) psum += pr[r];
-#pragma unroll
-      for (int w = 0; w < 4; ++w) pb[h][w] = E::pack(pr[2 * w], pr[2 * w + 1]);
-    }
-    lrun = lrun * alpha + psum;
-#pragma unroll
-    for (int b = 0; b < DB; ++b) {
-      o[b] *= alpha;
-      const int d = b * 16 + n;
-      const uint16_t* vrow = vt_lds + d * kPrefillKeys;
-      const int sw = 4 * vt_swz(d);
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow + ((32 * h + 4 * j4) ^ sw));
-        const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + ((32 * h + 16 + 4 * j4) ^ sw));
-        const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
-        o[b] = E::mfma16x16x32(a, pb[h], o[b]);
-      }
-    }
-  }
-
-  lrun += shfl_xor(lrun, 16);
-  lrun += shfl_xor(lrun, 32);
-  if (qvalid) {
-    const float inv = lrun > 0.f ? 1.f / lrun : 0.f;
-    char* dst = p.out + (int64_t)(q0 + qi) * p.o_st + head * p.o_sh;
-#pragma unroll
-    for (int b = 0; b < DB; ++b) {
-      u32x2 packed = {E::pack(o[b][0] * inv, o[b][1] * inv), E::pack(o[b][2] * inv, o[b][3] * inv)};
-      *reinterpret_cast<u32x2*>(dst + (int64_t)(b * 16 + 4 * j4) * 2) = packed;
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------------------------------------
 // Kernels.
 
 template <int D, int GS>
 struct SmemBytes {
   static constexpr int kDecode = kWaves * GS * (D + 2) * 4;
-  static constexpr int kPrefill = PrefillSmem<D>::kBytes;
+  static constexpr int kPrefill = PromptSmem<D, D>::kBytes;
   static constexpr int kMixed = kDecode > kPrefill ? kDecode : kPrefill;
 };
 
@@ -515,7 +334,7 @@ __global__ __launch_bounds__(256) void paged_attention_kernel(AttnParams p) {
     if (!MIXED || it.y >= 0)
       decode_item<T, D, GS>(p, it.x, it.y, kvh, qg, smem);
     else if (qg == 0)
-      prefill_item<T, D>(p, it.x, -1 - it.y, kvh, smem);
+      prefill_item<T, D, D>(p, it.x, -1 - it.y, kvh, smem);
   } else {
     const int kvh = blockIdx.y / p.qgroups, qg = blockIdx.y % p.qgroups;
     decode_item<T, D, GS>(p, blockIdx.x / p.max_splits, blockIdx.x % p.max_splits, kvh, qg, smem);
@@ -766,6 +585,10 @@ extern "C" int lv_paged_attention(const void* q, int64_t q_stride_t, int64_t q_s
   p.c_sb = cache_stride_block * 2;
   p.c_st = cache_stride_token * 2;
   p.c_sh = cache_stride_head * 2;
+  p.v_st = p.c_st;
+  p.v_sh = p.c_sh;
+  p.paged = true;
+  p.causal = 1;
   p.bs = FastDiv::make((uint32_t)block_size);
   p.tables = block_tables;
   p.t_stride = table_stride;

@@ -2,11 +2,13 @@
 
 - ``MI355XAttention``: the per-layer attention backend (store_kvcache, decode, prefill, mixed steps).
 - ``Packer``: the ragged-batch packing of a step on the GPU.
+- ``merge_attention`` / ``merge_attention_``: the log-sum-exp merge of two partial attentions.
 - ``Context``, ``LayerSpec``, ``AttentionBackend``, ``get_attention_backend``: the reference's interface.
 """
 
 from .abstract import AttentionBackend, LayerSpec, write_into
 from .backend import MI355XAttention
+from .merge import merge_attention, merge_attention_
 from .context import Context, get_context, reset_context, set_context, split_decodes_and_prefills, use_context
 from .pack import Packer, StagingBuffers, decode_query_len
 from .selector import BACKENDS, get_attention_backend
@@ -22,6 +24,8 @@ __all__ = [
     "decode_query_len",
     "get_attention_backend",
     "get_context",
+    "merge_attention",
+    "merge_attention_",
     "reset_context",
     "set_context",
     "split_decodes_and_prefills",

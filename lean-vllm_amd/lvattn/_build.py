@@ -18,7 +18,7 @@ CSRC = PACKAGE_DIR.parent / "csrc"
 INCLUDE = PACKAGE_DIR.parent.parent / "include"
 LIBRARY = PACKAGE_DIR / "liblvattn.so"
 BUILD_DIR = PACKAGE_DIR.parent / "_build"
-SOURCES = ("capi.hip", "store.hip", "pack.hip", "paged_attention.hip", "merge.hip", "mla_decode.hip")
+SOURCES = ("capi.hip", "store.hip", "pack.hip", "paged_attention.hip", "merge.hip", "mla_decode.hip", "varlen.hip")
 ARCH = "gfx950"
 
 

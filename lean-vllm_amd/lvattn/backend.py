@@ -54,7 +54,7 @@ class MI355XAttention(AttentionBackend):
     """Paged attention, cache stores and MLA latent decode on MI355X (gfx950) HIP kernels."""
 
     supported_dtypes = (torch.float16, torch.bfloat16)
-    supported_kinds = ("decoder",)
+    supported_kinds = ("decoder", "mla")
 
     @staticmethod
     def get_name() -> str:
@@ -78,13 +78,18 @@ class MI355XAttention(AttentionBackend):
 
     @staticmethod
     def supports_head_size(head_size: int) -> bool:
-        return head_size in (64, 128)
+        return head_size in (64, 128, 192)
 
     @classmethod
     def validate(cls, spec) -> list[str]:
         reasons = super().validate(spec)
-        if spec.kind == "decoder" and spec.num_kv_heads and spec.num_heads // max(spec.num_kv_heads, 1) > 64:
-            reasons.append(f"{spec.num_heads // spec.num_kv_heads} query heads per key head exceed 64")
+        if spec.kind == "decoder":
+            if spec.head_size == 192:
+                reasons.append("head size 192 is served for MLA layers (192-wide q.k, 128-wide values) only")
+            if spec.num_kv_heads and spec.num_heads // max(spec.num_kv_heads, 1) > 64:
+                reasons.append(f"{spec.num_heads // spec.num_kv_heads} query heads per key head exceed 64")
+        elif spec.kind == "mla" and spec.latent_dim != 576:
+            reasons.append(f"MLA latent width {spec.latent_dim} is not 576 (kv_lora_rank 512 + rope 64)")
         return reasons
 
     @staticmethod
@@ -155,8 +160,10 @@ class MI355XAttention(AttentionBackend):
         rows of one query take the streaming decode path inside the same launch."""
         cu_q, cu_k = context.cu_seqlens_q, context.cu_seqlens_k
         assert cu_q is not None and cu_k is not None
-        if context.block_tables is None:
-            raise NotImplementedError("the mi355x backend reads keys from the paged cache; pass block_tables")
+        if context.block_tables is None:  # warmup, or an MLA prompt with no cached context: keys are k, v
+            max_q = context.max_seqlen_q or q.size(0)
+            o, _ = self._varlen(q, k, v, cu_q, cu_k, max_q, causal=True, want_lse=False, out=out)
+            return o
         bt = context.block_tables
         max_k = context.max_seqlen_k or bt.size(1) * k_cache.size(1)
         max_q = context.max_seqlen_q or q.size(0)
@@ -192,3 +199,29 @@ class MI355XAttention(AttentionBackend):
                    out.stride(0), out.stride(1), _capi.ptr(ws), 0 if ws is None else ws.numel(),
                    _capi.DTYPES[q.dtype], _capi.stream_of(q.device))
         return out
+
+    # -- packed keys (no pages) ----------------------------------------------------------------------------
+    def _varlen(self, q, k, v, cu_q, cu_k, max_q, *, causal: bool, want_lse: bool, out=None):
+        assert q.dtype in _capi.DTYPES and k.dtype == q.dtype == v.dtype
+        assert q.stride(-1) == 1 and k.stride(-1) == 1 and v.stride(-1) == 1
+        tokens, heads, dqk = q.shape
+        dv = v.size(-1)
+        cu_q = cu_q if cu_q.dtype == torch.int32 else cu_q.to(torch.int32)
+        cu_k = cu_k if cu_k.dtype == torch.int32 else cu_k.to(torch.int32)
+        if out is None:
+            out = torch.empty(tokens, heads, dv, dtype=q.dtype, device=q.device)
+        assert out.shape == (tokens, heads, dv) and out.stride(-1) == 1 and out.dtype == q.dtype
+        lse = torch.empty(tokens, heads, dtype=torch.float32, device=q.device) if want_lse else None
+        _capi.call("lv_varlen_attention", q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0),
+                   k.stride(1), v.data_ptr(), v.stride(0), v.stride(1), cu_q.data_ptr(), cu_k.data_ptr(),
+                   cu_q.numel() - 1, heads, k.size(1), dqk, dv, float(self.scale), int(causal), int(max_q),
+                   out.data_ptr(), out.stride(0), out.stride(1), _capi.ptr(lse), heads if want_lse else 0,
+                   1 if want_lse else 0, _capi.DTYPES[q.dtype], _capi.stream_of(q.device))
+        return out, lse
+
+    def varlen_with_lse(self, q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, causal,
+                        host_cu_seqlens=None):
+        """Attention over packed keys, bottom-right causal or unmasked, plus the natural log-sum-exp ``[T, H]`` of
+        every query row for merging (``abstract.py:187-204``); -inf for a row with no keys. ``host_cu_seqlens``
+        is not needed: the grid is sized from ``max_seqlen_q``."""
+        return self._varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, causal=causal, want_lse=True)

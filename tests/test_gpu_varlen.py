@@ -1,0 +1,168 @@
+"""Attention over packed keys (prefill without block tables, varlen_with_lse) and the log-sum-exp merge on the GPU.
+
+Cases of the reference's tests (tests/test_attention_backends.py:171-263, 266-287): rows of 5, 1 and 12 queries;
+causal and unmasked chunks that hold more keys than queries; MLA prefill's 192-wide q.k with 128-wide values
+handed over as a view of a wider tensor; the merge in place and into a strided output with lse in a transposed
+layout and a row with no keys. Expected values: the textbook dense oracle in fp32 (outputs and natural lse).
+Tolerances: fp16 6e-3, bf16 2e-2 / 1e-2.
+"""
+
+import pytest
+import torch
+
+from lvattn import Context, MI355XAttention, merge_attention, merge_attention_
+from oracle import attention as A
+
+pytestmark = pytest.mark.gpu
+
+H, HKV, SCALE = 8, 2, 0.137
+TOL = {torch.float16: dict(atol=6e-3, rtol=6e-3), torch.bfloat16: dict(atol=2e-2, rtol=1e-2)}
+CASES = [(torch.float16, 64), (torch.bfloat16, 64), (torch.bfloat16, 128)]
+IDS = ["fp16-d64", "bf16-d64", "bf16-d128"]
+
+
+def rnd(*shape, gen, dtype, device):
+    return torch.randn(*shape, generator=gen).to(dtype).to(device)
+
+
+def cumulative(lens, device):
+    return torch.tensor([0, *torch.tensor(lens).cumsum(0).tolist()], dtype=torch.int32, device=device)
+
+
+def dense_rows(qs, ks, vs, causal, scale=SCALE):
+    out = torch.cat([A.dense_attention(q.cpu().float(), k.cpu().float(), v.cpu().float(), scale, causal=causal)
+                     for q, k, v in zip(qs, ks, vs)])
+    lse = torch.cat([A.dense_scores(q.cpu().float(), k.cpu().float(), scale, causal=causal).logsumexp(-1).T
+                     for q, k in zip(qs, ks)])
+    return out, lse
+
+
+@pytest.mark.parametrize("dtype, dim", CASES, ids=IDS)
+def test_prefill_without_cache(cuda, dtype, dim):
+    gen = torch.Generator().manual_seed(0)
+    lens = [5, 1, 12]
+    qs = [rnd(n, H, dim, gen=gen, dtype=dtype, device=cuda) for n in lens]
+    ks = [rnd(n, HKV, dim, gen=gen, dtype=dtype, device=cuda) for n in lens]
+    vs = [rnd(n, HKV, dim, gen=gen, dtype=dtype, device=cuda) for n in lens]
+    cu = cumulative(lens, cuda)
+    ctx = Context(is_prefill=True, cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=max(lens), max_seqlen_k=max(lens))
+    empty = torch.tensor([], dtype=dtype, device=cuda)
+    b = MI355XAttention(H, dim, SCALE, HKV)
+    out = b.forward(torch.cat(qs), torch.cat(ks), torch.cat(vs), empty, empty, ctx)
+    torch.testing.assert_close(out.float().cpu(), dense_rows(qs, ks, vs, True)[0], **TOL[dtype])
+
+
+@pytest.mark.parametrize("causal", [True, False], ids=["causal", "unmasked"])
+@pytest.mark.parametrize("dtype, dim", CASES, ids=IDS)
+def test_varlen_with_lse(cuda, dtype, dim, causal):
+    gen = torch.Generator().manual_seed(1)
+    lens_q = [5, 1, 12]
+    lens_k = lens_q if causal else [7, 4, 16]
+    qs = [rnd(n, H, dim, gen=gen, dtype=dtype, device=cuda) for n in lens_q]
+    ks = [rnd(n, HKV, dim, gen=gen, dtype=dtype, device=cuda) for n in lens_k]
+    vs = [rnd(n, HKV, dim, gen=gen, dtype=dtype, device=cuda) for n in lens_k]
+    out, lse = MI355XAttention(H, dim, SCALE, HKV).varlen_with_lse(
+        torch.cat(qs), torch.cat(ks), torch.cat(vs), cumulative(lens_q, cuda), cumulative(lens_k, cuda),
+        max(lens_q), max(lens_k), causal)
+    want, want_lse = dense_rows(qs, ks, vs, causal)
+    assert lse.dtype == torch.float32 and lse.shape == (sum(lens_q), H)
+    torch.testing.assert_close(out.float().cpu(), want, **TOL[dtype])
+    torch.testing.assert_close(lse.cpu(), want_lse, **TOL[dtype])
+
+
+@pytest.mark.parametrize("causal", [True, False], ids=["causal", "unmasked"])
+def test_narrow_values_match_padded_ones(cuda, causal):
+    """192-wide q.k with 128-wide values given as a view of a wider tensor, as MLA prefill hands them over."""
+    dtype, heads, qk, vd = torch.bfloat16, 16, 192, 128
+    gen = torch.Generator().manual_seed(2)
+    lens_q = [5, 1, 12, 200]
+    lens_k = lens_q if causal else [7, 4, 16, 333]
+    q = rnd(sum(lens_q), heads, qk, gen=gen, dtype=dtype, device=cuda)
+    k = rnd(sum(lens_k), heads, qk, gen=gen, dtype=dtype, device=cuda)
+    v = rnd(sum(lens_k), heads, qk, gen=gen, dtype=dtype, device=cuda)[..., :vd]
+    padded = torch.nn.functional.pad(v, (0, qk - vd))
+    b = MI355XAttention(heads, qk, SCALE, heads)
+    args = (cumulative(lens_q, cuda), cumulative(lens_k, cuda), max(lens_q), max(lens_k), causal)
+    out, lse = b.varlen_with_lse(q, k, v, *args)
+    wide, wide_lse = b.varlen_with_lse(q, k, padded, *args)
+    assert out.shape[-1] == vd
+    torch.testing.assert_close(out, wide[..., :vd], **TOL[dtype])
+    torch.testing.assert_close(lse, wide_lse, **TOL[dtype])
+    split = lambda x, lens: list(torch.split(x, lens))  # noqa: E731
+    want, want_lse = dense_rows(split(q, lens_q), split(k, lens_k), split(v, lens_k), causal)
+    torch.testing.assert_close(out.float().cpu(), want, **TOL[dtype])
+    torch.testing.assert_close(lse.cpu(), want_lse, **TOL[dtype])
+    if causal:
+        ctx = Context(is_prefill=True, cu_seqlens_q=args[0], cu_seqlens_k=args[1], max_seqlen_q=args[2],
+                      max_seqlen_k=args[3])
+        empty = torch.tensor([], dtype=dtype, device=cuda)
+        torch.testing.assert_close(b.prefill(q, k, v, empty, empty, ctx), out, atol=0, rtol=0)
+
+
+def test_mla_prefill_shape_against_the_torch_restatement(cuda):
+    """DeepSeek-V2-Lite's expanded prefill (16 heads, 192/128) on a 1536-token chunk beside short rows."""
+    dtype, heads, qk, vd = torch.bfloat16, 16, 192, 128
+    gen = torch.Generator().manual_seed(3)
+    lens = [1536, 3, 400]
+    q = rnd(sum(lens), heads, qk, gen=gen, dtype=dtype, device=cuda)
+    k = rnd(sum(lens), heads, qk, gen=gen, dtype=dtype, device=cuda)
+    v = rnd(sum(lens), heads, vd, gen=gen, dtype=dtype, device=cuda)
+    cu = cumulative(lens, cuda)
+    out, lse = MI355XAttention(heads, qk, 1 / 192 ** 0.5, heads).varlen_with_lse(q, k, v, cu, cu, max(lens),
+                                                                                 max(lens), True)
+    m = A.TorchMath(heads, qk, 1 / 192 ** 0.5, heads)
+    want, want_lse = m.varlen_with_lse(q.cpu(), k.cpu(), v.cpu(), cu.cpu(), cu.cpu(), max(lens), max(lens), True)
+    torch.testing.assert_close(out.float().cpu(), want, **TOL[dtype])
+    torch.testing.assert_close(lse.cpu(), want_lse, **TOL[dtype])
+
+
+def test_rows_without_keys_give_zero_and_minus_infinity(cuda):
+    gen = torch.Generator().manual_seed(4)
+    q = rnd(4, H, 64, gen=gen, dtype=torch.bfloat16, device=cuda)
+    k = rnd(3, HKV, 64, gen=gen, dtype=torch.bfloat16, device=cuda)
+    v = rnd(3, HKV, 64, gen=gen, dtype=torch.bfloat16, device=cuda)
+    out, lse = MI355XAttention(H, 64, SCALE, HKV).varlen_with_lse(
+        q, k, v, cumulative([2, 2], cuda), cumulative([0, 3], cuda), 2, 3, False)
+    assert torch.equal(out[:2], torch.zeros_like(out[:2]))
+    assert torch.isneginf(lse[:2]).all() and torch.isfinite(lse[2:]).all()
+
+
+def test_merge_of_a_split_equals_the_whole(cuda):
+    """Unmasked attention over a row's keys == the merge of attention over its two halves."""
+    gen = torch.Generator().manual_seed(5)
+    q = rnd(6, H, 128, gen=gen, dtype=torch.bfloat16, device=cuda)
+    k = rnd(40, HKV, 128, gen=gen, dtype=torch.bfloat16, device=cuda)
+    v = rnd(40, HKV, 128, gen=gen, dtype=torch.bfloat16, device=cuda)
+    b = MI355XAttention(H, 128, SCALE, HKV)
+    cq = cumulative([6], cuda)
+    whole, whole_lse = b.varlen_with_lse(q, k, v, cq, cumulative([40], cuda), 6, 40, False)
+    o_a, lse_a = b.varlen_with_lse(q, k[:17], v[:17], cq, cumulative([17], cuda), 6, 17, False)
+    o_b, lse_b = b.varlen_with_lse(q, k[17:], v[17:], cq, cumulative([23], cuda), 6, 23, False)
+    merge_attention_(o_a, lse_a, o_b, lse_b)
+    torch.testing.assert_close(o_a, whole, **TOL[torch.bfloat16])
+    torch.testing.assert_close(lse_a, whole_lse, atol=1e-4, rtol=1e-4)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("into", [False, True], ids=["in_place", "into_out"])
+def test_merge_matches_the_oracle(cuda, dtype, into):
+    """In place or into an output strided as a split's rows, with lse in a transposed layout and a row whose lse
+    is -inf (no cached keys), as tests/test_attention_backends.py:266-287."""
+    gen = torch.Generator().manual_seed(6)
+    tokens, heads, dim = 37, 16, 128
+    o_a = rnd(tokens, heads, dim, gen=gen, dtype=dtype, device=cuda)
+    o_b = rnd(tokens, heads, dim, gen=gen, dtype=dtype, device=cuda)
+    lse_a = (torch.randn(heads, tokens, generator=gen) * 3).to(cuda).T
+    lse_b = (torch.randn(heads, tokens, generator=gen) * 3).to(cuda).T
+    lse_a[0] = float("-inf")
+    want_o, want_lse = A.merge_attention(o_a.cpu(), lse_a.cpu(), o_b.cpu(), lse_b.cpu())
+    got_o, got_lse = merge_attention(o_a, lse_a, o_b, lse_b)
+    torch.testing.assert_close(got_o.float().cpu(), want_o, atol=1e-2, rtol=1e-2)
+    torch.testing.assert_close(got_lse.cpu(), want_lse)
+    before = o_a.clone()
+    out = torch.empty(tokens + 3, heads, dim, dtype=dtype, device=cuda)[3:] if into else None
+    merge_attention_(o_a, lse_a, o_b, lse_b, out)
+    torch.testing.assert_close((o_a if out is None else out).float().cpu(), want_o, atol=1e-2, rtol=1e-2)
+    torch.testing.assert_close(lse_a.cpu(), want_lse)
+    if into:
+        assert torch.equal(o_a, before)
