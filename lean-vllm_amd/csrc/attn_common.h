@@ -6,7 +6,7 @@
 namespace lv {
 
 constexpr int kPrefillKeys = 64;  // keys per prompt tile
-constexpr int kPrefillRows = 64;  // (position, head) query rows per prompt item, 16 per wave
+constexpr int kPrefillRows = 128;  // (position, head) query rows per prompt item, 32 per wave
 
 struct AttnParams {
   const char* q;
@@ -42,12 +42,17 @@ __device__ inline int key_len(const AttnParams& p, int row) {
 }
 
 // ---------------------------------------------------------------------------------------------------------
-// Prompt item: (row, tile of query positions, kv head). The 64 (position, head) query rows of one GQA group
-// (16 per wave) run against 64-key tiles staged row-major in LDS, the next tile's K/V loads in flight in
-// registers meanwhile. S^T = K Q^T and O^T += V^T P^T on MFMA 16x16x32 with fp32 accumulation; the V^T
-// operands come from the row-major value tile by the transposing LDS read. Online softmax per query row;
-// bottom-right causal mask (query j of a row with lq queries and lk keys sees keys 0 .. lk - lq + j) unless
-// p.causal is 0. DQK: q.k width; DV: value width.
+// Prompt item: (row, tile of query positions, kv head). The 128 (position, head) query rows of one GQA group (32
+// per wave, as two 16-row MFMA blocks that share every K and V operand read) run against 64-key tiles staged
+// row-major in LDS, the next tile's K/V loads in flight in registers meanwhile. S^T = K Q^T and O^T += V^T P^T on
+// MFMA 16x16x32 with fp32 accumulation; the V^T operands come from the row-major value tile by the transposing
+// LDS read. Online softmax per query row with the scale folded into the exp2 argument; the running max is
+// replaced only when a tile raises it by more than kRescaleSlack (log2 units), so rescaling the accumulators is
+// rare and probabilities stay <= 2^kRescaleSlack. The causal mask (query j of a row with lq queries and lk keys
+// sees keys 0 .. lk - lq + j; none if p.causal is 0) is applied only on tiles that cross it.
+// DQK: q.k width; DV: value width.
+
+constexpr float kRescaleSlack = 8.f;
 
 template <int DQK, int DV>
 struct PromptSmem {
@@ -56,7 +61,8 @@ struct PromptSmem {
   static constexpr int kBytes = kPrefillKeys * (kKRow + kVRow) * 2;
 };
 
-template <typename T, int DQK, int DV>
+// PREFETCH: the next tile's K/V loads are in flight in registers while this tile is consumed (more registers).
+template <typename T, int DQK, int DV, bool PREFETCH = true>
 __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, char* smem) {
   using E = Elem<T>;
   constexpr int KS = DQK / 32;  // MFMA k-steps over the q.k width
@@ -65,8 +71,9 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
   constexpr int VROW = PromptSmem<DQK, DV>::kVRow;
   constexpr int KCH = DQK / 8, VCH = DV / 8;  // 16-byte chunks per key / value row
   constexpr int KCHUNKS = kPrefillKeys * KCH;
-  constexpr int PER = kPrefillKeys * (KCH + VCH) / 256;  // chunks each thread stages per tile
-  static_assert(kPrefillKeys * (KCH + VCH) % 256 == 0, "tile chunks split evenly over 256 threads");
+  constexpr int KPER = KCHUNKS / 256;                   // key chunks each thread stages per tile
+  constexpr int PER = kPrefillKeys * (KCH + VCH) / 256;  // all chunks each thread stages per tile
+  static_assert(KCHUNKS % 256 == 0 && kPrefillKeys * (KCH + VCH) % 256 == 0, "tile chunks split over 256 threads");
   static_assert(DQK % 32 == 0 && DV % 16 == 0, "MFMA tile widths");
   uint16_t* ks = reinterpret_cast<uint16_t*>(smem);  // [64 keys][KROW]
   uint16_t* vs = ks + kPrefillKeys * KROW;            // [64 keys][VROW]
@@ -79,27 +86,42 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
   const int lk = key_len(p, row);
   const int p0 = qtile * qp;
   if (p0 >= lq) return;  // a grid sized for the longest row
+  const float c = p.scale_log2;
 
-  const int mrow = wave * 16 + n;
-  const int qi = p0 + mrow / G;
-  const int head = kvh * G + mrow % G;
-  const bool qvalid = mrow < qp * G && qi < lq;
-  u32x4 qb[KS];
+  // Two 16-row query blocks per wave: rows 32 wave + 16 nb + n.
+  int qi[2], head[2], lim[2];
+  bool qvalid[2];
+  u32x4 qb[2][KS];
 #pragma unroll
-  for (int k = 0; k < KS; ++k)
-    qb[k] = qvalid ? ld16(p.q + (int64_t)(q0 + qi) * p.q_st + head * p.q_sh + (int64_t)(32 * k + 8 * j4) * 2)
-                   : u32x4{0, 0, 0, 0};
-  // This query row sees keys < lim; the item needs keys < kmax.
-  const int lim = qvalid && p.causal ? lk - lq + qi + 1 : lk;
-  const int kmax = p.causal ? min(lk, lk - lq + min(p0 + qp, lq)) : lk;
-
-  float mrun = -INFINITY, lrun = 0.f;
-  f32x4 o[DB];
+  for (int nb = 0; nb < 2; ++nb) {
+    const int mrow = wave * 32 + nb * 16 + n;
+    qi[nb] = p0 + mrow / G;
+    head[nb] = kvh * G + mrow % G;
+    qvalid[nb] = mrow < qp * G && qi[nb] < lq;
+    lim[nb] = qvalid[nb] && p.causal ? lk - lq + qi[nb] + 1 : lk;  // this query row sees keys < lim
 #pragma unroll
-  for (int b = 0; b < DB; ++b) o[b] = f32x4{0, 0, 0, 0};
+    for (int k = 0; k < KS; ++k)
+      qb[nb][k] = qvalid[nb] ? ld16(p.q + (int64_t)(q0 + qi[nb]) * p.q_st + head[nb] * p.q_sh +
+                                    (int64_t)(32 * k + 8 * j4) * 2)
+                             : u32x4{0, 0, 0, 0};
+  }
+  const int kmax = p.causal ? min(lk, lk - lq + min(p0 + qp, lq)) : lk;  // keys the item needs
 
+  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};  // raw-score running max and row sums
+  f32x4 o[2][DB];
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+    for (int b = 0; b < DB; ++b) o[nb][b] = f32x4{0, 0, 0, 0};
+
+  // Staging: chunk i of this thread is key key_of(i) (a tile row), 16-byte part part_of(i).
+  auto key_of = [&](int i) { return i < KPER ? (tid + 256 * i) / KCH : (tid + 256 * i - KCHUNKS) / VCH; };
+  auto part_of = [&](int i) {
+    return i < KPER ? (tid + 256 * i) % KCH : (tid + 256 * i - KCHUNKS) % VCH;
+  };
   const int32_t* table = p.tables + (int64_t)row * p.t_stride;
   const int kbase = p.paged ? 0 : p.cu_k[row];
+  const bool one_page = !p.paged || p.bs.d % kPrefillKeys == 0;  // every tile lies in one page
   // Byte offset of key row j of this kv head in the key (v = false) or value (v = true) source.
   auto row_off = [&](int j, bool v) -> int64_t {
     const int64_t st = v ? p.v_st : p.c_st, sh = v ? p.v_sh : p.c_sh;
@@ -111,105 +133,139 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
   };
   // Keys past the row are staged as zeros: their weight is 0 and 0 * NaN must not happen.
   auto fetch = [&](int kt, u32x4 (&st)[PER]) {
+    const bool tail = kt + kPrefillKeys > lk;
+    if (one_page) {
+      const char* kb = p.k_cache + row_off(kt, false);
+      const char* vb = p.v_cache + row_off(kt, true);
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int c = tid + 256 * i;
-      const bool isv = c >= KCHUNKS;
-      const int cc = isv ? c - KCHUNKS : c;
-      const int key = isv ? cc / VCH : cc / KCH;
-      const int part = isv ? cc - key * VCH : cc - key * KCH;
-      const int jk = kt + key;
-      st[i] = jk < lk ? ld16((isv ? p.v_cache : p.k_cache) + row_off(jk, isv) + part * 16) : u32x4{0, 0, 0, 0};
+      for (int i = 0; i < PER; ++i) {
+        const int key = key_of(i);
+        const char* src = i < KPER ? kb + (int64_t)key * p.c_st : vb + (int64_t)key * p.v_st;
+        st[i] = !tail || kt + key < lk ? ld16(src + part_of(i) * 16) : u32x4{0, 0, 0, 0};
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int jk = kt + key_of(i);
+        st[i] = jk < lk ? ld16((i < KPER ? p.k_cache : p.v_cache) + row_off(jk, i >= KPER) + part_of(i) * 16)
+                        : u32x4{0, 0, 0, 0};
+      }
     }
   };
   auto stash = [&](const u32x4 (&st)[PER]) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      const int c = tid + 256 * i;
-      const bool isv = c >= KCHUNKS;
-      const int cc = isv ? c - KCHUNKS : c;
-      const int key = isv ? cc / VCH : cc / KCH;
-      const int part = isv ? cc - key * VCH : cc - key * KCH;
-      st16(reinterpret_cast<char*>(isv ? vs + key * VROW + part * 8 : ks + key * KROW + part * 8), st[i]);
+      uint16_t* dst = i < KPER ? ks + key_of(i) * KROW : vs + key_of(i) * VROW;
+      st16(reinterpret_cast<char*>(dst + part_of(i) * 8), st[i]);
     }
   };
 
   u32x4 stage[PER];
-  if (kmax > 0) fetch(0, stage);
+  if (PREFETCH && kmax > 0) fetch(0, stage);
   for (int kt = 0; kt < kmax; kt += kPrefillKeys) {
+    if (!PREFETCH) fetch(kt, stage);
     __syncthreads();  // the previous tile's operand reads are done
     stash(stage);
     __syncthreads();
-    if (kt + kPrefillKeys < kmax) fetch(kt + kPrefillKeys, stage);
+    if (PREFETCH && kt + kPrefillKeys < kmax) fetch(kt + kPrefillKeys, stage);
 
-    // S^T (keys x query rows): lane holds keys kt + 16 kb + 4 j4 + r of query row n.
-    f32x4 st[4];
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      st[kb] = f32x4{0, 0, 0, 0};
-#pragma unroll
-      for (int k = 0; k < KS; ++k) {
-        const u32x4 a = *reinterpret_cast<const u32x4*>(ks + (kb * 16 + n) * KROW + 32 * k + 8 * j4);
-        st[kb] = E::mfma16x16x32(a, qb[k], st[kb]);
-      }
-    }
-    float mx = -INFINITY;
+    // S^T (keys x query rows): st[kb][nb] lane holds keys kt + 16 kb + 4 j4 + r of query row (nb, n).
+    f32x4 st[4][2];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = kt + kb * 16 + 4 * j4 + r;
-        const float s = key < lim ? st[kb][r] * p.scale_log2 : -INFINITY;
-        st[kb][r] = s;
-        mx = fmaxf(mx, s);
+      for (int nb = 0; nb < 2; ++nb) st[kb][nb] = f32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int k = 0; k < KS; ++k)
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(ks + (kb * 16 + n) * KROW + 32 * k + 8 * j4);
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) st[kb][nb] = E::mfma16x16x32(a, qb[nb][k], st[kb][nb]);
       }
-    mx = xor32_max(xor16_max(mx));
-    const float mnew = fmaxf(mrun, mx);
-    const float mref = mnew == -INFINITY ? 0.f : mnew;
-    const float alpha = fast_exp2(mrun - mref);
-    mrun = mnew;
-    float psum = 0.f;
-    u32x4 pb[2];  // P^T operands: k slots 8 j4 .. 8 j4 + 7 = keys 32 h + 4 j4 + 0..3, then 32 h + 16 + 4 j4 + 0..3
+    // Mask only a tile that crosses some row's last key (wave-uniform test).
+    if (__any(kt + kPrefillKeys > lim[0] || kt + kPrefillKeys > lim[1])) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      float pr[8];
+      for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        pr[r] = fast_exp2(st[2 * h][r] - mref);
-        pr[4 + r] = fast_exp2(st[2 * h + 1][r] - mref);
-      }
+        for (int r = 0; r < 4; ++r) {
+          const int key = kt + kb * 16 + 4 * j4 + r;
 #pragma unroll
-      for (int r = 0; r < 8; ++r) psum += pr[r];
-#pragma unroll
-      for (int w = 0; w < 4; ++w) pb[h][w] = E::pack(pr[2 * w], pr[2 * w + 1]);
+          for (int nb = 0; nb < 2; ++nb) st[kb][nb][r] = key < lim[nb] ? st[kb][nb][r] : -INFINITY;
+        }
     }
-    lrun = lrun * alpha + psum;
+    float mx[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      float x = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+        x = fmaxf(x, fmaxf(fmaxf(st[kb][nb][0], st[kb][nb][1]), fmaxf(st[kb][nb][2], st[kb][nb][3])));
+      mx[nb] = xor32_max(xor16_max(x));  // over the row's 64 keys of this tile
+    }
+    const bool grow = (mx[0] > m[0] && (m[0] == -INFINITY || (mx[0] - m[0]) * c > kRescaleSlack)) ||
+                      (mx[1] > m[1] && (m[1] == -INFINITY || (mx[1] - m[1]) * c > kRescaleSlack));
+    if (__any(grow)) {
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        const float mn = fmaxf(m[nb], mx[nb]);
+        const float alpha = m[nb] == -INFINITY ? 0.f : fast_exp2((m[nb] - mn) * c);
+        m[nb] = mn;
+        l[nb] *= alpha;
+#pragma unroll
+        for (int b = 0; b < DB; ++b) o[nb][b] *= alpha;
+      }
+    }
+    // P^T operands: k slots 8 j4 .. 8 j4 + 7 = keys 32 h + 4 j4 + 0..3, then 32 h + 16 + 4 j4 + 0..3.
+    u32x4 pb[2][2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const float mc = m[nb] == -INFINITY ? 0.f : m[nb] * c;  // a row with no key yet: every score is -inf
+      float psum = 0.f;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        float pr[8];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          pr[r] = fast_exp2(fmaf(st[2 * h][nb][r], c, -mc));
+          pr[4 + r] = fast_exp2(fmaf(st[2 * h + 1][nb][r], c, -mc));
+        }
+#pragma unroll
+        for (int r = 0; r < 8; ++r) psum += pr[r];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) pb[nb][h][w] = E::pack(pr[2 * w], pr[2 * w + 1]);
+      }
+      l[nb] += psum;
+    }
     // V^T operand rows (dims) 16 b + n; transposing reads of rows 32 h + 4 j4 + (n >> 2) (+ 16), dims + 4 (n & 3).
     const uint16_t* vrow = vs + (4 * j4 + (n >> 2)) * VROW + 4 * (n & 3);
 #pragma unroll
-    for (int b = 0; b < DB; ++b) {
-      o[b] *= alpha;
+    for (int b = 0; b < DB; ++b)
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const u32x2 lo = lds_read_tr16(vrow + 32 * h * VROW + 16 * b);
         const u32x2 hi = lds_read_tr16(vrow + (32 * h + 16) * VROW + 16 * b);
-        o[b] = E::mfma16x16x32(u32x4{lo[0], lo[1], hi[0], hi[1]}, pb[h], o[b]);
+        const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) o[nb][b] = E::mfma16x16x32(a, pb[nb][h], o[nb][b]);
       }
-    }
   }
 
-  lrun = xor32_sum(xor16_sum(lrun));
-  if (qvalid) {
-    const float inv = lrun > 0.f ? 1.f / lrun : 0.f;
-    char* dst = p.out + (int64_t)(q0 + qi) * p.o_st + head * p.o_sh;
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+    const float lsum = xor32_sum(xor16_sum(l[nb]));
+    if (!qvalid[nb]) continue;
+    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+    char* dst = p.out + (int64_t)(q0 + qi[nb]) * p.o_st + head[nb] * p.o_sh;
 #pragma unroll
     for (int b = 0; b < DB; ++b) {
-      const u32x2 packed = {E::pack(o[b][0] * inv, o[b][1] * inv), E::pack(o[b][2] * inv, o[b][3] * inv)};
+      const u32x2 packed = {E::pack(o[nb][b][0] * inv, o[nb][b][1] * inv),
+                            E::pack(o[nb][b][2] * inv, o[nb][b][3] * inv)};
       *reinterpret_cast<u32x2*>(dst + (int64_t)(b * 16 + 4 * j4) * 2) = packed;
     }
     if (p.lse && j4 == 0)
-      p.lse[(int64_t)(q0 + qi) * p.lse_st + (int64_t)head * p.lse_sh] =
-          lrun > 0.f ? (mrun + fast_log2(lrun)) * kLn2 : -INFINITY;
+      p.lse[(int64_t)(q0 + qi[nb]) * p.lse_st + (int64_t)head[nb] * p.lse_sh] =
+          lsum > 0.f ? (m[nb] * c + fast_log2(lsum)) * kLn2 : -INFINITY;
   }
 }
 

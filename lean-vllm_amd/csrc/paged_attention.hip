@@ -23,6 +23,9 @@ constexpr int kPlanMaxRows = 4096;  // rows of a step with prompts (the work-lis
 #ifndef LV_DECODE_PIPE
 #define LV_DECODE_PIPE 2
 #endif
+#ifndef LV_PROMPT_PREFETCH
+#define LV_PROMPT_PREFETCH true
+#endif
 #ifndef LV_SPLIT_TARGET
 #define LV_SPLIT_TARGET 4096
 #endif
@@ -314,31 +317,39 @@ __device__ void decode_item(const AttnParams& p, int row, int split, int kvh, in
 template <int D, int GS>
 struct SmemBytes {
   static constexpr int kDecode = kWaves * GS * (D + 2) * 4;
-  static constexpr int kPrefill = PromptSmem<D, D>::kBytes;
-  static constexpr int kMixed = kDecode > kPrefill ? kDecode : kPrefill;
 };
 
-// LISTED: blockIdx.x walks the device work list with the query-head groups innermost, so workgroups are
-// dispatched in list order (longest first). Otherwise (decode of more rows than the planner holds) blockIdx.x is
-// (row, split) and blockIdx.y the query-head group. MIXED: the list holds prompt items (MFMA path) too.
-template <typename T, int D, int GS, bool LISTED, bool MIXED>
-__global__ __launch_bounds__(256) void paged_attention_kernel(AttnParams p) {
-  constexpr int kSmem = MIXED ? SmemBytes<D, GS>::kMixed : SmemBytes<D, GS>::kDecode;
-  __shared__ __attribute__((aligned(16))) char smem[kSmem];
-  if constexpr (LISTED) {
-    const int ny = p.hkv * p.qgroups;
-    const int bx = blockIdx.x / ny, by = blockIdx.x - bx * ny;
-    const int kvh = by / p.qgroups, qg = by - kvh * p.qgroups;
-    if (bx >= *p.n_items) return;
-    const int2 it = p.items[bx];
-    if (!MIXED || it.y >= 0)
-      decode_item<T, D, GS>(p, it.x, it.y, kvh, qg, smem);
-    else if (qg == 0)
-      prefill_item<T, D, D>(p, it.x, -1 - it.y, kvh, smem);
-  } else {
-    const int kvh = blockIdx.y / p.qgroups, qg = blockIdx.y % p.qgroups;
-    decode_item<T, D, GS>(p, blockIdx.x / p.max_splits, blockIdx.x % p.max_splits, kvh, qg, smem);
-  }
+// Work-list kernels. blockIdx.x walks the device work list with the query-head groups innermost, so workgroups
+// are dispatched in list order (longest first). The list holds a step's prompt items first (n_items[1] of them),
+// then its decode items (n_items[0] in all). Decode items run in decode_list_kernel at the decode item's register
+// budget; prompt items in prompt_list_kernel, whose MFMA tile needs more registers and LDS.
+template <typename T, int D, int GS>
+__global__ __launch_bounds__(256) void decode_list_kernel(AttnParams p) {
+  __shared__ __attribute__((aligned(16))) char smem[SmemBytes<D, GS>::kDecode];
+  const int ny = p.hkv * p.qgroups;
+  const int bx = blockIdx.x / ny, by = blockIdx.x - bx * ny;
+  const int kvh = by / p.qgroups, qg = by - kvh * p.qgroups;
+  const int i = bx + p.n_items[1];
+  if (i >= p.n_items[0]) return;
+  const int2 it = p.items[i];
+  decode_item<T, D, GS>(p, it.x, it.y, kvh, qg, smem);
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256, 2) void prompt_list_kernel(AttnParams p) {
+  __shared__ __attribute__((aligned(16))) char smem[PromptSmem<D, D>::kBytes];
+  const int bx = blockIdx.x / p.hkv, kvh = blockIdx.x - bx * p.hkv;
+  if (bx >= p.n_items[1]) return;
+  const int2 it = p.items[bx];
+  prefill_item<T, D, D, LV_PROMPT_PREFETCH>(p, it.x, -1 - it.y, kvh, smem);
+}
+
+// Decode of more rows than the planner holds: blockIdx.x is (row, split), blockIdx.y the query-head group.
+template <typename T, int D, int GS>
+__global__ __launch_bounds__(256) void decode_grid_kernel(AttnParams p) {
+  __shared__ __attribute__((aligned(16))) char smem[SmemBytes<D, GS>::kDecode];
+  const int kvh = blockIdx.y / p.qgroups, qg = blockIdx.y % p.qgroups;
+  decode_item<T, D, GS>(p, blockIdx.x / p.max_splits, blockIdx.x % p.max_splits, kvh, qg, smem);
 }
 
 constexpr int kLenBuckets = 64;
@@ -402,7 +413,10 @@ __global__ __launch_bounds__(kScanThreads) void plan_kernel(const int32_t* __res
       if (pos < max_items) items[pos] = make_int2(r, n - 1);
     }
   }
-  if (tid == 0) *n_items = min(npre + nfull + npart, max_items);
+  if (tid == 0) {
+    n_items[0] = min(npre + nfull + npart, max_items);
+    n_items[1] = min(npre, max_items);
+  }
 }
 
 // Combine a split row's partial outputs: o = sum_s 2^(lse_s - M) o_s / sum_s 2^(lse_s - M).
@@ -447,7 +461,7 @@ __global__ __launch_bounds__(64) void splitk_merge_kernel(AttnParams p) {
 // Host side.
 
 struct Shape {
-  int32_t split, max_splits, max_items, gs;
+  int32_t split, max_splits, max_items, max_prompt_items, max_decode_items, gs;
   size_t items_off, count_off, lse_off, o_off, bytes;
 };
 
@@ -471,7 +485,9 @@ static Shape plan_shape(int32_t rows, int32_t tokens, int32_t hq, int32_t hkv, i
   s.split = (int32_t)split;
   s.max_splits = (int32_t)((keys + split - 1) / split);
   const int qp = kPrefillRows / (group > 0 ? group : 1);
-  s.max_items = listed ? rows * s.max_splits + (tokens + qp - 1) / qp + rows : 0;
+  s.max_prompt_items = listed ? (tokens + qp - 1) / qp + rows : 0;
+  s.max_decode_items = listed ? rows * s.max_splits : 0;
+  s.max_items = s.max_prompt_items + s.max_decode_items;
   size_t off = 0;
   s.items_off = off;
   off += (size_t)s.max_items * sizeof(int2);
@@ -489,32 +505,33 @@ static Shape plan_shape(int32_t rows, int32_t tokens, int32_t hq, int32_t hkv, i
 }
 
 template <typename T, int D, int GS>
-static void launch(const AttnParams& p, bool listed, bool mixed, int max_items, hipStream_t stream) {
+static void launch(const AttnParams& p, bool listed, bool mixed, const Shape& s, hipStream_t stream) {
   const int ny = p.hkv * p.qgroups;
-  if (listed && mixed)
-    hipLaunchKernelGGL((paged_attention_kernel<T, D, GS, true, true>), dim3(max_items * ny), dim3(256), 0, stream, p);
-  else if (listed)
-    hipLaunchKernelGGL((paged_attention_kernel<T, D, GS, true, false>), dim3(max_items * ny), dim3(256), 0, stream,
-                       p);
-  else
-    hipLaunchKernelGGL((paged_attention_kernel<T, D, GS, false, false>), dim3(p.rows * p.max_splits, ny), dim3(256),
-                       0, stream, p);
+  if (listed && mixed) {
+    hipLaunchKernelGGL((prompt_list_kernel<T, D>), dim3(s.max_prompt_items * p.hkv), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((decode_list_kernel<T, D, GS>), dim3(s.max_decode_items * ny), dim3(256), 0, stream, p);
+  } else if (listed) {
+    hipLaunchKernelGGL((decode_list_kernel<T, D, GS>), dim3(s.max_decode_items * ny), dim3(256), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL((decode_grid_kernel<T, D, GS>), dim3(p.rows * p.max_splits, ny), dim3(256), 0, stream, p);
+  }
   if (p.max_splits > 1)
     hipLaunchKernelGGL((splitk_merge_kernel<T, D>), dim3(p.rows, p.hq), dim3(64), 0, stream, p);
 }
 
 template <typename T, int D>
-static void launch_gs(const AttnParams& p, int gs, bool listed, bool mixed, int max_items, hipStream_t stream) {
-  if (gs == 4) launch<T, D, 4>(p, listed, mixed, max_items, stream);
-  else if (gs == 2) launch<T, D, 2>(p, listed, mixed, max_items, stream);
-  else launch<T, D, 1>(p, listed, mixed, max_items, stream);
+static void launch_gs(const AttnParams& p, int gs, bool listed, bool mixed, const Shape& s, hipStream_t stream) {
+  if (gs == 4) launch<T, D, 4>(p, listed, mixed, s, stream);
+  else if (gs == 2) launch<T, D, 2>(p, listed, mixed, s, stream);
+  else launch<T, D, 1>(p, listed, mixed, s, stream);
 }
 
 template <typename T>
-static int launch_d(const AttnParams& p, int d, int gs, bool listed, bool mixed, int max_items, hipStream_t stream) {
+static int launch_d(const AttnParams& p, int d, int gs, bool listed, bool mixed, const Shape& s,
+                    hipStream_t stream) {
   switch (d) {
-    case 64: launch_gs<T, 64>(p, gs, listed, mixed, max_items, stream); return LV_OK;
-    case 128: launch_gs<T, 128>(p, gs, listed, mixed, max_items, stream); return LV_OK;
+    case 64: launch_gs<T, 64>(p, gs, listed, mixed, s, stream); return LV_OK;
+    case 128: launch_gs<T, 128>(p, gs, listed, mixed, s, stream); return LV_OK;
     default: set_error("paged_attention: head_dim %d is not 64 or 128", d); return LV_EINVAL;
   }
 }
@@ -620,8 +637,8 @@ extern "C" int lv_paged_attention(const void* q, int64_t q_stride_t, int64_t q_s
                        reinterpret_cast<int32_t*>(ws + s.count_off));
     LV_LAUNCH_CHECK("plan_kernel");
   }
-  const int rc = dtype == LV_DTYPE_BF16 ? launch_d<BF16>(p, head_dim, s.gs, listed, mixed, s.max_items, st)
-                                        : launch_d<F16>(p, head_dim, s.gs, listed, mixed, s.max_items, st);
+  const int rc = dtype == LV_DTYPE_BF16 ? launch_d<BF16>(p, head_dim, s.gs, listed, mixed, s, st)
+                                        : launch_d<F16>(p, head_dim, s.gs, listed, mixed, s, st);
   if (rc != LV_OK) return rc;
   LV_LAUNCH_CHECK("paged_attention_kernel");
   return LV_OK;

@@ -11,7 +11,7 @@
 namespace lv {
 
 template <typename T, int DQK, int DV>
-__global__ __launch_bounds__(256) void varlen_kernel(AttnParams p, int32_t qtiles) {
+__global__ __launch_bounds__(256, DQK <= 128 ? 2 : 1) void varlen_kernel(AttnParams p, int32_t qtiles) {
   __shared__ __attribute__((aligned(16))) char smem[PromptSmem<DQK, DV>::kBytes];
   const int row = blockIdx.x / qtiles, qt = blockIdx.x - row * qtiles;
   prefill_item<T, DQK, DV>(p, row, qt, blockIdx.y, smem);
