@@ -52,8 +52,6 @@ __device__ inline int key_len(const AttnParams& p, int row) {
 // sees keys 0 .. lk - lq + j; none if p.causal is 0) is applied only on tiles that cross it.
 // DQK: q.k width; DV: value width.
 
-constexpr float kRescaleSlack = 8.f;
-
 template <int DQK, int DV>
 struct PromptSmem {
   static constexpr int kKRow = DQK + 8;   // key tile row pitch, elements: conflict-free operand reads

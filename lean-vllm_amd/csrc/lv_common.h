@@ -55,6 +55,8 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4v __attribute__((ext_vector_type(4)));
 
 struct BF16 {};  // tag types for the two 16-bit element formats
 struct F16 {};
@@ -78,6 +80,10 @@ template <> struct Elem<BF16> {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
                                                    0, 0, 0);
   }
+  __device__ static inline f32x4 mfma16x16x16(u32x2 a, u32x2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4v, a), __builtin_bit_cast(i16x4v, b), c,
+                                                     0, 0, 0);
+  }
 };
 
 template <> struct Elem<F16> {
@@ -95,6 +101,10 @@ template <> struct Elem<F16> {
   __device__ static inline f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
                                                   0, 0);
+  }
+  __device__ static inline f32x4 mfma16x16x16(u32x2 a, u32x2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c, 0, 0,
+                                                 0);
   }
 };
 
@@ -245,6 +255,9 @@ __device__ inline void block_scan(int* a, int n, int* wave_tot) {
 }
 
 constexpr float kLog2e = 1.4426950408889634f;
+// log2 units by which an online softmax's running max may trail the true max before the accumulators are
+// rescaled: probabilities then stay below 2^kRescaleSlack, well inside bf16 / fp16 and fp32 range.
+constexpr float kRescaleSlack = 8.f;
 constexpr float kLn2 = 0.6931471805599453f;
 
 }  // namespace lv

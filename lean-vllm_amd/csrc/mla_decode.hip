@@ -30,6 +30,12 @@ static_assert(kMlaTile * kLatChunks % 256 == 0, "tile chunks split evenly over 2
 constexpr int kMlaMaxSplit = 4096;        // latents per work item at most
 constexpr int kMlaMaxBlocks = kMlaMaxSplit / 16 + 2;  // pages one work item touches at most (pages >= 16 latents)
 
+#ifndef LV_MLA_STAGES
+#define LV_MLA_STAGES 4
+#endif
+#ifndef LV_MLA_DMA
+#define LV_MLA_DMA 1
+#endif
 #ifndef LV_MLA_SPLIT_TARGET
 #define LV_MLA_SPLIT_TARGET 4096
 #endif
@@ -206,6 +212,211 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------------------------------------
+// Streaming variant: latents move from HBM straight into LDS (global_load_lds_dwordx4), a ring of three 16-latent
+// stages with two in flight while the third is consumed; no registers stage data. Each wave computes the stage's
+// whole S^T (16 latents x 16 heads, K = 576) from LDS, then O^T for its 128 output dims with MFMA 16x16x16 whose
+// V^T operands come from one transposing LDS read each. One unfenced barrier per stage; every wait on the stage
+// loads is an explicit vmcnt.
+
+constexpr int kDmaTile = 16;                            // latents per stage
+constexpr int kDmaRowSlots = kLatChunks + 1;            // 16-byte slots per LDS row (one pad slot: pitch 1168 B)
+constexpr int kDmaStageSlots = kDmaTile * kDmaRowSlots;  // 1168
+constexpr int kDmaInstr = (kDmaStageSlots + 63) / 64;   // 64-lane loads per stage: 19, 5 per wave (4 for wave 3)
+constexpr int kDmaStageElems = kDmaStageSlots * 8;
+static_assert(kDmaRowSlots * 8 == kMlaPitch, "one LDS row pitch for both variants");
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// Cache rows are read once per launch: non-temporal, as ld16_stream.
+#if LV_STREAM_NT
+#define LV_DMA_NT " nt"
+#else
+#define LV_DMA_NT ""
+#endif
+
+// One 16-byte load per lane from base + off into LDS at lds_base + 16 lane (lds_base wave-uniform, set through
+// M0). Issued as inline assembly so that the compiler, which cannot tell which LDS bytes the load writes, adds no
+// wait-for-every-load before later LDS reads; the kernel waits for these loads itself (vmcnt).
+__device__ __forceinline__ void lds_dma16(const char* base, uint32_t off, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" LV_DMA_NT ::"v"(off), "s"(base),
+               "s"(lds_base)
+               : "memory", "m0");
+}
+
+// As above, from a per-lane address.
+__device__ __forceinline__ void lds_dma16(const char* src, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" LV_DMA_NT ::"v"(src), "s"(lds_base)
+               : "memory", "m0");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(lds_void_t*)p;
+}
+
+// Wait until at most `ahead` stages of this wave's loads (5 per stage, 4 for wave 3) are outstanding, then meet
+// the other waves. No fence: the stage's LDS writes are exactly the loads waited for, and a fence would wait for
+// the stages still in flight as well.
+__device__ __forceinline__ void dma_stage_barrier(int ahead, int wave) {
+  const int outstanding = ahead * (wave < 3 ? 5 : 4);
+  switch (outstanding) {
+    case 0: asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory"); break;
+    case 4: asm volatile("s_waitcnt vmcnt(4)\n\ts_barrier" ::: "memory"); break;
+    case 5: asm volatile("s_waitcnt vmcnt(5)\n\ts_barrier" ::: "memory"); break;
+    case 8: asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(10)\n\ts_barrier" ::: "memory"); break;
+  }
+}
+
+// STAGES: ring depth (STAGES - 1 stages in flight while one is consumed; at most 4). ONE_PAGE: block_size is a
+// multiple of 16, so a stage (16 latents starting at a multiple of 16) lies in one page: one page lookup per
+// stage, every lane's load a fixed offset from it.
+template <typename T, int STAGES, bool ONE_PAGE>
+__global__ __launch_bounds__(256) void mla_decode_dma_kernel(MlaParams p) {
+  static_assert(STAGES >= 2 && STAGES <= 4, "the stage waits cover up to three stages in flight");
+  using E = Elem<T>;
+  __shared__ __attribute__((aligned(16))) uint16_t ring[STAGES * kDmaStageElems];
+  __shared__ int64_t page_off[kMlaMaxBlocks];
+  const int row = blockIdx.x / p.max_splits, split = blockIdx.x % p.max_splits;
+  const int qj = blockIdx.y / p.htiles, ht = blockIdx.y % p.htiles;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 15, g = lane >> 4;
+
+  const int lk = p.lens[row] - p.lq + qj + 1;  // latents this query sees
+  const int kbeg = split * p.split;
+  if ((split > 0 && kbeg >= lk) || split >= p.max_splits) return;
+  const int kend = min(lk, kbeg + p.split);
+  const int nsplit = lk > 0 ? min((lk + p.split - 1) / p.split, p.max_splits) : 0;
+  const int tokq = row * p.lq + qj;
+  const int head = ht * 16 + n;
+  const bool hvalid = head < p.heads;
+  const float c = p.scale_log2;
+
+  // Q^T operand over the whole latent: lane holds dims 32 s + 8 g .. + 7 of head n.
+  u32x4 qb[18];
+  {
+    const char* qrow = p.q + tokq * p.q_st + (int64_t)head * p.q_sh;
+#pragma unroll
+    for (int s = 0; s < 18; ++s) qb[s] = hvalid ? ld16(qrow + (int64_t)(32 * s + 8 * g) * 2) : u32x4{0, 0, 0, 0};
+  }
+  const int page0 = kend > kbeg ? (int)p.bs.div(kbeg) : 0;
+  const int npages = kend > kbeg ? (int)p.bs.div(kend - 1) - page0 + 1 : 0;
+  {
+    const int32_t* table = p.tables + (int64_t)row * p.t_stride + page0;
+    for (int i = tid; i < npages; i += 256) page_off[i] = (int64_t)table[i] * p.c_sb;
+  }
+  // This wave's loads j = wave + 4 i (i < 5) of a stage's 19: slot 64 j + lane is 16-byte chunk `part` of latent
+  // row r of the stage. Slot 73 r + 72 of row r is LDS padding, filled with a copy of chunk 71.
+  int lrow[5], lpart[5];
+#pragma unroll
+  for (int i = 0; i < 5; ++i) {
+    const int slot = min(64 * (wave + 4 * i) + lane, kDmaStageSlots - 1);
+    lrow[i] = slot / kDmaRowSlots;
+    lpart[i] = min(slot - lrow[i] * kDmaRowSlots, kLatChunks - 1) * 16;
+  }
+  __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0): q is in registers before the stage loads are counted
+  __syncthreads();
+
+  // Stage load of latents t0 .. t0 + 15; latents at or past kend load a latent of the range instead (finite
+  // values; their weight is 0).
+  auto fill = [&](int t0, uint16_t* stage) {
+    const int last = kend - 1 - t0;  // rows past it are clamped
+    int64_t base = 0;
+    if (ONE_PAGE) {
+      const int pg = (int)p.bs.div(t0);
+      const int64_t po = page_off[pg - page0];
+      // Uniform: move it to scalar registers. The low half is widened unsigned (offsets reach past 2 GiB).
+      base = (int64_t)((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)po) |
+                       ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(po >> 32)) << 32));
+      base += (int64_t)(t0 - pg * (int)p.bs.d) * p.c_st;
+    }
+#pragma unroll
+    for (int i = 0; i < 5; ++i) {
+      const int j = wave + 4 * i;
+      if (j < kDmaInstr && 64 * j + lane < kDmaStageSlots) {
+        const int r = min(lrow[i], last);
+        if (ONE_PAGE) {
+          lds_dma16(p.cache + base, (uint32_t)(r * (int)p.c_st + lpart[i]), lds_addr(stage + 64 * 8 * j));
+        } else {
+          const int tok = t0 + r;
+          const int pg = (int)p.bs.div(tok);
+          lds_dma16(p.cache + page_off[pg - page0] + (int64_t)(tok - pg * (int)p.bs.d) * p.c_st + lpart[i],
+                    lds_addr(stage + 64 * 8 * j));
+        }
+      }
+    }
+  };
+
+  float m = -INFINITY, lsum = 0.f;
+  f32x4 o[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) o[j] = f32x4{0, 0, 0, 0};
+
+  const int ntiles = kend > kbeg ? (kend - kbeg + kDmaTile - 1) / kDmaTile : 0;
+  for (int t = 0; t < STAGES - 1 && t < ntiles; ++t) fill(kbeg + t * kDmaTile, ring + t * kDmaStageElems);
+  for (int it = 0; it < ntiles; ++it) {
+    const int t0 = kbeg + it * kDmaTile;
+    dma_stage_barrier(min(STAGES - 2, ntiles - 1 - it), wave);  // stage `it` has landed for every wave
+    const bool refill = it + STAGES - 1 < ntiles;
+    // Refill the stage read last iteration (every wave has passed the barrier, so its reads are done), then
+    // consume this one.
+    auto step = [&](uint16_t* next, const uint16_t* stage) {
+      if (refill) fill(t0 + (STAGES - 1) * kDmaTile, next);
+      f32x4 sc = {0, 0, 0, 0};  // latents t0 + 4 g + r of head n
+      const uint16_t* arow = stage + n * kMlaPitch + 8 * g;
+#pragma unroll
+      for (int s = 0; s < 18; ++s) sc = E::mfma16x16x32(*reinterpret_cast<const u32x4*>(arow + 32 * s), qb[s], sc);
+      if (t0 + kDmaTile > kend) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sc[r] = t0 + 4 * g + r < kend ? sc[r] : -INFINITY;
+      }
+      float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+      mx = xor32_max(xor16_max(mx));
+      if (__any(mx > m && (m == -INFINITY || (mx - m) * c > kRescaleSlack))) {
+        const float mn = fmaxf(m, mx);
+        const float alpha = m == -INFINITY ? 0.f : fast_exp2((m - mn) * c);
+        m = mn;
+        lsum *= alpha;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] *= alpha;
+      }
+      const float mc = m * c;
+      float pr[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) pr[r] = fast_exp2(fmaf(sc[r], c, -mc));
+      lsum += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+      const u32x2 pb = {E::pack(pr[0], pr[1]), E::pack(pr[2], pr[3])};
+      const uint16_t* v = stage + (4 * g + (n >> 2)) * kMlaPitch + 128 * wave + 4 * (n & 3);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] = E::mfma16x16x16(lds_read_tr16(v + 16 * j), pb, o[j]);
+    };
+    step(ring + ((it + STAGES - 1) % STAGES) * kDmaStageElems, ring + (it % STAGES) * kDmaStageElems);
+  }
+
+  lsum = xor32_sum(xor16_sum(lsum));
+  if (!hvalid) return;
+  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+  if (nsplit <= 1) {
+    char* dst = p.out + tokq * p.o_st + (int64_t)head * p.o_sh;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int d = 128 * wave + 16 * j + 4 * g;
+      const u32x2 v = {E::pack(o[j][0] * inv, o[j][1] * inv), E::pack(o[j][2] * inv, o[j][3] * inv)};
+      *reinterpret_cast<u32x2*>(dst + d * 2) = v;
+    }
+  } else {
+    const int64_t slot = ((int64_t)tokq * p.heads + head) * p.max_splits + split;
+    float* dst = p.part_o + slot * kVDim;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int d = 128 * wave + 16 * j + 4 * g;
+      *reinterpret_cast<f32x4*>(dst + d) = o[j] * inv;
+    }
+    if (wave == 0 && g == 0) p.part_lse[slot] = lsum > 0.f ? m * c + fast_log2(lsum) : -INFINITY;
+  }
+}
+
 // Combine a split query's partials: o = sum_s 2^(lse_s - M) o_s / sum_s 2^(lse_s - M).
 template <typename T>
 __global__ __launch_bounds__(64) void mla_merge_kernel(MlaParams p) {
@@ -247,6 +458,14 @@ struct MlaShape {
   int32_t split, max_splits;
   size_t lse_off, o_off, bytes;
 };
+
+template <typename T>
+static void launch_dma(const MlaParams& p, bool one_page, dim3 grid, hipStream_t st) {
+  if (one_page)
+    hipLaunchKernelGGL((mla_decode_dma_kernel<T, LV_MLA_STAGES, true>), grid, dim3(256), 0, st, p);
+  else
+    hipLaunchKernelGGL((mla_decode_dma_kernel<T, LV_MLA_STAGES, false>), grid, dim3(256), 0, st, p);
+}
 
 static MlaShape mla_shape(int32_t rows, int32_t lq, int32_t heads, int32_t max_k) {
   MlaShape s{};
@@ -330,10 +549,17 @@ extern "C" int lv_mla_decode(const void* q, int64_t q_stride_t, int64_t q_stride
 
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid(num_rows * s.max_splits, queries_per_row * p.htiles);
-  if (dtype == LV_DTYPE_BF16)
+  const bool one_page = block_size % kDmaTile == 0 && p.c_st * kDmaTile < ((int64_t)1 << 31);
+  if (LV_MLA_DMA) {
+    if (dtype == LV_DTYPE_BF16)
+      launch_dma<BF16>(p, one_page, grid, st);
+    else
+      launch_dma<F16>(p, one_page, grid, st);
+  } else if (dtype == LV_DTYPE_BF16) {
     hipLaunchKernelGGL(mla_decode_kernel<BF16>, grid, dim3(256), 0, st, p);
-  else
+  } else {
     hipLaunchKernelGGL(mla_decode_kernel<F16>, grid, dim3(256), 0, st, p);
+  }
   LV_LAUNCH_CHECK("mla_decode_kernel");
   if (s.max_splits > 1) {
     const dim3 mgrid(num_rows * queries_per_row, num_heads);

@@ -218,3 +218,34 @@ def test_decode_replays_in_a_graph(cuda):
         eager = b.decode(q, kc, vc, ctx)
         torch.cuda.synchronize()
         torch.testing.assert_close(out, eager, atol=0, rtol=0)
+
+
+def test_mixed_step_replays_in_a_graph(cuda):
+    """A captured mixed step (work-list plan, prompt kernel, decode kernel, split-K merge) replays with new queries
+    and cache contents; each replay equals an eager call, with eager work between replays."""
+    b = MI355XAttention(32, 128, 1 / math.sqrt(128), 8)
+    bs, width = 256, 24
+    num_cached, num_new = [300, 5000, 0, 1999], [1, 1, 700, 64]
+    tables = [[r * width + j for j in range(width)] for r in range(4)]
+    qs, kf, vf, kn, vn, kc, vc, slots = paged_step(num_cached, num_new, tables, 4 * width, heads=32, kv_heads=8,
+                                                   dim=128, bs=bs, device=cuda, dtype=torch.bfloat16)
+    b.store_kvcache(kn, vn, kc, vc, slots)
+    ctx = context_for(num_cached, num_new, tables, cuda)
+    q = torch.cat(qs).clone()
+    out = torch.empty_like(q)
+    b.forward(q, kn, vn, kc, vc, ctx, out=out)  # warm: grows the workspace outside capture
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out.float().cpu(), dense_expected(qs, kf, vf, 1 / math.sqrt(128)),
+                               atol=2e-2, rtol=1e-2)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        b.forward(q, kn, vn, kc, vc, ctx, out=out)
+    gen = torch.Generator().manual_seed(9)
+    for _ in range(3):
+        q.copy_(torch.randn(q.shape, generator=gen).to(q.dtype))
+        kc.view(-1)[: 1 << 20].copy_(torch.randn(1 << 20, generator=gen).to(kc.dtype))
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = b.forward(q, kn, vn, kc, vc, ctx)
+        torch.cuda.synchronize()
+        torch.testing.assert_close(out, eager, atol=0, rtol=0)

@@ -110,3 +110,29 @@ def test_mla_decode_at_deepseek_v2_lite_shape(cuda):
         want = m.mla_decode(t.q[r:r + 1].cpu(), cache, wl.v_dim, ctx)
         torch.testing.assert_close(out[r:r + 1].float().cpu(), want, **TOL[torch.bfloat16])
     assert math.isclose(wl.scale, 1 / math.sqrt(192))
+
+
+def test_mla_decode_replays_in_a_graph(cuda):
+    """A captured MLA decode (split latents + merge) replays with new queries and lengths; each replay equals an
+    eager call."""
+    b = MI355XAttention(16, LATENT, SCALE, 16)
+    gen = torch.Generator().manual_seed(8)
+    cache = torch.randn(64, 64, LATENT, generator=gen).to(torch.bfloat16).to(cuda)
+    lens = [3000, 65, 1]
+    tables = torch.arange(3 * 20, dtype=torch.int32, device=cuda).view(3, 20)
+    ctx = Context(context_lens=torch.tensor(lens, dtype=torch.int32, device=cuda), block_tables=tables)
+    q = torch.randn(3, 16, LATENT, generator=gen).to(torch.bfloat16).to(cuda)
+    out = torch.empty(3, 16, VDIM, dtype=torch.bfloat16, device=cuda)
+    b.mla_decode(q, cache, VDIM, ctx, out=out)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        b.mla_decode(q, cache, VDIM, ctx, out=out)
+    for step in range(3):
+        q.copy_(torch.randn(q.shape, generator=gen).to(q.dtype))
+        ctx.context_lens.copy_(torch.tensor([max(n - 300 * step, 1) for n in lens], dtype=torch.int32))
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = b.mla_decode(q, cache, VDIM, ctx)
+        torch.cuda.synchronize()
+        torch.testing.assert_close(out, eager, atol=0, rtol=0)
