@@ -14,6 +14,8 @@
 //   O^T += V^T P^T    (512 dims x 16 heads, K = 32 latents) on MFMA 16x16x32: wave w owns dims [128 w, 128 w + 128).
 //                     V^T operands come from the row-major tile by gfx950's transposing LDS read (ds_read_b64_tr_b16).
 // Rows whose latents were split are combined by log-sum-exp in mla_merge_kernel.
+#include <algorithm>
+
 #include "lv_common.h"
 
 namespace lv {
@@ -36,6 +38,9 @@ constexpr int kMlaMaxBlocks = kMlaMaxSplit / 16 + 2;  // pages one work item tou
 #ifndef LV_MLA_DMA
 #define LV_MLA_DMA 1
 #endif
+#ifndef LV_MLA_RUNS
+#define LV_MLA_RUNS 1
+#endif
 #ifndef LV_MLA_SPLIT_TARGET
 #define LV_MLA_SPLIT_TARGET 4096
 #endif
@@ -54,8 +59,10 @@ struct MlaParams {
   char* out;
   int64_t o_st, o_sh;  // bytes
   int32_t split, max_splits;
-  float* part_o;    // [rows * lq][heads][max_splits][kVDim]
-  float* part_lse;  // [rows * lq][heads][max_splits], log2 domain
+  float* part_o;    // split schedule: [rows * lq][heads][max_splits][kVDim]; runs: [runs][2][16][kVDim]
+  float* part_lse;  // split schedule: [rows * lq][heads][max_splits]; runs: [runs][2][16]; log2 domain
+  int32_t units;    // runs: (row, query, 16-head tile) units
+  int32_t* prefix;  // runs: [units + 2] stage prefix over units, then the stage total and the run length
 };
 
 template <typename T>
@@ -254,19 +261,34 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(lds_void_t*)p;
 }
 
-// Wait until at most `ahead` stages of this wave's loads (5 per stage, 4 for wave 3) are outstanding, then meet
+// Wait until at most `ahead` (<= 6) stages of this wave's loads (5 per stage, 4 for wave 3) are outstanding, then meet
 // the other waves. No fence: the stage's LDS writes are exactly the loads waited for, and a fence would wait for
 // the stages still in flight as well.
+#define LV_WAIT_BARRIER(N) asm volatile("s_waitcnt vmcnt(" #N ")\n\ts_barrier" ::: "memory")
 __device__ __forceinline__ void dma_stage_barrier(int ahead, int wave) {
-  const int outstanding = ahead * (wave < 3 ? 5 : 4);
-  switch (outstanding) {
-    case 0: asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory"); break;
-    case 4: asm volatile("s_waitcnt vmcnt(4)\n\ts_barrier" ::: "memory"); break;
-    case 5: asm volatile("s_waitcnt vmcnt(5)\n\ts_barrier" ::: "memory"); break;
-    case 8: asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory"); break;
-    default: asm volatile("s_waitcnt vmcnt(10)\n\ts_barrier" ::: "memory"); break;
+  if (wave < 3) {
+    switch (ahead) {
+      case 0: LV_WAIT_BARRIER(0); break;
+      case 1: LV_WAIT_BARRIER(5); break;
+      case 2: LV_WAIT_BARRIER(10); break;
+      case 3: LV_WAIT_BARRIER(15); break;
+      case 4: LV_WAIT_BARRIER(20); break;
+      case 5: LV_WAIT_BARRIER(25); break;
+      default: LV_WAIT_BARRIER(30); break;
+    }
+  } else {
+    switch (ahead) {
+      case 0: LV_WAIT_BARRIER(0); break;
+      case 1: LV_WAIT_BARRIER(4); break;
+      case 2: LV_WAIT_BARRIER(8); break;
+      case 3: LV_WAIT_BARRIER(12); break;
+      case 4: LV_WAIT_BARRIER(16); break;
+      case 5: LV_WAIT_BARRIER(20); break;
+      default: LV_WAIT_BARRIER(24); break;
+    }
   }
 }
+#undef LV_WAIT_BARRIER
 
 // STAGES: ring depth (STAGES - 1 stages in flight while one is consumed; at most 4). ONE_PAGE: block_size is a
 // multiple of 16, so a stage (16 latents starting at a multiple of 16) lies in one page: one page lookup per
@@ -417,6 +439,321 @@ __global__ __launch_bounds__(256) void mla_decode_dma_kernel(MlaParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------------------------------------
+// Balanced schedule over equal runs of stages, for pages whose size is a multiple of 16 latents.
+//
+// Unit u = (row, query j, 16-head tile), u = (row * lq + j) * htiles + tile, needs T_u = ceil(L_u / 16) stages
+// of 16 latents (L_u latents seen). Laid end to end (prefix P_u) the units' stages are cut into equal runs, one
+// per workgroup of a grid that fills the GPU once; every workgroup streams its run through the LDS ring of the
+// kernel above, each unit it enters preceded by one stage holding that unit's 16 query rows (the same 16 x 576
+// shape as a latent stage). A unit that lies wholly inside one run is finished in place. A unit cut by run
+// boundaries leaves (o / l, log2 l + m) per head in slot 0 (the run's first unit) or slot 1 (its last unit) of
+// every run it touches, and mla_run_merge_kernel combines them; that kernel also writes the zero output of units
+// that see no latents. Every run does equal work, whatever the spread of row lengths, and partials are written
+// only where a row crosses a run boundary.
+
+constexpr int kRunMin = 16;          // stages per run at least (256 latents)
+#ifndef LV_MLA_RUN_STAGES
+#define LV_MLA_RUN_STAGES 4
+#endif
+constexpr int kRunsPerCU = LV_MLA_RUN_STAGES <= 4 ? 2 : 1;  // workgroups that fit a CU's 160 KB of LDS
+constexpr int kRunMaxUnits = 8192;   // units the in-kernel scan serves
+
+__device__ __forceinline__ int unit_latents(const MlaParams& p, int u) {
+  const int tq = u / p.htiles;  // row * lq + j
+  const int row = tq / p.lq, qj = tq - row * p.lq;
+  return p.lens[row] - p.lq + qj + 1;
+}
+
+// Load of a wave-uniform int through the scalar cache. For tables this kernel only reads: the compiler would use
+// a vector load here (the kernel's stores might alias), and its wait for that load would also wait for every
+// latent load in flight.
+__device__ __forceinline__ int sload(const int32_t* ptr) {
+  int v;
+  asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(ptr));
+  return v;
+}
+
+__device__ __forceinline__ int unit_latents_uniform(const MlaParams& p, int u) {
+  const int tq = u / p.htiles;
+  const int row = tq / p.lq, qj = tq - row * p.lq;
+  return sload(p.lens + row) - p.lq + qj + 1;
+}
+
+__device__ __forceinline__ int unit_stages(const MlaParams& p, int u) {
+  const int lk = unit_latents(p, u);
+  return lk > 0 ? (lk + kDmaTile - 1) / kDmaTile : 0;
+}
+
+// Position in a run's stage sequence: unit u (prefix pu, tu stages, lk latents), next tile t (-1: its query).
+struct RunCursor {
+  int u, pu, tu, lk, t;
+  bool done;
+};
+
+template <typename T, int STAGES>
+__global__ __launch_bounds__(256) void mla_run_kernel(MlaParams p) {
+  static_assert(STAGES >= 2 && STAGES <= 8, "the stage waits cover up to seven stages in flight");
+  using E = Elem<T>;
+  __shared__ __attribute__((aligned(16))) uint16_t ring[STAGES * kDmaStageElems];
+  __shared__ f32x4 spart[4][64];  // each wave's partial S^T of the stage
+  __shared__ int wave_tot[4];
+  __shared__ int first[2];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 15, g = lane >> 4;
+  const float c = p.scale_log2;
+
+  // Stage counts over units; thread tid sums units [ulo, uhi). Exclusive scan of those sums across the block.
+  const int per_thread = (p.units + 255) / 256;
+  const int ulo = min(tid * per_thread, p.units), uhi = min(ulo + per_thread, p.units);
+  int local = 0;
+  for (int u = ulo; u < uhi; ++u) local += unit_stages(p, u);
+  int x = local;
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(x, d, 64);
+    if (lane >= d) x += y;
+  }
+  if (lane == 63) wave_tot[wave] = x;
+  __syncthreads();
+  int excl = x - local, total = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    excl += w < wave ? wave_tot[w] : 0;
+    total += wave_tot[w];
+  }
+  total = __builtin_amdgcn_readfirstlane(total);
+  const int per = max((total + (int)gridDim.x - 1) / (int)gridDim.x, kRunMin);
+  if (blockIdx.x == 0) {  // the prefix, for the merge
+    int run = excl;
+    for (int u = ulo; u < uhi; ++u) {
+      p.prefix[u] = run;
+      run += unit_stages(p, u);
+    }
+    if (tid == 0) {
+      p.prefix[p.units] = total;
+      p.prefix[p.units + 1] = per;
+    }
+  }
+  const int start = blockIdx.x * per;
+  if (start >= total) return;
+  const int end = min(start + per, total);
+  if (local > 0 && excl <= start && start < excl + local) {
+    int u = ulo, acc = excl;
+    for (int tu = unit_stages(p, u); acc + tu <= start; tu = unit_stages(p, u)) {
+      acc += tu;
+      ++u;
+    }
+    first[0] = u;
+    first[1] = acc;
+  }
+  __syncthreads();
+
+  // Both cursors walk the same sequence: for each unit, its query stage, then its tiles inside [start, end).
+  auto enter = [&](RunCursor& r, int u, int pu) {
+    int lk = unit_latents_uniform(p, u);
+    while (lk <= 0) lk = unit_latents_uniform(p, ++u);  // units without latents hold no stages
+    r.u = u;
+    r.pu = pu;
+    r.lk = lk;
+    r.tu = (lk + kDmaTile - 1) / kDmaTile;
+    r.t = -1;
+    r.done = false;
+  };
+  auto advance = [&](RunCursor& r) {
+    if (r.t < 0) {
+      r.t = max(start, r.pu) - r.pu;
+    } else if (r.pu + r.t + 1 == end) {
+      r.done = true;
+    } else if (r.t + 1 == r.tu) {
+      enter(r, r.u + 1, r.pu + r.tu);
+    } else {
+      ++r.t;
+    }
+  };
+  RunCursor prod, cons;
+  enter(prod, __builtin_amdgcn_readfirstlane(first[0]), __builtin_amdgcn_readfirstlane(first[1]));
+  cons = prod;
+
+  // This wave's loads j = wave + 4 i (i < 5) of a stage's 19: slot 64 j + lane is 16-byte chunk `part` of row r
+  // (latent or head) of the stage. Slot 73 r + 72 of row r is LDS padding, filled with a copy of chunk 71.
+  int lrow[5], lpart[5];
+#pragma unroll
+  for (int i = 0; i < 5; ++i) {
+    const int slot = min(64 * (wave + 4 * i) + lane, kDmaStageSlots - 1);
+    lrow[i] = slot / kDmaRowSlots;
+    lpart[i] = min(slot - lrow[i] * kDmaRowSlots, kLatChunks - 1) * 16;
+  }
+  // Query stage: head ht 16 + r of the unit's token (heads past the last load the last head; not written).
+  // Latent stage: latents t0 .. t0 + 15 of the row, one page (the page size is a multiple of 16); latents at
+  // or past lk load latent lk - 1 instead (finite values; their weight is 0).
+  auto fill = [&](const RunCursor& r, uint16_t* stage) {
+    const int tq = r.u / p.htiles, ht = r.u - tq * p.htiles;
+    if (r.t < 0) {
+      const char* qrow = p.q + tq * p.q_st;
+#pragma unroll
+      for (int i = 0; i < 5; ++i) {
+        const int j = wave + 4 * i;
+        if (j < kDmaInstr && 64 * j + lane < kDmaStageSlots)
+          lds_dma16(qrow + (int64_t)min(ht * 16 + lrow[i], p.heads - 1) * p.q_sh + lpart[i],
+                    lds_addr(stage + 64 * 8 * j));
+      }
+    } else {
+      const int row = tq / p.lq;
+      const int t0 = r.t * kDmaTile;
+      const int pg = (int)p.bs.div(t0);
+      const int64_t blk = sload(p.tables + (int64_t)row * p.t_stride + pg);
+      const char* base = p.cache + blk * p.c_sb + (int64_t)(t0 - pg * (int)p.bs.d) * p.c_st;
+      const int last = r.lk - 1 - t0;
+#pragma unroll
+      for (int i = 0; i < 5; ++i) {
+        const int j = wave + 4 * i;
+        if (j < kDmaInstr && 64 * j + lane < kDmaStageSlots)
+          lds_dma16(base, (uint32_t)(min(lrow[i], last) * (int)p.c_st + lpart[i]), lds_addr(stage + 64 * 8 * j));
+      }
+    }
+  };
+
+  // S^T = Lat Q^T over K = 576 is split over the waves: wave w takes MFMA k-steps [s0, s0 + ns) of the 18.
+  const int s0 = wave < 2 ? 5 * wave : 4 * wave + 2, ns = wave < 2 ? 5 : 4;
+  u32x4 qb[5];
+  float m = -INFINITY, lsum = 0.f;
+  f32x4 o[8];
+  int issued = 0;
+  for (; issued < STAGES - 1 && !prod.done; ++issued) {
+    fill(prod, ring + issued * kDmaStageElems);
+    advance(prod);
+  }
+  for (int k = 0; !cons.done; ++k) {
+    dma_stage_barrier(issued - k - 1, wave);  // stage k has landed for every wave
+    // Refill the slot read last iteration (every wave has passed the barrier, so its reads are done).
+    if (!prod.done) {
+      fill(prod, ring + (issued % STAGES) * kDmaStageElems);
+      advance(prod);
+      ++issued;
+    }
+    const uint16_t* stage = ring + (k % STAGES) * kDmaStageElems;
+    if (cons.t < 0) {
+      // Q^T operand of this wave's k-steps: lane holds dims 32 (s0 + i) + 8 g .. + 7 of head n.
+      const uint16_t* qs = stage + n * kMlaPitch + 32 * s0 + 8 * g;
+#pragma unroll
+      for (int i = 0; i < 5; ++i)
+        if (i < ns) qb[i] = *reinterpret_cast<const u32x4*>(qs + 32 * i);
+      m = -INFINITY;
+      lsum = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] = f32x4{0, 0, 0, 0};
+      advance(cons);
+      continue;
+    }
+    const int t0 = cons.t * kDmaTile;
+    f32x4 sc = {0, 0, 0, 0};  // latents t0 + 4 g + r of head n
+    const uint16_t* arow = stage + n * kMlaPitch + 32 * s0 + 8 * g;
+#pragma unroll
+    for (int i = 0; i < 5; ++i)
+      if (i < ns) sc = E::mfma16x16x32(*reinterpret_cast<const u32x4*>(arow + 32 * i), qb[i], sc);
+    // Sum the four partials, in the same order in every wave (every wave then holds the same S^T). The barrier
+    // waits for LDS only: the stage loads in flight are not waited for.
+    spart[wave][lane] = sc;
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    sc = (spart[0][lane] + spart[1][lane]) + (spart[2][lane] + spart[3][lane]);
+    if (t0 + kDmaTile > cons.lk) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sc[r] = t0 + 4 * g + r < cons.lk ? sc[r] : -INFINITY;
+    }
+    float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+    mx = xor32_max(xor16_max(mx));
+    if (__any(mx > m && (m == -INFINITY || (mx - m) * c > kRescaleSlack))) {
+      const float mn = fmaxf(m, mx);
+      const float alpha = m == -INFINITY ? 0.f : fast_exp2((m - mn) * c);
+      m = mn;
+      lsum *= alpha;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] *= alpha;
+    }
+    const float mc = m * c;
+    float pr[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) pr[r] = fast_exp2(fmaf(sc[r], c, -mc));
+    lsum += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+    const u32x2 pb = {E::pack(pr[0], pr[1]), E::pack(pr[2], pr[3])};
+    const uint16_t* v = stage + (4 * g + (n >> 2)) * kMlaPitch + 128 * wave + 4 * (n & 3);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = E::mfma16x16x16(lds_read_tr16(v + 16 * j), pb, o[j]);
+
+    if (cons.t + 1 == cons.tu || cons.pu + cons.t + 1 == end) {  // the unit's last stage in this run
+      const float l = xor32_sum(xor16_sum(lsum));
+      const int tq = cons.u / p.htiles, head = (cons.u - tq * p.htiles) * 16 + n;
+      const float inv = 1.f / l;  // l > 0: each of the run's stages of the unit holds a latent in range
+      if (head < p.heads) {
+        if (cons.pu >= start && cons.pu + cons.tu <= end) {
+          char* dst = p.out + tq * p.o_st + (int64_t)head * p.o_sh;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const int d = 128 * wave + 16 * j + 4 * g;
+            const u32x2 val = {E::pack(o[j][0] * inv, o[j][1] * inv), E::pack(o[j][2] * inv, o[j][3] * inv)};
+            *reinterpret_cast<u32x2*>(dst + d * 2) = val;
+          }
+        } else {
+          const int slot = (blockIdx.x * 2 + (cons.pu <= start ? 0 : 1)) * 16 + n;
+          float* dst = p.part_o + (int64_t)slot * kVDim;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const int d = 128 * wave + 16 * j + 4 * g;
+            *reinterpret_cast<f32x4*>(dst + d) = o[j] * inv;
+          }
+          if (wave == 0 && g == 0) p.part_lse[slot] = m * c + fast_log2(l);
+        }
+      }
+    }
+    advance(cons);
+  }
+}
+
+// Finish units cut by run boundaries (log-sum-exp over the runs that touched them) and zero the output of units
+// that see no latents; units finished in place are left alone. Block (unit, head of its tile), 64 threads.
+template <typename T>
+__global__ __launch_bounds__(64) void mla_run_merge_kernel(MlaParams p) {
+  using E = Elem<T>;
+  const int u = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+  const int tq = u / p.htiles, head = (u - tq * p.htiles) * 16 + h;
+  if (head >= p.heads) return;
+  const int pu = p.prefix[u], tu = p.prefix[u + 1] - pu, per = p.prefix[p.units + 1];
+  constexpr int PER = kVDim / 64;
+  float o[PER];
+#pragma unroll
+  for (int e = 0; e < PER; ++e) o[e] = 0.f;
+  if (tu > 0) {
+    const int b0 = pu / per, b1 = (pu + tu - 1) / per;
+    if (b0 == b1) return;
+    float mmax = -INFINITY;
+    for (int b = b0; b <= b1; ++b) {
+      const int slot = (b * 2 + (b == b0 && pu != b0 * per ? 1 : 0)) * 16 + h;
+      mmax = fmaxf(mmax, p.part_lse[slot]);
+    }
+    float den = 0.f;
+    for (int b = b0; b <= b1; ++b) {
+      const int slot = (b * 2 + (b == b0 && pu != b0 * per ? 1 : 0)) * 16 + h;
+      const float w = fast_exp2(p.part_lse[slot] - mmax);
+      den += w;
+      const f32x4* src = reinterpret_cast<const f32x4*>(p.part_o + (int64_t)slot * kVDim + lane * PER);
+#pragma unroll
+      for (int e = 0; e < PER / 4; ++e) {
+        const f32x4 v = src[e];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[4 * e + r] = fmaf(w, v[r], o[4 * e + r]);
+      }
+    }
+    const float inv = 1.f / den;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) o[e] *= inv;
+  }
+  u32x4 packed;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) packed[w] = E::pack(o[2 * w], o[2 * w + 1]);
+  *reinterpret_cast<u32x4*>(p.out + tq * p.o_st + (int64_t)head * p.o_sh + lane * PER * 2) = packed;
+}
+
 // Combine a split query's partials: o = sum_s 2^(lse_s - M) o_s / sum_s 2^(lse_s - M).
 template <typename T>
 __global__ __launch_bounds__(64) void mla_merge_kernel(MlaParams p) {
@@ -455,9 +792,22 @@ __global__ __launch_bounds__(64) void mla_merge_kernel(MlaParams p) {
 }
 
 struct MlaShape {
-  int32_t split, max_splits;
-  size_t lse_off, o_off, bytes;
+  int32_t split, max_splits;  // split schedule
+  int32_t runs, units;        // run schedule: workgroups, units
+  size_t lse_off, o_off, prefix_off, bytes;
 };
+
+// Compute units of the current device (cached per device; 256 on MI355X).
+static int device_cus() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+  if (dev < 64 && cached[dev] > 0) return cached[dev];
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+  if (dev < 64) cached[dev] = cus;
+  return cus;
+}
 
 template <typename T>
 static void launch_dma(const MlaParams& p, bool one_page, dim3 grid, hipStream_t st) {
@@ -471,16 +821,31 @@ static MlaShape mla_shape(int32_t rows, int32_t lq, int32_t heads, int32_t max_k
   MlaShape s{};
   const int64_t units = (int64_t)rows * lq * ((heads + 15) / 16);
   const int64_t keys = max_k > 0 ? max_k : 1;
+  // Split schedule (pages not a multiple of 16 latents, or too many units for the in-kernel scan).
   int64_t split = 256;
   while (split < kMlaMaxSplit && split < keys && units * ((keys + split - 1) / split) > LV_MLA_SPLIT_TARGET)
     split *= 2;
   s.split = (int32_t)split;
   s.max_splits = (int32_t)((keys + split - 1) / split);
   const size_t parts = s.max_splits > 1 ? (size_t)rows * lq * heads * s.max_splits : 0;
+  // Run schedule: two workgroups per CU, fewer when the stages cannot fill runs of kRunMin.
+  const int64_t stages = units * ((keys + kDmaTile - 1) / kDmaTile);
+  s.units = (int32_t)std::min<int64_t>(units, INT32_MAX);
+  s.runs = (int32_t)std::max<int64_t>(
+      1, std::min<int64_t>(kRunsPerCU * device_cus(), (stages + kRunMin - 1) / kRunMin));
+  const size_t run_parts = (size_t)s.runs * 2 * 16;
+  const size_t nparts = std::max(parts, run_parts);
   s.lse_off = 0;
-  s.o_off = (parts * sizeof(float) + 255) / 256 * 256;
-  s.bytes = s.o_off + parts * kVDim * sizeof(float);
+  s.o_off = (nparts * sizeof(float) + 255) / 256 * 256;
+  s.prefix_off = s.o_off + nparts * kVDim * sizeof(float);
+  s.bytes = s.prefix_off + (size_t)(units + 2) * sizeof(int32_t);
   return s;
+}
+
+template <typename T>
+static void launch_runs(const MlaParams& p, int runs, hipStream_t st) {
+  hipLaunchKernelGGL((mla_run_kernel<T, LV_MLA_RUN_STAGES>), dim3(runs), dim3(256), 0, st, p);
+  hipLaunchKernelGGL(mla_run_merge_kernel<T>, dim3(p.units, 16), dim3(64), 0, st, p);
 }
 
 }  // namespace lv
@@ -548,8 +913,20 @@ extern "C" int lv_mla_decode(const void* q, int64_t q_stride_t, int64_t q_stride
   p.part_o = s.max_splits > 1 ? reinterpret_cast<float*>(ws + s.o_off) : nullptr;
 
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const dim3 grid(num_rows * s.max_splits, queries_per_row * p.htiles);
   const bool one_page = block_size % kDmaTile == 0 && p.c_st * kDmaTile < ((int64_t)1 << 31);
+  if (LV_MLA_RUNS && one_page && s.units <= kRunMaxUnits) {
+    p.units = s.units;
+    p.part_lse = reinterpret_cast<float*>(ws + s.lse_off);
+    p.part_o = reinterpret_cast<float*>(ws + s.o_off);
+    p.prefix = reinterpret_cast<int32_t*>(ws + s.prefix_off);
+    if (dtype == LV_DTYPE_BF16)
+      launch_runs<BF16>(p, s.runs, st);
+    else
+      launch_runs<F16>(p, s.runs, st);
+    LV_LAUNCH_CHECK("mla_run_kernel");
+    return LV_OK;
+  }
+  const dim3 grid(num_rows * s.max_splits, queries_per_row * p.htiles);
   if (LV_MLA_DMA) {
     if (dtype == LV_DTYPE_BF16)
       launch_dma<BF16>(p, one_page, grid, st);

@@ -31,7 +31,7 @@ def check_mla(device, dtype, block_size, context_lens, tables, queries=1, heads=
     cache = torch.zeros(nblocks, block_size, LATENT, dtype=dtype)
     latents = [torch.randn(n, LATENT, generator=gen).to(dtype) for n in context_lens]
     for lat, table in zip(latents, tables):
-        slots = torch.tensor(slots_for(table, block_size, 0, lat.size(0)))
+        slots = torch.tensor(slots_for(table, block_size, 0, lat.size(0)), dtype=torch.long)
         cache.view(-1, LATENT)[slots] = lat
     q = torch.randn(len(context_lens) * queries, heads, LATENT, generator=gen).to(dtype)
     ctx = Context(context_lens=torch.tensor(context_lens, dtype=torch.int32, device=device),
@@ -46,7 +46,8 @@ def check_mla(device, dtype, block_size, context_lens, tables, queries=1, heads=
     torch.testing.assert_close(out.float().cpu(), want, **TOL[dtype])
 
 
-CASES = [(dtype, bs) for dtype in (torch.float16, torch.bfloat16) for bs in (16, 64)]
+# Pages of 40 latents are not a multiple of 16: the kernel's split schedule instead of its balanced runs.
+CASES = [(dtype, bs) for dtype in (torch.float16, torch.bfloat16) for bs in (16, 64)] + [(torch.bfloat16, 40)]
 IDS = [f"{'fp16' if d == torch.float16 else 'bf16'}-bs{bs}" for d, bs in CASES]
 
 
@@ -72,6 +73,22 @@ def test_mla_decode_over_several_head_tiles(cuda, heads):
     """16 heads fill one MFMA tile; 20 and 32 take two, the last one partly empty for 20."""
     check_mla(cuda, torch.bfloat16, 64, [700, 65, 3000], [list(range(0, 11)) + [-1] * 36, [11, 12] + [-1] * 45,
                                                          list(range(13, 60))], heads=heads)
+
+
+@pytest.mark.parametrize("queries", [1, 2])
+def test_mla_decode_of_many_ragged_rows(cuda, queries):
+    """64 rows of 0 to 600 latents: with runs of 256 latents most rows are cut over several runs and merged; a
+    row without latents gives zeros, a row of `queries` latents lets its first query see one."""
+    gen = torch.Generator().manual_seed(7)
+    lens = torch.randint(queries, 601, (64,), generator=gen).tolist()
+    lens[3], lens[10] = 0, queries
+    need = [max(1, -(-n // 64)) for n in lens]
+    perm = torch.randperm(sum(need), generator=gen).tolist()
+    tables, at = [], 0
+    for k in need:
+        tables.append(perm[at:at + k] + [-1] * (max(need) - k))
+        at += k
+    check_mla(cuda, torch.bfloat16, 64, lens, tables, queries=queries, heads=16, seed=7)
 
 
 def test_mla_rows_with_no_latents_give_zeros(cuda):
