@@ -224,8 +224,16 @@ def cpu_baseline(wl, t, dec_sample: int = 4096):
     }
 
 
+def attention_op(wl) -> str:
+    """The kernels of one attention op on this workload (the roofline's subject)."""
+    if wl.is_mla:
+        return "lv_mla_decode (mla_run_kernel + mla_run_merge_kernel)"
+    prompt = "prompt_list_kernel + " if any(n > 1 for n in wl.num_new) else ""
+    return f"lv_paged_attention (plan_kernel + {prompt}decode_list_kernel + splitk_merge_kernel)"
+
+
 def traffic_of(name: str):
-    """HBM bytes per attention launch from the committed rocprofv3 counter summary, if there is one."""
+    """HBM bytes per attention op (all its kernels, one step) from the committed rocprofv3 counter summary."""
     f = ROOT / "profiles" / f"traffic_{name}.json"
     if f.exists():
         return json.loads(f.read_text()).get("hbm_bytes_per_launch")
@@ -288,7 +296,7 @@ def main():
             "unit": "GB/s",
             "frac": primary["attention_frac_of_peak"],
             "traffic": traffic_of(primary["workload"]),
-            "kernel": "lv_paged_attention (paged_attention_kernel + work-list plan + split-K merge)",
+            "kernel": attention_op(wl),
             "algorithmic_bytes_per_launch": primary["bytes"]["attention"],
             "tflops": primary["attention_TFLOPs"],
         },

@@ -25,7 +25,7 @@ extern "C" {
 #define LV_DTYPE_BF16 0
 #define LV_DTYPE_F16 1
 
-#define LV_ABI_VERSION 1
+#define LV_ABI_VERSION 2
 
 /* The last error message of the calling thread ("" if none). */
 const char* lv_last_error(void);
@@ -49,12 +49,19 @@ int lv_abi_version(void);
  *                       (compacted, as model_runner.py:442-445)
  *   context_lens[B]     int32 num_cached + num_new
  *   block_tables[B*W]   int32 block lists padded with -1 (may be NULL when table_width == 0)
+ * Optional, for steps that gather logits rows (model_runner.py:424-430): num_logits[B] (scheduler order) is the
+ * number of logits rows each row samples -- its drafts + 1, or 0 for a chunk that does not sample (at most its
+ * num_new); then
+ *   logits_indices[L]   int64, L = sum(num_logits): for each sampling row in scheduler order, the last
+ *                       num_logits token rows of its chunk, cu_seqlens_q[b+1] - n .. cu_seqlens_q[b+1] - 1
+ * (both NULL to skip).
  * Limit: num_rows <= LV_PACK_MAX_ROWS. */
 #define LV_PACK_MAX_ROWS 4096
 int lv_pack(const int32_t* num_cached, const int32_t* num_new, const int32_t* blk_indptr, const int32_t* blk_ids,
             int32_t num_rows, int32_t query_len, int32_t block_size, int32_t table_width, int32_t num_tokens,
             int32_t* order, int32_t* cu_seqlens_q, int32_t* cu_seqlens_k, int64_t* positions,
-            int32_t* slot_mapping, int32_t* context_lens, int32_t* block_tables, void* stream);
+            int32_t* slot_mapping, int32_t* context_lens, int32_t* block_tables, const int32_t* num_logits,
+            int64_t* logits_indices, void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------
  * Scatter new keys/values into the paged cache. Replaces AttentionBackend.store_kvcache

@@ -4,22 +4,24 @@
 // ints), then fills its share of the per-token outputs (positions, slot_mapping) and of the padded block table.
 // Workgroup 0 also writes the row-level outputs. No grid-wide synchronisation, no atomics, no host read back.
 // The integer arithmetic mirrors ModelRunner.prepare_batch (lean_vllm/engine/model_runner.py:367-446).
+// num_logits[s] <= num_new[s] is the caller's contract (a row samples at most its own token rows).
 #include "lv_common.h"
 
 namespace lv {
 
 constexpr int kPackThreads = kScanThreads;
-constexpr int kPackMaxRows = 4096;  // LDS holds three (rows + 1)-int arrays
+constexpr int kPackMaxRows = 4096;  // LDS holds four (rows + 1)-int arrays
 
 __global__ __launch_bounds__(kPackThreads) void pack_kernel(
     const int32_t* __restrict__ num_cached, const int32_t* __restrict__ num_new, const int32_t* __restrict__ indptr,
     const int32_t* __restrict__ blk_ids, int32_t rows, int32_t query_len, int32_t bs, int32_t width, int32_t tokens,
     int32_t* __restrict__ order, int32_t* __restrict__ cu_q_out, int32_t* __restrict__ cu_k_out,
     int64_t* __restrict__ positions, int32_t* __restrict__ slots, int32_t* __restrict__ context_lens,
-    int32_t* __restrict__ tables) {
+    int32_t* __restrict__ tables, const int32_t* __restrict__ num_logits, int64_t* __restrict__ logits) {
   __shared__ int src[kPackMaxRows];       // batch row -> scheduler row
   __shared__ int cu_q[kPackMaxRows + 1];  // token offsets, batch order
   __shared__ int cu_s[kPackMaxRows + 1];  // slot_mapping offsets (rows with a block list only), batch order
+  __shared__ int row_of[kPackMaxRows];    // scheduler row -> batch row (logits only)
   __shared__ int wave_tot[kPackThreads / 64 + 1];
   const int tid = threadIdx.x;
 
@@ -84,7 +86,29 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
     tables[e] = j < len ? blk_ids[list + j] : -1;
   }
 
-  // 6. cu_seqlens_k (model_runner.py:395-397), in workgroup 0, reusing cu_q's LDS now that its tokens are done.
+  // 6. logits_indices (model_runner.py:424-430), in workgroup 0: the sampling rows in scheduler order, each the
+  // last num_logits[s] token rows of its chunk (its drafts, then the next token).
+  if (blockIdx.x == 0 && num_logits) {
+    __syncthreads();  // this workgroup's tokens are done with cu_s
+    for (int i = tid; i < rows; i += kPackThreads) cu_s[i] = num_new[i] == query_len ? 1 : 0;
+    __syncthreads();
+    block_scan(cu_s, rows, wave_tot);
+    for (int i = tid; i < rows; i += kPackThreads) {
+      const int before = cu_s[i];
+      row_of[i] = num_new[i] == query_len ? before : leading + (i - before);
+    }
+    __syncthreads();
+    for (int i = tid; i < rows; i += kPackThreads) cu_s[i] = num_logits[i];
+    __syncthreads();
+    block_scan(cu_s, rows, wave_tot);
+    for (int s = tid; s < rows; s += kPackThreads) {
+      const int n = num_logits[s];
+      const int64_t first = (int64_t)cu_q[row_of[s] + 1] - n;
+      for (int j = 0; j < n; ++j) logits[cu_s[s] + j] = first + j;
+    }
+  }
+
+  // 7. cu_seqlens_k (model_runner.py:395-397), in workgroup 0, reusing cu_q's LDS now that its tokens are done.
   if (blockIdx.x == 0) {
     __syncthreads();
     for (int r = tid; r < rows; r += kPackThreads) {
@@ -105,7 +129,7 @@ extern "C" int lv_pack(const int32_t* num_cached, const int32_t* num_new, const 
                        const int32_t* blk_ids, int32_t num_rows, int32_t query_len, int32_t block_size,
                        int32_t table_width, int32_t num_tokens, int32_t* order, int32_t* cu_seqlens_q,
                        int32_t* cu_seqlens_k, int64_t* positions, int32_t* slot_mapping, int32_t* context_lens,
-                       int32_t* block_tables, void* stream) {
+                       int32_t* block_tables, const int32_t* num_logits, int64_t* logits_indices, void* stream) {
   LV_REQUIRE(num_rows > 0 && num_rows <= kPackMaxRows, "pack: %d rows; 1 to %d are supported", num_rows,
              kPackMaxRows);
   LV_REQUIRE(block_size > 0, "pack: block_size must be positive, got %d", block_size);
@@ -114,13 +138,14 @@ extern "C" int lv_pack(const int32_t* num_cached, const int32_t* num_new, const 
              "pack: null row pointer");
   LV_REQUIRE(num_tokens == 0 || positions, "pack: null positions");
   LV_REQUIRE(table_width == 0 || (block_tables && blk_ids && slot_mapping), "pack: null table pointer");
+  LV_REQUIRE(!num_logits || logits_indices, "pack: num_logits given without logits_indices");
   const int64_t work = (int64_t)num_tokens + (int64_t)num_rows * table_width;
   int grid = (int)((work + kPackThreads * 4 - 1) / (kPackThreads * 4));
   grid = grid < 1 ? 1 : (grid > 64 ? 64 : grid);
   hipLaunchKernelGGL(pack_kernel, dim3(grid), dim3(kPackThreads), 0, reinterpret_cast<hipStream_t>(stream),
                      num_cached, num_new, blk_indptr, blk_ids, num_rows, query_len, block_size, table_width,
                      num_tokens, order, cu_seqlens_q, cu_seqlens_k, positions, slot_mapping, context_lens,
-                     block_tables);
+                     block_tables, num_logits, logits_indices);
   LV_LAUNCH_CHECK("pack_kernel");
   return LV_OK;
 }

@@ -73,11 +73,12 @@ class StagingBuffers:
 class PackPlan:
     """One step's staged packing inputs (device) and the row-level host ints derived from them."""
 
-    __slots__ = ("rows", "tokens", "width", "slot_count", "query_len", "inputs", "host")
+    __slots__ = ("rows", "tokens", "width", "slot_count", "query_len", "inputs", "host", "logits")
 
-    def __init__(self, rows, tokens, width, slot_count, query_len, inputs, host):
+    def __init__(self, rows, tokens, width, slot_count, query_len, inputs, host, logits=-1):
         self.rows, self.tokens, self.width, self.slot_count = rows, tokens, width, slot_count
         self.query_len, self.inputs, self.host = query_len, inputs, host
+        self.logits = logits  # logits rows gathered, or -1 for none (the whole batch samples)
 
 
 class Packer:
@@ -88,21 +89,25 @@ class Packer:
         self.buffers = StagingBuffers(device)
 
     def pack(self, num_cached, num_new, block_lists, num_speculative_tokens: int = 0,
-             is_prompt=None) -> tuple[torch.Tensor, dict]:
+             is_prompt=None, num_logits=None) -> tuple[torch.Tensor, dict]:
         """Per-row ``num_cached``, ``num_new`` (scheduler order) and block lists -> ``(positions, context)``.
 
         ``context`` has the keys of ``prepare_batch``'s context dict (``model_runner.py:448-462``) that attention
-        reads, plus ``order`` (batch row -> scheduler row). ``is_prompt`` marks prompt rows (default: rows with
-        more than one new token), which makes the step ``is_prefill``. The returned tensors live in buffers the
+        and the logits gather read, plus ``order`` (batch row -> scheduler row). ``is_prompt`` marks prompt rows
+        (default: rows with more than one new token), which makes the step ``is_prefill``. ``num_logits``
+        (scheduler order) is the number of logits rows each row samples: its drafts + 1, or 0 for a chunk that
+        does not sample (default: 1 per row). As in the reference, ``logits_indices`` is gathered only for an
+        ``is_prefill`` step and is None otherwise (every row samples). The returned tensors live in buffers the
         next call reuses.
         """
         self.buffers.begin()
-        plan = self.stage(num_cached, num_new, block_lists, num_speculative_tokens, is_prompt)
+        plan = self.stage(num_cached, num_new, block_lists, num_speculative_tokens, is_prompt, num_logits)
         out = self.run(plan)
         self.buffers.end()
         return out
 
-    def stage(self, num_cached, num_new, block_lists, num_speculative_tokens: int = 0, is_prompt=None) -> PackPlan:
+    def stage(self, num_cached, num_new, block_lists, num_speculative_tokens: int = 0, is_prompt=None,
+              num_logits=None) -> PackPlan:
         """Copy the per-row inputs to the device (one pinned copy) and derive the host-side row ints."""
         num_cached = np.asarray(num_cached, dtype=np.int32)
         num_new = np.asarray(num_new, dtype=np.int32)
@@ -129,10 +134,17 @@ class Packer:
             cu_seqlens_k_host=[0, *np.cumsum(ends_b).tolist()],
             decode_query_len=query_len,
         )
-        staged = np.concatenate([num_cached, num_new, indptr, ids])
-        inputs = self.buffers.put("inputs", staged, torch.int32)
+        parts = [num_cached, num_new, indptr, ids]
+        logits = -1
+        if host["is_prefill"]:
+            n_log = np.ones(rows, np.int32) if num_logits is None else np.asarray(num_logits, dtype=np.int32)
+            if n_log.shape != (rows,) or (n_log < 0).any() or (n_log > num_new).any():
+                raise ValueError("pack: num_logits must give 0 .. num_new logits rows per row")
+            parts.append(n_log)
+            logits = int(n_log.sum())
+        inputs = self.buffers.put("inputs", np.concatenate(parts), torch.int32)
         slot_count = int(num_new[lengths > 0].sum())
-        return PackPlan(rows, tokens, width, slot_count, query_len, inputs, host)
+        return PackPlan(rows, tokens, width, slot_count, query_len, inputs, host, logits)
 
     def run(self, plan: PackPlan) -> tuple[torch.Tensor, dict]:
         """Launch the pack kernel on staged inputs; returns ``(positions, context)``."""
@@ -140,7 +152,10 @@ class Packer:
         d_cached = plan.inputs[:rows]
         d_new = plan.inputs[rows:2 * rows]
         d_indptr = plan.inputs[2 * rows:3 * rows + 1]
-        d_ids = plan.inputs[3 * rows + 1:]
+        n_ids = plan.inputs.numel() - (3 * rows + 1) - (rows if plan.logits >= 0 else 0)
+        d_ids = plan.inputs[3 * rows + 1:3 * rows + 1 + n_ids]
+        d_nlog = plan.inputs[3 * rows + 1 + n_ids:] if plan.logits >= 0 else None
+        logits = buf.device_buffer("logits_indices", plan.logits, torch.int64) if plan.logits >= 0 else None
         has_tables = width > 0
         out_order = buf.device_buffer("order", rows, torch.int32)
         cu_q = buf.device_buffer("cu_seqlens_q", rows + 1, torch.int32)
@@ -153,7 +168,9 @@ class Packer:
                    d_ids.data_ptr() if d_ids.numel() else None, rows, plan.query_len, self.block_size, width,
                    plan.tokens, out_order.data_ptr(), cu_q.data_ptr(), cu_k.data_ptr(), positions.data_ptr(),
                    slots.data_ptr() if has_tables else None, context_lens.data_ptr(),
-                   tables.data_ptr() if has_tables else None, _capi.stream_of(buf.device))
+                   tables.data_ptr() if has_tables else None,
+                   d_nlog.data_ptr() if plan.logits > 0 else None,
+                   logits.data_ptr() if plan.logits > 0 else None, _capi.stream_of(buf.device))
         context = dict(
             plan.host,
             cu_seqlens_q=cu_q,
@@ -161,6 +178,7 @@ class Packer:
             slot_mapping=slots,
             context_lens=context_lens,
             block_tables=tables.view(rows, width) if has_tables else None,
+            logits_indices=logits,
             order=out_order,
         )
         return positions, context

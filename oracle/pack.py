@@ -2,16 +2,19 @@
 
 Restates the integer part of ``ModelRunner.prepare_batch`` (``lean_vllm/engine/model_runner.py:349-464``) for
 the fields the attention path consumes: the decode-first row order, ``cu_seqlens_q/k``, ``positions``,
-``slot_mapping``, ``context_lens``, the ``-1``-padded ``block_tables`` and the host maxima. Token ids, sampling
-and speculative-decoding bookkeeping are outside the path and are not restated.
+``slot_mapping``, ``context_lens``, the ``-1``-padded ``block_tables``, the host maxima and ``logits_indices``
+(given each row's count of sampled logits rows). Token ids and the sampling and speculative-decoding bookkeeping
+that decide those counts are outside the path and are not restated.
 
 Pinned by (``tests/test_oracle_pack.py``):
 - known answers from ``tests/test_model_runner.py:29-52`` and ``:179-195`` (positions ``[0,1,2]``/``[3]``,
-  decode-first positions ``[2,0,1,2]``, ``cu_seqlens_q_host == [0,1,4]``);
+  decode-first positions ``[2,0,1,2]``, ``cu_seqlens_q_host == [0,1,4]``, ``logits_indices`` ``[2]`` and
+  ``[3, 0]``), and ``:437-443`` (a chunk that does not sample gives ``[]``);
 - ``pack_loops``, a per-token loop restatement of the reference's own test oracle ``reference_batch``
   (``tests/test_model_runner.py:509-533``) driven by a restatement of ``random_batch`` (``:536-554``), compared
   field by field as ``check_batch`` does (``:571-596``);
-- closed-form invariants (``cu`` differences equal the lengths, every slot lies in its row's own pages).
+- closed-form invariants (``cu`` differences equal the lengths, every slot lies in its row's own pages, a row
+  with d drafts samples the last d + 1 token rows of its chunk).
 """
 
 from __future__ import annotations
@@ -35,10 +38,13 @@ def pack_numpy(
     block_lists: list[list[int]],
     block_size: int,
     num_speculative_tokens: int = 0,
+    num_logits=None,
 ) -> dict:
     """Vectorised restatement of ``prepare_batch``'s packing (``model_runner.py:356-446``, ``:448-462``).
 
     Inputs are in scheduler order. Returns the batch-order fields plus ``order`` (batch row -> scheduler row).
+    ``num_logits`` (scheduler order, optional): logits rows each row samples -- its drafts + 1, or 0 for a row
+    that does not sample this step; then ``logits_indices`` follows ``model_runner.py:424-430``.
     """
     num_cached = np.asarray(num_cached, dtype=np.int64)
     num_new = np.asarray(num_new, dtype=np.int64)
@@ -64,7 +70,20 @@ def pack_numpy(
         pos = positions[has]
         blocks = block_tables[token_rows[has], pos // block_size].astype(np.int64)
         slot_mapping = (blocks * block_size + pos % block_size).astype(np.int32)
+    logits_indices = None
+    if num_logits is not None:
+        # model_runner.py:424-430: sampling rows in scheduler order, each the last num_logits token rows of its
+        # chunk (its drafts, then the next token).
+        n_all = np.asarray(num_logits, dtype=np.int64)
+        row_of = np.empty(rows, dtype=np.int64)
+        row_of[order] = np.arange(rows)
+        sampling = np.flatnonzero(n_all > 0)
+        n = n_all[sampling]
+        last_index = cu_q[1:] - 1
+        offsets = np.arange(int(n.sum())) - np.repeat(np.cumsum(n) - n, n)
+        logits_indices = (np.repeat(last_index[row_of[sampling]] - (n - 1), n) + offsets).astype(np.int64)
     return dict(
+        logits_indices=logits_indices,
         order=order.astype(np.int32),
         cu_seqlens_q=cu_q.astype(np.int32),
         cu_seqlens_k=cu_k.astype(np.int32),
@@ -80,13 +99,16 @@ def pack_numpy(
     )
 
 
-def pack_loops(num_cached, num_new, block_lists: list[list[int]], block_size: int) -> dict:
+def pack_loops(num_cached, num_new, block_lists: list[list[int]], block_size: int, sampling=None) -> dict:
     """Per-token loops, restating the reference's test oracle ``reference_batch``
-    (``tests/test_model_runner.py:509-533``) and its row order ``decodes_first`` (``:503-506``)."""
+    (``tests/test_model_runner.py:509-533``) and its row order ``decodes_first`` (``:503-506``). ``sampling``
+    (scheduler order) marks rows that sample their last token; ``logits_indices`` lists those tokens' rows in
+    scheduler order (``:521-527``)."""
     lens = [int(x) for x in num_new]
     query_len = decode_query_len(np.array(lens))
     batch = sorted(range(len(lens)), key=lambda i: lens[i] != query_len)  # sorted() is stable
     out = dict(positions=[], slot_mapping=[], cu_seqlens_q=[0], cu_seqlens_k=[0], context_lens=[], order=batch)
+    last_token = {}
     for i in batch:
         start = int(num_cached[i])
         end = start + lens[i]
@@ -94,12 +116,15 @@ def pack_loops(num_cached, num_new, block_lists: list[list[int]], block_size: in
         out["cu_seqlens_q"].append(out["cu_seqlens_q"][-1] + lens[i])
         out["cu_seqlens_k"].append(out["cu_seqlens_k"][-1] + end)
         out["context_lens"].append(end)
+        last_token[i] = out["cu_seqlens_q"][-1] - 1
         table = block_lists[i]
         if table:
             out["slot_mapping"] += [table[p // block_size] * block_size + p % block_size for p in range(start, end)]
     tables = [list(block_lists[i]) for i in batch]
     width = max((len(t) for t in tables), default=0)
     out["block_tables"] = [t + [-1] * (width - len(t)) for t in tables] if width else None
+    if sampling is not None:
+        out["logits_indices"] = [last_token[i] for i in range(len(lens)) if sampling[i]]
     return out
 
 

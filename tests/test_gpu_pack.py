@@ -14,10 +14,17 @@ from oracle import pack as P
 pytestmark = pytest.mark.gpu
 
 
-def check(packer, cached, new, lists, bs):
-    positions, ctx = packer.pack(cached, new, lists)
+def check(packer, cached, new, lists, bs, num_logits=None, drafts=0):
+    positions, ctx = packer.pack(cached, new, lists, num_speculative_tokens=drafts, num_logits=num_logits)
     torch.cuda.synchronize()
-    want = P.pack_numpy(cached, new, lists, bs)
+    prefill = bool(np.any(np.asarray(new) > 1))
+    want = P.pack_numpy(cached, new, lists, bs, drafts,
+                        num_logits=(num_logits if num_logits is not None else [1] * len(new)) if prefill else None)
+    if prefill:
+        assert ctx["logits_indices"].dtype == torch.int64
+        assert ctx["logits_indices"].tolist() == want["logits_indices"].tolist()
+    else:
+        assert ctx["logits_indices"] is None
     assert ctx["order"].tolist() == want["order"].tolist()
     assert positions.dtype == torch.int64 and positions.tolist() == want["positions"].tolist()
     for key in ("cu_seqlens_q", "cu_seqlens_k", "context_lens", "slot_mapping"):
@@ -42,13 +49,32 @@ def test_random_steps_match_the_oracle(cuda, seed):
         check(packer, cached, new, lists, 8)
 
 
+@pytest.mark.parametrize("seed", [2, 3])
+def test_random_steps_with_sampling_and_drafts_match_the_oracle(cuda, seed):
+    """Rows that do or do not sample, and decode rows verifying up to 3 drafts (drafts + 1 logits rows each)."""
+    rng = random.Random(seed)
+    packer = Packer(cuda, 8)
+    for _ in range(10):
+        cached, new, lists = P.random_rows(rng, 8)
+        drafts = rng.randint(0, 3)
+        new = [n if n > 1 else 1 + rng.randint(0, drafts) for n in new]
+        lists = [lst + [lst[-1]] * 2 if lst else lst for lst in lists]  # room for the drafts' pages
+        n_log = [rng.choice([0, 1]) if n > 1 + drafts else rng.choice([0, n]) for n in new]
+        check(packer, cached, new, lists, 8, num_logits=n_log, drafts=drafts)
+
+
 def test_known_answers(cuda):
-    """tests/test_model_runner.py:179-195."""
+    """tests/test_model_runner.py:179-195 and :29-52."""
     packer = Packer(cuda, 8)
     positions, ctx = packer.pack([0, 2], [3, 1], [[0], [0]])
     assert positions.tolist() == [2, 0, 1, 2]
     assert ctx["cu_seqlens_q_host"] == [0, 1, 4] and ctx["is_prefill"]
     assert ctx["slot_mapping"].tolist() == [2, 0, 1, 2]
+    assert ctx["logits_indices"].tolist() == [3, 0]
+    positions, ctx = packer.pack([0], [3], [[0]])
+    assert ctx["logits_indices"].tolist() == [2]
+    positions, ctx = packer.pack([3], [1], [[0]])
+    assert not ctx["is_prefill"] and ctx["logits_indices"] is None
 
 
 def test_many_rows(cuda):

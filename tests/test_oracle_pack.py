@@ -11,8 +11,9 @@ from oracle import pack as P
 
 def test_known_answer_single_prompt_and_decode():
     """tests/test_model_runner.py:29-52: a 3-token prompt packs positions [0,1,2]; its next decode step [3]."""
-    got = P.pack_numpy([0], [3], [[0]], block_size=8)
+    got = P.pack_numpy([0], [3], [[0]], block_size=8, num_logits=[1])
     assert got["positions"].tolist() == [0, 1, 2]
+    assert got["logits_indices"].tolist() == [2]
     got = P.pack_numpy([3], [1], [[0]], block_size=8)
     assert got["positions"].tolist() == [3]
     assert got["cu_seqlens_q_host"] == [0, 1] and got["context_lens"].tolist() == [4]
@@ -21,14 +22,39 @@ def test_known_answer_single_prompt_and_decode():
 def test_known_answer_one_query_rows_lead_the_batch():
     """tests/test_model_runner.py:179-195: a decoding row after a prompt in scheduler order leads the batch:
     positions [2, 0, 1, 2] and cu_seqlens_q_host [0, 1, 4]."""
-    got = P.pack_numpy([0, 2], [3, 1], [[0], [0]], block_size=8)
+    got = P.pack_numpy([0, 2], [3, 1], [[0], [0]], block_size=8, num_logits=[1, 1])
     assert got["positions"].tolist() == [2, 0, 1, 2]
     assert got["cu_seqlens_q_host"] == [0, 1, 4]
+    assert got["logits_indices"].tolist() == [3, 0]  # scheduler order: the prompt's last row, then the decode
     assert got["order"].tolist() == [1, 0]
     # closed forms for the rest of the row: both rows end at 3 keys, all in page 0
     assert got["cu_seqlens_k_host"] == [0, 3, 6]
     assert got["slot_mapping"].tolist() == [2, 0, 1, 2]
     assert got["block_tables"].tolist() == [[0], [0]]
+
+
+def test_known_answer_a_chunk_that_does_not_sample():
+    """tests/test_model_runner.py:437-443: a recomputed chunk short of its planned end gathers no logits rows."""
+    got = P.pack_numpy([2], [2], [[0]], block_size=8, num_logits=[0])
+    assert got["logits_indices"].tolist() == []
+    got = P.pack_numpy([8], [1], [[0, 1]], block_size=8, num_logits=[1])
+    assert got["logits_indices"].tolist() == [0]
+
+
+def test_rows_with_drafts_sample_their_last_token_rows():
+    """Closed form (model_runner.py:424-430): a row verifying d drafts samples the last d + 1 token rows of its
+    chunk, in order; rows keep scheduler order among themselves."""
+    cached, new = [5, 0, 9, 4], [3, 7, 3, 2]
+    n_log = [3, 1, 0, 2]
+    got = P.pack_numpy(cached, new, [[0, 1]] * 4, block_size=8, num_speculative_tokens=2, num_logits=n_log)
+    ends = dict(zip(got["order"].tolist(), got["cu_seqlens_q"][1:].tolist()))
+    want = []
+    for s, n in enumerate(n_log):
+        want += list(range(ends[s] - n, ends[s]))
+    assert got["logits_indices"].tolist() == want
+    # a planted mistake (indices from the chunk's first row) is told apart
+    firsts = dict(zip(got["order"].tolist(), got["cu_seqlens_q"][:-1].tolist()))
+    assert want != [firsts[s] + j for s, n in enumerate(n_log) for j in range(n)]
 
 
 def test_query_len_is_the_most_common_short_length():
@@ -47,8 +73,10 @@ def test_vectorised_packing_matches_the_per_token_loops(seed):
     bs = 8
     for step in range(20):
         cached, new, lists = P.random_rows(rng, bs, with_tables=step % 5 != 0)
-        got = P.pack_numpy(cached, new, lists, bs)
-        want = P.pack_loops(cached, new, lists, bs)
+        sampling = [rng.random() < 0.7 for _ in new]
+        got = P.pack_numpy(cached, new, lists, bs, num_logits=[int(x) for x in sampling])
+        want = P.pack_loops(cached, new, lists, bs, sampling=sampling)
+        assert got["logits_indices"].tolist() == want["logits_indices"]
         assert got["order"].tolist() == want["order"]
         assert got["positions"].tolist() == want["positions"]
         assert got["slot_mapping"].tolist() == want["slot_mapping"]
