@@ -260,4 +260,16 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleSlack = 8.f;
 constexpr float kLn2 = 0.6931471805599453f;
 
+// Compute units of the current device (cached per device; 256 on MI355X). Host code.
+inline int device_cus() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+  if (dev < 64 && cached[dev] > 0) return cached[dev];
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+  if (dev < 64) cached[dev] = cus;
+  return cus;
+}
+
 }  // namespace lv

@@ -797,17 +797,6 @@ struct MlaShape {
   size_t lse_off, o_off, prefix_off, bytes;
 };
 
-// Compute units of the current device (cached per device; 256 on MI355X).
-static int device_cus() {
-  static int cached[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
-  if (dev < 64 && cached[dev] > 0) return cached[dev];
-  int cus = 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-  if (dev < 64) cached[dev] = cus;
-  return cus;
-}
 
 template <typename T>
 static void launch_dma(const MlaParams& p, bool one_page, dim3 grid, hipStream_t st) {

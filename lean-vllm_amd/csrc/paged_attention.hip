@@ -12,6 +12,9 @@
 //
 // Math: TorchAttention.decode / prefill (lean_vllm/attention/torch_backend.py:62-103,159-181): query head h reads
 // key head h / (Hq/Hkv); query j of a row with lq queries and lk keys sees keys 0..lk-lq+j.
+#include <algorithm>
+#include <mutex>
+
 #include "attn_common.h"
 
 namespace lv {
@@ -25,6 +28,9 @@ constexpr int kPlanMaxRows = 4096;  // rows of a step with prompts (the work-lis
 #endif
 #ifndef LV_PROMPT_PREFETCH
 #define LV_PROMPT_PREFETCH true
+#endif
+#ifndef LV_OVERLAP
+#define LV_OVERLAP 1
 #endif
 #ifndef LV_SPLIT_TARGET
 #define LV_SPLIT_TARGET 4096
@@ -344,6 +350,23 @@ __global__ __launch_bounds__(256, 2) void prompt_list_kernel(AttnParams p) {
   prefill_item<T, D, D, LV_PROMPT_PREFETCH>(p, it.x, -1 - it.y, kvh, smem);
 }
 
+// Prompt items of a mixed step, run at the same time as its decode items: one workgroup per CU, each walking the
+// prompt items blockIdx.x, + gridDim.x, ... in list order. Its LDS request (padded at launch, so the compiler still
+// budgets registers for 2 waves per SIMD) leaves room for no second one, and the decode workgroups take the CU's
+// remaining registers: the MFMA work of the prompt tiles hides under the decode rows' memory streaming.
+constexpr int kOverlapLds = 84 * 1024;
+template <typename T, int D>
+__global__ __launch_bounds__(256, 2) void prompt_overlap_kernel(AttnParams p) {
+  __shared__ __attribute__((aligned(16))) char smem[PromptSmem<D, D>::kBytes];
+  const int n = p.n_items[1] * p.hkv;
+  for (int f = blockIdx.x; f < n; f += gridDim.x) {
+    const int bx = f / p.hkv, kvh = f - bx * p.hkv;
+    const int2 it = p.items[bx];
+    prefill_item<T, D, D, LV_PROMPT_PREFETCH>(p, it.x, -1 - it.y, kvh, smem);
+    __syncthreads();  // the next item restages the LDS tiles
+  }
+}
+
 // Decode of more rows than the planner holds: blockIdx.x is (row, split), blockIdx.y the query-head group.
 template <typename T, int D, int GS>
 __global__ __launch_bounds__(256) void decode_grid_kernel(AttnParams p) {
@@ -504,10 +527,53 @@ static Shape plan_shape(int32_t rows, int32_t tokens, int32_t hq, int32_t hkv, i
   return s;
 }
 
+// A second stream per device and the fork/join events that tie it to the caller's stream, created on first use.
+// The mutex makes each call's record / wait / launch sequence atomic against calls from other host threads that
+// share the device's second stream.
+struct SideStream {
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+  std::mutex lock;
+};
+static SideStream* side_stream() {
+  static SideStream side[64];
+  static std::mutex create;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  SideStream& s = side[dev];
+  std::lock_guard<std::mutex> g(create);
+  if (!s.stream) {  // default priority, non-blocking with respect to the legacy stream
+    hipStream_t st = nullptr;
+    hipEvent_t f = nullptr, j = nullptr;
+    if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&f, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&j, hipEventDisableTiming) != hipSuccess)
+      return nullptr;
+    s.fork = f;
+    s.join = j;
+    s.stream = st;
+  }
+  return &s;
+}
+
 template <typename T, int D, int GS>
 static void launch(const AttnParams& p, bool listed, bool mixed, const Shape& s, hipStream_t stream) {
   const int ny = p.hkv * p.qgroups;
-  if (listed && mixed) {
+  SideStream* side = LV_OVERLAP && listed && mixed ? side_stream() : nullptr;
+  if (side) {
+    // Decode items go to the second stream first, then the prompt items to the caller's stream: the prompt
+    // workgroups (one per CU) are dispatched as soon as the plan ends, the decode workgroups fill the rest.
+    constexpr int pad = kOverlapLds - PromptSmem<D, D>::kBytes;
+    const int grid = std::min(s.max_prompt_items * p.hkv, device_cus());
+    std::lock_guard<std::mutex> g(side->lock);
+    hipEventRecord(side->fork, stream);
+    hipStreamWaitEvent(side->stream, side->fork, 0);
+    hipLaunchKernelGGL((decode_list_kernel<T, D, GS>), dim3(s.max_decode_items * ny), dim3(256), 0, side->stream,
+                       p);
+    hipEventRecord(side->join, side->stream);
+    hipLaunchKernelGGL((prompt_overlap_kernel<T, D>), dim3(grid), dim3(256), pad, stream, p);
+    hipStreamWaitEvent(stream, side->join, 0);
+  } else if (listed && mixed) {
     hipLaunchKernelGGL((prompt_list_kernel<T, D>), dim3(s.max_prompt_items * p.hkv), dim3(256), 0, stream, p);
     hipLaunchKernelGGL((decode_list_kernel<T, D, GS>), dim3(s.max_decode_items * ny), dim3(256), 0, stream, p);
   } else if (listed) {
