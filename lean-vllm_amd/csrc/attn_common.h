@@ -60,7 +60,9 @@ struct PromptSmem {
 };
 
 // PREFETCH: the next tile's K/V loads are in flight in registers while this tile is consumed (more registers).
-template <typename T, int DQK, int DV, bool PREFETCH = true>
+// OPAQUE_TID: for a caller that runs items in a loop; the thread index is hidden from the optimiser, so per-lane
+// offsets are recomputed per item rather than hoisted out of the loop and spilled.
+template <typename T, int DQK, int DV, bool PREFETCH = true, bool OPAQUE_TID = false>
 __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, char* smem) {
   using E = Elem<T>;
   constexpr int KS = DQK / 32;  // MFMA k-steps over the q.k width
@@ -75,7 +77,9 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
   static_assert(DQK % 32 == 0 && DV % 16 == 0, "MFMA tile widths");
   uint16_t* ks = reinterpret_cast<uint16_t*>(smem);  // [64 keys][KROW]
   uint16_t* vs = ks + kPrefillKeys * KROW;            // [64 keys][VROW]
-  const int tid = threadIdx.x, lane = tid & 63;
+  int tid = threadIdx.x;
+  if (OPAQUE_TID) asm volatile("" : "+v"(tid));
+  const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, j4 = lane >> 4;
   const int G = p.group;

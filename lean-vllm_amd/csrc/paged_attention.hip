@@ -32,6 +32,9 @@ constexpr int kPlanMaxRows = 4096;  // rows of a step with prompts (the work-lis
 #ifndef LV_OVERLAP
 #define LV_OVERLAP 1
 #endif
+#ifndef LV_OVERLAP_CUS
+#define LV_OVERLAP_CUS 75  // percent of the CUs that hold a prompt workgroup in a mixed step (swept: 60-100)
+#endif
 #ifndef LV_SPLIT_TARGET
 #define LV_SPLIT_TARGET 4096
 #endif
@@ -362,7 +365,7 @@ __global__ __launch_bounds__(256, 2) void prompt_overlap_kernel(AttnParams p) {
   for (int f = blockIdx.x; f < n; f += gridDim.x) {
     const int bx = f / p.hkv, kvh = f - bx * p.hkv;
     const int2 it = p.items[bx];
-    prefill_item<T, D, D, LV_PROMPT_PREFETCH>(p, it.x, -1 - it.y, kvh, smem);
+    prefill_item<T, D, D, LV_PROMPT_PREFETCH, true>(p, it.x, -1 - it.y, kvh, smem);
     __syncthreads();  // the next item restages the LDS tiles
   }
 }
@@ -564,7 +567,7 @@ static void launch(const AttnParams& p, bool listed, bool mixed, const Shape& s,
     // Decode items go to the second stream first, then the prompt items to the caller's stream: the prompt
     // workgroups (one per CU) are dispatched as soon as the plan ends, the decode workgroups fill the rest.
     constexpr int pad = kOverlapLds - PromptSmem<D, D>::kBytes;
-    const int grid = std::min(s.max_prompt_items * p.hkv, device_cus());
+    const int grid = std::min(s.max_prompt_items * p.hkv, std::max(1, device_cus() * LV_OVERLAP_CUS / 100));
     std::lock_guard<std::mutex> g(side->lock);
     hipEventRecord(side->fork, stream);
     hipStreamWaitEvent(side->stream, side->fork, 0);
