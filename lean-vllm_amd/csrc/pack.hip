@@ -17,7 +17,8 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
     const int32_t* __restrict__ blk_ids, int32_t rows, int32_t query_len, int32_t bs, int32_t width, int32_t tokens,
     int32_t* __restrict__ order, int32_t* __restrict__ cu_q_out, int32_t* __restrict__ cu_k_out,
     int64_t* __restrict__ positions, int32_t* __restrict__ slots, int32_t* __restrict__ context_lens,
-    int32_t* __restrict__ tables, const int32_t* __restrict__ num_logits, int64_t* __restrict__ logits) {
+    int32_t* __restrict__ tables, const int32_t* __restrict__ num_logits, int64_t* __restrict__ logits,
+    bool dense_slots) {
   __shared__ int src[kPackMaxRows];       // batch row -> scheduler row
   __shared__ int cu_q[kPackMaxRows + 1];  // token offsets, batch order
   __shared__ int cu_s[kPackMaxRows + 1];  // slot_mapping offsets (rows with a block list only), batch order
@@ -41,7 +42,7 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
   for (int r = tid; r < rows; r += kPackThreads) {
     const int s = src[r];
     cu_q[r] = num_new[s];
-    cu_s[r] = indptr[s + 1] > indptr[s] ? num_new[s] : 0;
+    cu_s[r] = dense_slots || indptr[s + 1] > indptr[s] ? num_new[s] : 0;
   }
   __syncthreads();
   block_scan(cu_q, rows, wave_tot);
@@ -74,6 +75,8 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
     if (len > 0) {
       const int64_t block = blk_ids[list + (int)(pos / bs)];
       slots[cu_s[r] + offset] = (int32_t)(block * bs + pos % bs);
+    } else if (dense_slots) {
+      slots[cu_s[r] + offset] = -1;  // a padding row of a captured step: its tokens store nothing
     }
   }
 
@@ -129,7 +132,8 @@ extern "C" int lv_pack(const int32_t* num_cached, const int32_t* num_new, const 
                        const int32_t* blk_ids, int32_t num_rows, int32_t query_len, int32_t block_size,
                        int32_t table_width, int32_t num_tokens, int32_t* order, int32_t* cu_seqlens_q,
                        int32_t* cu_seqlens_k, int64_t* positions, int32_t* slot_mapping, int32_t* context_lens,
-                       int32_t* block_tables, const int32_t* num_logits, int64_t* logits_indices, void* stream) {
+                       int32_t* block_tables, const int32_t* num_logits, int64_t* logits_indices, int32_t flags,
+                       void* stream) {
   LV_REQUIRE(num_rows > 0 && num_rows <= kPackMaxRows, "pack: %d rows; 1 to %d are supported", num_rows,
              kPackMaxRows);
   LV_REQUIRE(block_size > 0, "pack: block_size must be positive, got %d", block_size);
@@ -139,13 +143,16 @@ extern "C" int lv_pack(const int32_t* num_cached, const int32_t* num_new, const 
   LV_REQUIRE(num_tokens == 0 || positions, "pack: null positions");
   LV_REQUIRE(table_width == 0 || (block_tables && blk_ids && slot_mapping), "pack: null table pointer");
   LV_REQUIRE(!num_logits || logits_indices, "pack: num_logits given without logits_indices");
+  LV_REQUIRE((flags & ~LV_PACK_DENSE_SLOTS) == 0, "pack: unknown flags 0x%x", flags);
+  const bool dense = (flags & LV_PACK_DENSE_SLOTS) != 0;
+  LV_REQUIRE(!dense || num_tokens == 0 || slot_mapping, "pack: dense slots need slot_mapping");
   const int64_t work = (int64_t)num_tokens + (int64_t)num_rows * table_width;
   int grid = (int)((work + kPackThreads * 4 - 1) / (kPackThreads * 4));
   grid = grid < 1 ? 1 : (grid > 64 ? 64 : grid);
   hipLaunchKernelGGL(pack_kernel, dim3(grid), dim3(kPackThreads), 0, reinterpret_cast<hipStream_t>(stream),
                      num_cached, num_new, blk_indptr, blk_ids, num_rows, query_len, block_size, table_width,
                      num_tokens, order, cu_seqlens_q, cu_seqlens_k, positions, slot_mapping, context_lens,
-                     block_tables, num_logits, logits_indices);
+                     block_tables, num_logits, logits_indices, dense);
   LV_LAUNCH_CHECK("pack_kernel");
   return LV_OK;
 }

@@ -2,6 +2,7 @@
 
 - ``MI355XAttention``: the per-layer attention backend (store_kvcache, decode, prefill, mixed steps).
 - ``Packer``: the ragged-batch packing of a step on the GPU.
+- ``DecodeGraphs``: full-graph decode steps (pack, store and attention captured per batch size).
 - ``merge_attention`` / ``merge_attention_``: the log-sum-exp merge of two partial attentions.
 - ``Context``, ``LayerSpec``, ``AttentionBackend``, ``get_attention_backend``: the reference's interface.
 """
@@ -11,12 +12,14 @@ from .backend import MI355XAttention
 from .merge import merge_attention, merge_attention_
 from .context import Context, get_context, reset_context, set_context, split_decodes_and_prefills, use_context
 from .pack import Packer, StagingBuffers, decode_query_len
+from .graphs import DecodeGraphs
 from .selector import BACKENDS, get_attention_backend
 
 __all__ = [
     "BACKENDS",
     "AttentionBackend",
     "Context",
+    "DecodeGraphs",
     "LayerSpec",
     "MI355XAttention",
     "Packer",

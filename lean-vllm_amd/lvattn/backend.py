@@ -31,10 +31,13 @@ def _arch_ok() -> bool:
 
 class _Workspace:
     """One growing device buffer per device for split-K partials and work lists. Its contents need no
-    initialisation, so a captured graph replays with whatever the last call left."""
+    initialisation, so a captured graph replays with whatever the last call left. A buffer outgrown by a later
+    call is kept, not freed: a graph captured earlier still addresses it. Calls that share it are ordered on one
+    stream per device (as the engine's step loop issues them)."""
 
     def __init__(self):
         self._buf: dict[torch.device, torch.Tensor] = {}
+        self._retired: list[torch.Tensor] = []
 
     def get(self, device: torch.device, nbytes: int) -> torch.Tensor | None:
         if nbytes == 0:
@@ -42,6 +45,8 @@ class _Workspace:
         buf = self._buf.get(device)
         if buf is None or buf.numel() < nbytes:
             size = max(nbytes, 2 * (buf.numel() if buf is not None else 0), 1 << 20)
+            if buf is not None:
+                self._retired.append(buf)
             buf = torch.empty(size, dtype=torch.uint8, device=device)
             self._buf[device] = buf
         return buf

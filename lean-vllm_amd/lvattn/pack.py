@@ -170,7 +170,7 @@ class Packer:
                    slots.data_ptr() if has_tables else None, context_lens.data_ptr(),
                    tables.data_ptr() if has_tables else None,
                    d_nlog.data_ptr() if plan.logits > 0 else None,
-                   logits.data_ptr() if plan.logits > 0 else None, _capi.stream_of(buf.device))
+                   logits.data_ptr() if plan.logits > 0 else None, 0, _capi.stream_of(buf.device))
         context = dict(
             plan.host,
             cu_seqlens_q=cu_q,

@@ -39,12 +39,15 @@ def pack_numpy(
     block_size: int,
     num_speculative_tokens: int = 0,
     num_logits=None,
+    dense_slots: bool = False,
 ) -> dict:
     """Vectorised restatement of ``prepare_batch``'s packing (``model_runner.py:356-446``, ``:448-462``).
 
     Inputs are in scheduler order. Returns the batch-order fields plus ``order`` (batch row -> scheduler row).
     ``num_logits`` (scheduler order, optional): logits rows each row samples -- its drafts + 1, or 0 for a row
     that does not sample this step; then ``logits_indices`` follows ``model_runner.py:424-430``.
+    ``dense_slots``: one slot per token, -1 for rows without a block list, as a captured graph's padded rows
+    carry (``model_runner.py:597-602``), instead of the compacted eager form (``:442-445``).
     """
     num_cached = np.asarray(num_cached, dtype=np.int64)
     num_new = np.asarray(num_new, dtype=np.int64)
@@ -70,6 +73,10 @@ def pack_numpy(
         pos = positions[has]
         blocks = block_tables[token_rows[has], pos // block_size].astype(np.int64)
         slot_mapping = (blocks * block_size + pos % block_size).astype(np.int32)
+        if dense_slots:
+            dense = np.full(int(cu_q[-1]), -1, dtype=np.int32)
+            dense[has] = slot_mapping
+            slot_mapping = dense
     logits_indices = None
     if num_logits is not None:
         # model_runner.py:424-430: sampling rows in scheduler order, each the last num_logits token rows of its

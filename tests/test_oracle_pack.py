@@ -57,6 +57,17 @@ def test_rows_with_drafts_sample_their_last_token_rows():
     assert want != [firsts[s] + j for s, n in enumerate(n_log) for j in range(n)]
 
 
+def test_dense_slots_pad_rows_without_a_table_with_minus_one():
+    """A captured graph's padding rows (model_runner.py:597-602): one slot per token, -1 where the row has no
+    block list; the kept entries are the compacted eager slots, in order."""
+    cached, new, lists = [4, -1, 9, -1], [1, 1, 1, 1], [[3], [], [5, 6], []]
+    eager = P.pack_numpy(cached, new, lists, 8)
+    dense = P.pack_numpy(cached, new, lists, 8, dense_slots=True)
+    assert dense["slot_mapping"].tolist() == [28, -1, 49, -1]
+    assert dense["slot_mapping"][dense["slot_mapping"] >= 0].tolist() == eager["slot_mapping"].tolist()
+    assert dense["context_lens"].tolist() == [5, 0, 10, 0]
+
+
 def test_query_len_is_the_most_common_short_length():
     """model_runner.py:51-63: most common length <= 1 + drafts, the shorter on ties, else 1."""
     assert P.decode_query_len(np.array([1, 1, 5, 3])) == 1
