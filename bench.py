@@ -13,7 +13,8 @@ cached prefix U[0, 6144], plus 2048 decode rows with context U[256, 4096]; 32/8 
 pages). The line also carries per-kernel times from HIP events on the launch stream, a ``roofline`` object for
 the attention op, a ``cpu_baseline`` (the oracle's restatement of the reference PyTorch backend timed on a bounded
 sample on the host cores) and, under ``workloads``, the same figures for the other shapes this path is measured on
-(Qwen3-8B pure decode at batch 256, long-context split-K decode, DeepSeek-V2-Lite MLA decode, Qwen3-0.6B mixed).
+(Qwen3-8B pure decode at batch 256, long-context split-K decode, DeepSeek-V2-Lite MLA decode, Qwen3-0.6B mixed,
+and DeepSeek-V2-Lite MLA prefill chunks, which are MFMA work and report TFLOP/s against the bf16 peak).
 """
 
 from __future__ import annotations
@@ -33,7 +34,7 @@ for _p in (ROOT, ROOT / "lean-vllm_amd"):
 PEAK_HBM_GBS = 8000.0
 PEAK_BF16_TFLOPS = 2500.0
 METRIC = "paged-attn HBM GB/s (% of peak) + tokens/s per layer, Qwen3-8B mixed batch"
-EXTRA = "qwen3_8b_decode,qwen3_8b_long,deepseek_v2_lite_mla,qwen3_0_6b_mixed"
+EXTRA = "qwen3_8b_decode,qwen3_8b_long,deepseek_v2_lite_mla,qwen3_0_6b_mixed,deepseek_v2_lite_mla_prefill"
 # Workloads whose whole working set fits the 256 MB Infinity Cache: each timed step starts from a flushed cache.
 FLUSHED = {"qwen3_0_6b_mixed"}
 
@@ -70,17 +71,24 @@ def measure(name: str, steps: int, warmup: int, seed: int, dev):
     """Time ``steps`` steps of one workload; returns (figures, workload, tensors)."""
     import torch
 
-    from lvattn import Context, MI355XAttention, Packer
+    import numpy as np
+
+    from lvattn import Context, MI355XAttention, Packer, merge_attention_
     from lvattn import workloads as W
 
     wl = W.WORKLOADS[name](seed)
     t = W.materialize(wl, dev, torch.bfloat16, seed=seed)
     heads_kv = wl.num_heads if wl.is_mla else wl.num_kv_heads
-    backend = MI355XAttention(wl.num_heads, wl.latent_dim if wl.is_mla else wl.head_dim, wl.scale, heads_kv)
+    head_dim = wl.expanded[0] if wl.is_mla_prefill else wl.latent_dim if wl.is_mla else wl.head_dim
+    backend = MI355XAttention(wl.num_heads, head_dim, wl.scale, heads_kv)
     packer = Packer(dev, wl.block_size)
     plan = packer.stage(wl.num_cached, wl.num_new, wl.block_lists)
-    out = torch.empty(wl.tokens, wl.num_heads, wl.v_dim if wl.is_mla else wl.head_dim, dtype=torch.bfloat16,
-                      device=dev)
+    out_dim = wl.expanded[1] if wl.is_mla_prefill else wl.v_dim if wl.is_mla else wl.head_dim
+    out = torch.empty(wl.tokens, wl.num_heads, out_dim, dtype=torch.bfloat16, device=dev)
+    if wl.is_mla_prefill:  # the cached prefix as one unmasked chunk (layers/attention.py:288-315)
+        ex = t.expanded
+        cu_ctx = torch.tensor([0, *np.cumsum(wl.num_cached).tolist()], dtype=torch.int32, device=dev)
+        max_ctx = max(max(wl.num_cached), 1)
     flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev) if name in FLUSHED else None
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
@@ -101,7 +109,12 @@ def measure(name: str, steps: int, warmup: int, seed: int, dev):
         if i is not None:
             ev["c"][i].record(stream)
         fields = {k: v for k, v in ctx.items() if k in Context.__slots__}
-        if wl.is_mla:
+        if wl.is_mla_prefill:
+            cu_q, max_q = ctx["cu_seqlens_q"], ctx["max_seqlen_q"]
+            o, lse = backend.varlen_with_lse(ex["q"], ex["k"], ex["v"], cu_q, cu_q, max_q, max_q, True)
+            co, clse = backend.varlen_with_lse(ex["q"], ex["k_ctx"], ex["v_ctx"], cu_q, cu_ctx, max_q, max_ctx, False)
+            merge_attention_(co, clse, o, lse, out)
+        elif wl.is_mla:
             backend.mla_decode(t.q, t.k_cache, wl.v_dim, Context(**fields), out=out)
         else:
             backend.forward(t.q, t.k_new, t.v_new, t.k_cache, t.v_cache, Context(**fields), out=out)
@@ -137,6 +150,8 @@ def measure(name: str, steps: int, warmup: int, seed: int, dev):
         "attention_GBs": round(attn_gbs, 1),
         "attention_frac_of_peak": round(attn_gbs / PEAK_HBM_GBS, 4),
         "attention_TFLOPs": round(flops / (attn_ms * 1e-3) / 1e12, 2),
+        "attention_frac_of_mfma_peak": round(flops / (attn_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "bound": "mfma" if wl.is_mla_prefill else "hbm",
         "bytes": nbytes,
         "flops": flops,
         "cache_flushed_each_step": flush is not None,
@@ -226,6 +241,8 @@ def cpu_baseline(wl, t, dec_sample: int = 4096):
 
 def attention_op(wl) -> str:
     """The kernels of one attention op on this workload (the roofline's subject)."""
+    if wl.is_mla_prefill:
+        return "lv_varlen_attention x2 (causal new tokens, unmasked prefix; varlen_kernel) + lv_merge_attn_states"
     if wl.is_mla:
         return "lv_mla_decode (mla_run_kernel + mla_run_merge_kernel)"
     if any(n > 1 for n in wl.num_new):

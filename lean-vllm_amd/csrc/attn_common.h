@@ -62,7 +62,10 @@ struct PromptSmem {
 // PREFETCH: the next tile's K/V loads are in flight in registers while this tile is consumed (more registers).
 // OPAQUE_TID: for a caller that runs items in a loop; the thread index is hidden from the optimiser, so per-lane
 // offsets are recomputed per item rather than hoisted out of the loop and spilled.
-template <typename T, int DQK, int DV, bool PREFETCH = true, bool OPAQUE_TID = false>
+// RING > 0: tiles go straight from memory into a ring of RING LDS stages (smem holds RING * PromptSmem::kBytes),
+// RING - 1 in flight while one is consumed, one barrier per tile; for keys whose 64-key tiles each lie in one page
+// (unpaged, or pages a multiple of 64). The caller picks it; the register path serves every other page size.
+template <typename T, int DQK, int DV, bool PREFETCH = true, bool OPAQUE_TID = false, int RING = 0>
 __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, char* smem) {
   using E = Elem<T>;
   constexpr int KS = DQK / 32;  // MFMA k-steps over the q.k width
@@ -75,8 +78,6 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
   constexpr int PER = kPrefillKeys * (KCH + VCH) / 256;  // all chunks each thread stages per tile
   static_assert(KCHUNKS % 256 == 0 && kPrefillKeys * (KCH + VCH) % 256 == 0, "tile chunks split over 256 threads");
   static_assert(DQK % 32 == 0 && DV % 16 == 0, "MFMA tile widths");
-  uint16_t* ks = reinterpret_cast<uint16_t*>(smem);  // [64 keys][KROW]
-  uint16_t* vs = ks + kPrefillKeys * KROW;            // [64 keys][VROW]
   int tid = threadIdx.x;
   if (OPAQUE_TID) asm volatile("" : "+v"(tid));
   const int lane = tid & 63;
@@ -154,7 +155,7 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
       }
     }
   };
-  auto stash = [&](const u32x4 (&st)[PER]) {
+  auto stash = [&](uint16_t* ks, uint16_t* vs, const u32x4 (&st)[PER]) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       uint16_t* dst = i < KPER ? ks + key_of(i) * KROW : vs + key_of(i) * VROW;
@@ -162,15 +163,8 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
     }
   };
 
-  u32x4 stage[PER];
-  if (PREFETCH && kmax > 0) fetch(0, stage);
-  for (int kt = 0; kt < kmax; kt += kPrefillKeys) {
-    if (!PREFETCH) fetch(kt, stage);
-    __syncthreads();  // the previous tile's operand reads are done
-    stash(stage);
-    __syncthreads();
-    if (PREFETCH && kt + kPrefillKeys < kmax) fetch(kt + kPrefillKeys, stage);
-
+  // One 64-key tile from the K/V tile in LDS at ks / vs: scores, mask, online softmax, P.V.
+  auto consume = [&](int kt, const uint16_t* ks, const uint16_t* vs) {
     // S^T (keys x query rows): st[kb][nb] lane holds keys kt + 16 kb + 4 j4 + r of query row (nb, n).
     f32x4 st[4][2];
 #pragma unroll
@@ -251,6 +245,89 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) o[nb][b] = E::mfma16x16x32(a, pb[nb][h], o[nb][b]);
       }
+  };
+
+  if constexpr (RING > 0) {
+    // Stage layout: key rows of KCH data slots + 1 pad slot, then value rows of VCH + 2 (the tile pitches); the
+    // pad slots hold a copy of the row's last chunk. 64-lane load j covers slots 64 j .. 64 j + 63; wave w issues
+    // j = w, w + 4, ... Keys at or past lk load key lk - 1 instead (finite values; their weight is 0).
+    constexpr int KJ = KCH + 1, VJ = VCH + 2;  // loads per stage for the key / value rows (64 keys each)
+    constexpr int NJ = KJ + VJ;
+    constexpr int CNT_HI = (NJ + 3) / 4, CNT_LO = NJ / 4;  // this wave's loads per stage: waves < NJ % 4 take HI
+    constexpr int kStageElems = PromptSmem<DQK, DV>::kBytes / 2;
+    static_assert(PromptSmem<DQK, DV>::kKRow == KJ * 8 && PromptSmem<DQK, DV>::kVRow == VJ * 8, "pitches");
+    static_assert(RING >= 2 && RING <= 3, "one or two tiles in flight");
+    uint16_t* ring = reinterpret_cast<uint16_t*>(smem);
+    const bool hi = wave < NJ % 4 || NJ % 4 == 0;
+    auto base_of = [&](int kt, bool v) -> const char* {  // wave-uniform source of key kt
+      const char* src = v ? p.v_cache : p.k_cache;
+      const int64_t st = v ? p.v_st : p.c_st, sh = v ? p.v_sh : p.c_sh;
+      if (p.paged) {
+        const int pg = (int)p.bs.div(kt);
+        return src + (int64_t)sload(table + pg) * p.c_sb + (int64_t)(kt - pg * (int)p.bs.d) * st + kvh * sh;
+      }
+      return src + (int64_t)(kbase + kt) * st + kvh * sh;
+    };
+    auto fill = [&](int kt, uint16_t* stage) {
+      const int last = lk - 1 - kt;
+      const char* kb = base_of(kt, false);
+      const char* vb = base_of(kt, true);
+#pragma unroll
+      for (int i = 0; i < (NJ + 3) / 4; ++i) {
+        const int j = wave + 4 * i;
+        if (j < NJ) {
+          uint32_t off;
+          const char* b;
+          if (j < KJ) {
+            const int slot = 64 * j + lane, key = slot / KJ;
+            off = (uint32_t)(min(key, last) * (int)p.c_st + min(slot - key * KJ, KCH - 1) * 16);
+            b = kb;
+          } else {
+            const int slot = 64 * (j - KJ) + lane, key = slot / VJ;
+            off = (uint32_t)(min(key, last) * (int)p.v_st + min(slot - key * VJ, VCH - 1) * 16);
+            b = vb;
+          }
+          lds_dma16<false>(b, off, lds_addr(stage + 64 * 8 * j));  // tiles other query tiles read again
+        }
+      }
+    };
+    // q must be in registers before the stage loads are counted. Reading q here makes the compiler wait for its
+    // loads now, outside the loop; otherwise its own wait lands at q's first use inside the loop, where it would
+    // also wait for every stage in flight.
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+      for (int k = 0; k < KS; ++k) asm volatile("" ::"v"(qb[nb][k]));
+    int issued = 0;
+    for (; issued < RING - 1 && issued * kPrefillKeys < kmax; ++issued)
+      fill(issued * kPrefillKeys, ring + issued * kStageElems);
+    for (int it = 0, kt = 0; kt < kmax; ++it, kt += kPrefillKeys) {
+      // This wave's loads of tile `it` have landed when only the later tiles' are outstanding; the barrier makes
+      // every wave's visible and frees the slot read last iteration.
+      const int ahead = issued - it - 1;
+      if (ahead == 0) vm_wait_barrier<0>();
+      else if (ahead == 1) { if (hi) vm_wait_barrier<CNT_HI>(); else vm_wait_barrier<CNT_LO>(); }
+      else { if (hi) vm_wait_barrier<2 * CNT_HI>(); else vm_wait_barrier<2 * CNT_LO>(); }
+      if (issued * kPrefillKeys < kmax) {
+        fill(issued * kPrefillKeys, ring + (issued % RING) * kStageElems);
+        ++issued;
+      }
+      const uint16_t* ks = ring + (it % RING) * kStageElems;
+      consume(kt, ks, ks + kPrefillKeys * KROW);
+    }
+  } else {
+    uint16_t* ks = reinterpret_cast<uint16_t*>(smem);  // [64 keys][KROW]
+    uint16_t* vs = ks + kPrefillKeys * KROW;            // [64 keys][VROW]
+    u32x4 stage[PER];
+    if (PREFETCH && kmax > 0) fetch(0, stage);
+    for (int kt = 0; kt < kmax; kt += kPrefillKeys) {
+      if (!PREFETCH) fetch(kt, stage);
+      __syncthreads();  // the previous tile's operand reads are done
+      stash(ks, vs, stage);
+      __syncthreads();
+      if (PREFETCH && kt + kPrefillKeys < kmax) fetch(kt + kPrefillKeys, stage);
+      consume(kt, ks, vs);
+    }
   }
 
 #pragma unroll

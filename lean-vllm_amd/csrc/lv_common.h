@@ -272,4 +272,66 @@ inline int device_cus() {
   return cus;
 }
 
+// ---------------------------------------------------------------------------------------------------------
+// Loads straight from global memory into LDS (global_load_lds_dwordx4), for staging rings.
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// STREAM: rows this launch reads once (non-temporal, as ld16_stream); otherwise cached, for tiles that other
+// workgroups read again.
+#if LV_STREAM_NT
+#define LV_DMA_NT " nt"
+#else
+#define LV_DMA_NT ""
+#endif
+
+// One 16-byte load per lane from base + off into LDS at lds_base + 16 lane (lds_base wave-uniform, set through
+// M0). Issued as inline assembly so that the compiler, which cannot tell which LDS bytes the load writes, adds no
+// wait-for-every-load before later LDS reads; the kernel waits for these loads itself (vmcnt).
+template <bool STREAM = true>
+__device__ __forceinline__ void lds_dma16(const char* base, uint32_t off, uint32_t lds_base) {
+  if (STREAM)
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" LV_DMA_NT ::"v"(off), "s"(base),
+                 "s"(lds_base)
+                 : "memory", "m0");
+  else
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base),
+                 "s"(lds_base)
+                 : "memory", "m0");
+}
+
+// As above, from a per-lane address.
+template <bool STREAM = true>
+__device__ __forceinline__ void lds_dma16(const char* src, uint32_t lds_base) {
+  if (STREAM)
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" LV_DMA_NT ::"v"(src),
+                 "s"(lds_base)
+                 : "memory", "m0");
+  else
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_base)
+                 : "memory", "m0");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(lds_void_t*)p;
+}
+
+// Load of a wave-uniform int through the scalar cache. For tables this kernel only reads: the compiler would use
+// a vector load here (the kernel's stores might alias), and its wait for that load would also wait for every
+// latent load in flight.
+__device__ __forceinline__ int sload(const int32_t* ptr) {
+  int v;
+  asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(ptr));
+  return v;
+}
+
+// Wait until at most N of this wave's vector-memory operations are outstanding, then meet the other waves. No
+// fence: a staging ring's LDS writes are exactly the loads waited for, and a fence would also wait for the stages
+// still in flight.
+template <int N>
+__device__ __forceinline__ void vm_wait_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
 }  // namespace lv

@@ -233,34 +233,6 @@ constexpr int kDmaInstr = (kDmaStageSlots + 63) / 64;   // 64-lane loads per sta
 constexpr int kDmaStageElems = kDmaStageSlots * 8;
 static_assert(kDmaRowSlots * 8 == kMlaPitch, "one LDS row pitch for both variants");
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-
-// Cache rows are read once per launch: non-temporal, as ld16_stream.
-#if LV_STREAM_NT
-#define LV_DMA_NT " nt"
-#else
-#define LV_DMA_NT ""
-#endif
-
-// One 16-byte load per lane from base + off into LDS at lds_base + 16 lane (lds_base wave-uniform, set through
-// M0). Issued as inline assembly so that the compiler, which cannot tell which LDS bytes the load writes, adds no
-// wait-for-every-load before later LDS reads; the kernel waits for these loads itself (vmcnt).
-__device__ __forceinline__ void lds_dma16(const char* base, uint32_t off, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" LV_DMA_NT ::"v"(off), "s"(base),
-               "s"(lds_base)
-               : "memory", "m0");
-}
-
-// As above, from a per-lane address.
-__device__ __forceinline__ void lds_dma16(const char* src, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" LV_DMA_NT ::"v"(src), "s"(lds_base)
-               : "memory", "m0");
-}
-
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(lds_void_t*)p;
-}
-
 // Wait until at most `ahead` (<= 6) stages of this wave's loads (5 per stage, 4 for wave 3) are outstanding, then meet
 // the other waves. No fence: the stage's LDS writes are exactly the loads waited for, and a fence would wait for
 // the stages still in flight as well.
@@ -463,15 +435,6 @@ __device__ __forceinline__ int unit_latents(const MlaParams& p, int u) {
   const int tq = u / p.htiles;  // row * lq + j
   const int row = tq / p.lq, qj = tq - row * p.lq;
   return p.lens[row] - p.lq + qj + 1;
-}
-
-// Load of a wave-uniform int through the scalar cache. For tables this kernel only reads: the compiler would use
-// a vector load here (the kernel's stores might alias), and its wait for that load would also wait for every
-// latent load in flight.
-__device__ __forceinline__ int sload(const int32_t* ptr) {
-  int v;
-  asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(ptr));
-  return v;
 }
 
 __device__ __forceinline__ int unit_latents_uniform(const MlaParams& p, int u) {
@@ -903,7 +866,9 @@ extern "C" int lv_mla_decode(const void* q, int64_t q_stride_t, int64_t q_stride
 
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const bool one_page = block_size % kDmaTile == 0 && p.c_st * kDmaTile < ((int64_t)1 << 31);
-  if (LV_MLA_RUNS && one_page && s.units <= kRunMaxUnits) {
+  // The run schedule counts stages in 32 bits on the device.
+  const int64_t stage_bound = (int64_t)s.units * (((int64_t)std::max(max_seqlen_k, 1) + kDmaTile - 1) / kDmaTile);
+  if (LV_MLA_RUNS && one_page && s.units <= kRunMaxUnits && stage_bound < ((int64_t)1 << 30)) {
     p.units = s.units;
     p.part_lse = reinterpret_cast<float*>(ws + s.lse_off);
     p.part_o = reinterpret_cast<float*>(ws + s.o_off);

@@ -26,6 +26,9 @@ constexpr int kPlanMaxRows = 4096;  // rows of a step with prompts (the work-lis
 #ifndef LV_DECODE_PIPE
 #define LV_DECODE_PIPE 2
 #endif
+#ifndef LV_PROMPT_RING
+#define LV_PROMPT_RING 2  // LDS stages of the prompt tiles' ring (0: register staging for every page size)
+#endif
 #ifndef LV_PROMPT_PREFETCH
 #define LV_PROMPT_PREFETCH true
 #endif
@@ -344,13 +347,14 @@ __global__ __launch_bounds__(256) void decode_list_kernel(AttnParams p) {
   decode_item<T, D, GS>(p, it.x, it.y, kvh, qg, smem);
 }
 
-template <typename T, int D>
+// RING > 0: pages are a multiple of 64 tokens, so prompt tiles stream through an LDS ring of RING stages.
+template <typename T, int D, int RING>
 __global__ __launch_bounds__(256, 2) void prompt_list_kernel(AttnParams p) {
-  __shared__ __attribute__((aligned(16))) char smem[PromptSmem<D, D>::kBytes];
+  __shared__ __attribute__((aligned(16))) char smem[(RING > 0 ? RING : 1) * PromptSmem<D, D>::kBytes];
   const int bx = blockIdx.x / p.hkv, kvh = blockIdx.x - bx * p.hkv;
   if (bx >= p.n_items[1]) return;
   const int2 it = p.items[bx];
-  prefill_item<T, D, D, LV_PROMPT_PREFETCH>(p, it.x, -1 - it.y, kvh, smem);
+  prefill_item<T, D, D, LV_PROMPT_PREFETCH, false, RING>(p, it.x, -1 - it.y, kvh, smem);
 }
 
 // Prompt items of a mixed step, run at the same time as its decode items: one workgroup per CU, each walking the
@@ -358,14 +362,14 @@ __global__ __launch_bounds__(256, 2) void prompt_list_kernel(AttnParams p) {
 // budgets registers for 2 waves per SIMD) leaves room for no second one, and the decode workgroups take the CU's
 // remaining registers: the MFMA work of the prompt tiles hides under the decode rows' memory streaming.
 constexpr int kOverlapLds = 84 * 1024;
-template <typename T, int D>
+template <typename T, int D, int RING>
 __global__ __launch_bounds__(256, 2) void prompt_overlap_kernel(AttnParams p) {
-  __shared__ __attribute__((aligned(16))) char smem[PromptSmem<D, D>::kBytes];
+  __shared__ __attribute__((aligned(16))) char smem[(RING > 0 ? RING : 1) * PromptSmem<D, D>::kBytes];
   const int n = p.n_items[1] * p.hkv;
   for (int f = blockIdx.x; f < n; f += gridDim.x) {
     const int bx = f / p.hkv, kvh = f - bx * p.hkv;
     const int2 it = p.items[bx];
-    prefill_item<T, D, D, LV_PROMPT_PREFETCH, true>(p, it.x, -1 - it.y, kvh, smem);
+    prefill_item<T, D, D, LV_PROMPT_PREFETCH, true, RING>(p, it.x, -1 - it.y, kvh, smem);
     __syncthreads();  // the next item restages the LDS tiles
   }
 }
@@ -562,11 +566,11 @@ static SideStream* side_stream() {
 template <typename T, int D, int GS>
 static void launch(const AttnParams& p, bool listed, bool mixed, const Shape& s, hipStream_t stream) {
   const int ny = p.hkv * p.qgroups;
+  const bool ring = LV_PROMPT_RING > 0 && p.bs.d % kPrefillKeys == 0;  // every 64-key tile in one page
   SideStream* side = LV_OVERLAP && listed && mixed ? side_stream() : nullptr;
   if (side) {
     // Decode items go to the second stream first, then the prompt items to the caller's stream: the prompt
     // workgroups (one per CU) are dispatched as soon as the plan ends, the decode workgroups fill the rest.
-    constexpr int pad = kOverlapLds - PromptSmem<D, D>::kBytes;
     const int grid = std::min(s.max_prompt_items * p.hkv, std::max(1, device_cus() * LV_OVERLAP_CUS / 100));
     std::lock_guard<std::mutex> g(side->lock);
     hipEventRecord(side->fork, stream);
@@ -574,10 +578,20 @@ static void launch(const AttnParams& p, bool listed, bool mixed, const Shape& s,
     hipLaunchKernelGGL((decode_list_kernel<T, D, GS>), dim3(s.max_decode_items * ny), dim3(256), 0, side->stream,
                        p);
     hipEventRecord(side->join, side->stream);
-    hipLaunchKernelGGL((prompt_overlap_kernel<T, D>), dim3(grid), dim3(256), pad, stream, p);
+    if (ring) {
+      constexpr int pad = std::max(0, kOverlapLds - LV_PROMPT_RING * PromptSmem<D, D>::kBytes);
+      hipLaunchKernelGGL((prompt_overlap_kernel<T, D, LV_PROMPT_RING>), dim3(grid), dim3(256), pad, stream, p);
+    } else {
+      constexpr int pad = kOverlapLds - PromptSmem<D, D>::kBytes;
+      hipLaunchKernelGGL((prompt_overlap_kernel<T, D, 0>), dim3(grid), dim3(256), pad, stream, p);
+    }
     hipStreamWaitEvent(stream, side->join, 0);
   } else if (listed && mixed) {
-    hipLaunchKernelGGL((prompt_list_kernel<T, D>), dim3(s.max_prompt_items * p.hkv), dim3(256), 0, stream, p);
+    if (ring)
+      hipLaunchKernelGGL((prompt_list_kernel<T, D, LV_PROMPT_RING>), dim3(s.max_prompt_items * p.hkv), dim3(256), 0,
+                         stream, p);
+    else
+      hipLaunchKernelGGL((prompt_list_kernel<T, D, 0>), dim3(s.max_prompt_items * p.hkv), dim3(256), 0, stream, p);
     hipLaunchKernelGGL((decode_list_kernel<T, D, GS>), dim3(s.max_decode_items * ny), dim3(256), 0, stream, p);
   } else if (listed) {
     hipLaunchKernelGGL((decode_list_kernel<T, D, GS>), dim3(s.max_decode_items * ny), dim3(256), 0, stream, p);

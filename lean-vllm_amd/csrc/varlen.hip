@@ -10,11 +10,24 @@
 
 namespace lv {
 
+#ifndef LV_VARLEN_RING
+#define LV_VARLEN_RING 2
+#endif
+
+// Keys are packed, so every 64-key tile is contiguous: tiles stream through an LDS ring. Two workgroups fit a CU
+// up to 128-wide q.k; wider tiles take one (and its registers).
+template <int DQK, int DV>
+struct VarlenCfg {
+  static constexpr int kRing = LV_VARLEN_RING;
+  static constexpr int kSmem = (kRing > 0 ? kRing : 1) * PromptSmem<DQK, DV>::kBytes;
+  static constexpr int kWaves = kSmem <= 80 * 1024 && DQK <= 128 ? 2 : 1;
+};
+
 template <typename T, int DQK, int DV>
-__global__ __launch_bounds__(256, DQK <= 128 ? 2 : 1) void varlen_kernel(AttnParams p, int32_t qtiles) {
-  __shared__ __attribute__((aligned(16))) char smem[PromptSmem<DQK, DV>::kBytes];
+__global__ __launch_bounds__(256, (VarlenCfg<DQK, DV>::kWaves)) void varlen_kernel(AttnParams p, int32_t qtiles) {
+  __shared__ __attribute__((aligned(16))) char smem[VarlenCfg<DQK, DV>::kSmem];
   const int row = blockIdx.x / qtiles, qt = blockIdx.x - row * qtiles;
-  prefill_item<T, DQK, DV>(p, row, qt, blockIdx.y, smem);
+  prefill_item<T, DQK, DV, true, false, VarlenCfg<DQK, DV>::kRing>(p, row, qt, blockIdx.y, smem);
 }
 
 template <typename T>

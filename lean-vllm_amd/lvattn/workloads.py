@@ -14,6 +14,9 @@ device. Key lengths include the token(s) stored this step (``context_lens = num_
 - ``qwen3_8b_long``: 32/8 heads, d128, bs 256, pool 10,000; 16 decode rows, context U[32768, 131072].
 - ``deepseek_v2_lite_mla``: 16 heads, latent 576 (512 + 64 rope), values 512, bs 64, pool 34,000; 128 decode
   rows, context U[1024, 16384]; values N(0, 0.5); scale 1/sqrt(192).
+- ``deepseek_v2_lite_mla_prefill``: the same layer's prompt chunks as ``MLAAttention._prefill`` runs them
+  (``lean_vllm/layers/attention.py:265-317``) on expanded heads (q.k 192, values 128): 4 chunks of 1536 new tokens
+  on a cached prefix U[0, 6144]; the new tokens attend each other causally, the prefix unmasked, merged by lse.
 """
 
 from __future__ import annotations
@@ -40,6 +43,7 @@ class Workload:
     value_std: float = 1.0
     latent_dim: int = 0  # MLA: cached latent width
     v_dim: int = 0  # MLA: value width (leading entries of a latent)
+    expanded: tuple = (0, 0)  # MLA prefill: (q.k width, value width) of the expanded heads
     notes: dict = field(default_factory=dict)
 
     @property
@@ -57,6 +61,10 @@ class Workload:
     @property
     def is_mla(self) -> bool:
         return self.latent_dim > 0
+
+    @property
+    def is_mla_prefill(self) -> bool:
+        return self.expanded[0] > 0
 
     def kv_bytes_per_token(self, elem_bytes: int = 2) -> int:
         """Cache bytes one attended key position costs: K and V of every kv head, or one MLA latent."""
@@ -124,12 +132,24 @@ def deepseek_v2_lite_mla(seed: int = 0) -> Workload:
                     _tables(rng, 34_000, ctx, 64), 1 / math.sqrt(192), value_std=0.5, latent_dim=576, v_dim=512)
 
 
+def deepseek_v2_lite_mla_prefill(seed: int = 0) -> Workload:
+    rng = np.random.default_rng(seed)
+    prefix = rng.integers(0, 6144 + 1, size=4)
+    num_cached = [int(p) for p in prefix]
+    num_new = [1536] * 4
+    ends = [c + n for c, n in zip(num_cached, num_new)]
+    return Workload("deepseek_v2_lite_mla_prefill", 16, 1, 576, 64, 1024, num_cached, num_new,
+                    _tables(rng, 1024, ends, 64), 1 / math.sqrt(192), value_std=0.5, latent_dim=576, v_dim=512,
+                    expanded=(192, 128))
+
+
 WORKLOADS = {
     "qwen3_0_6b_mixed": qwen3_0_6b_mixed,
     "qwen3_8b_decode": qwen3_8b_decode,
     "qwen3_8b_mixed": qwen3_8b_mixed,
     "qwen3_8b_long": qwen3_8b_long,
     "deepseek_v2_lite_mla": deepseek_v2_lite_mla,
+    "deepseek_v2_lite_mla_prefill": deepseek_v2_lite_mla_prefill,
 }
 
 
@@ -140,6 +160,7 @@ class Tensors:
     v_new: torch.Tensor | None
     k_cache: torch.Tensor  # [pool, bs, Hkv, D] (MLA: [pool, bs, latent])
     v_cache: torch.Tensor | None
+    expanded: dict | None = None  # MLA prefill: q, k, v of the new tokens and k, v of the cached prefix
 
 
 def _randn(shape, generator, device, dtype, std: float, chunk: int = 1 << 27):
@@ -159,6 +180,17 @@ def materialize(wl: Workload, device, dtype=torch.bfloat16, seed: int = 0) -> Te
     gen = torch.Generator(device=device)
     gen.manual_seed(seed)
     std = wl.value_std
+    if wl.is_mla_prefill:
+        dqk, dv = wl.expanded
+        lat = _randn((wl.tokens, wl.latent_dim), gen, device, dtype, std)
+        cache = _randn((wl.pool, wl.block_size, wl.latent_dim), gen, device, dtype, std)
+        prefix = int(sum(wl.num_cached))
+        ex = dict(q=_randn((wl.tokens, wl.num_heads, dqk), gen, device, dtype, 1.0),
+                  k=_randn((wl.tokens, wl.num_heads, dqk), gen, device, dtype, 1.0),
+                  v=_randn((wl.tokens, wl.num_heads, dv), gen, device, dtype, std),
+                  k_ctx=_randn((prefix, wl.num_heads, dqk), gen, device, dtype, 1.0),
+                  v_ctx=_randn((prefix, wl.num_heads, dv), gen, device, dtype, std))
+        return Tensors(ex["q"], lat, None, cache, None, ex)
     if wl.is_mla:
         q = _randn((wl.tokens, wl.num_heads, wl.latent_dim), gen, device, dtype, std)
         lat = _randn((wl.tokens, wl.latent_dim), gen, device, dtype, std)
@@ -181,7 +213,12 @@ def algorithmic_bytes(wl: Workload, elem_bytes: int = 2) -> dict:
     bytes, q and out, the store of this step's new K/V, and the pack kernel's inputs and outputs."""
     ctx = wl.context_lens
     kv = int(ctx.sum()) * wl.kv_bytes_per_token(elem_bytes)
-    if wl.is_mla:
+    if wl.is_mla_prefill:  # every expanded key and value once, q and out
+        dqk, dv = wl.expanded
+        kv = int(ctx.sum()) * wl.num_heads * (dqk + dv) * elem_bytes
+        qo = wl.tokens * wl.num_heads * (dqk + dv) * elem_bytes
+        store = 2 * wl.tokens * wl.latent_dim * elem_bytes
+    elif wl.is_mla:
         qo = wl.tokens * wl.num_heads * (wl.latent_dim + wl.v_dim) * elem_bytes
         store = 2 * wl.tokens * wl.latent_dim * elem_bytes
     else:
@@ -199,5 +236,8 @@ def algorithmic_flops(wl: Workload) -> int:
     for c, n in zip(wl.num_cached, wl.num_new):
         seen = n * c + n * (n + 1) // 2  # query j of the row sees c + j + 1 keys
         total += seen
-    d = (wl.latent_dim + wl.v_dim) // 2 if wl.is_mla else wl.head_dim
+    if wl.is_mla_prefill:
+        d = sum(wl.expanded) // 2
+    else:
+        d = (wl.latent_dim + wl.v_dim) // 2 if wl.is_mla else wl.head_dim
     return 4 * wl.num_heads * d * total

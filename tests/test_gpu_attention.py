@@ -40,6 +40,25 @@ def run_step(backend, dtype, dim, device, num_cached, num_new, tables, nblocks, 
     return out, dense_expected(qs, kf, vf, SCALE), (qs, kf, vf, kc, vc, ctx)
 
 
+@pytest.mark.parametrize("bs", [64, 256])
+def test_prefill_through_the_lds_ring(case, bs):
+    """Pages that hold whole 64-key tiles: prompt tiles stream through the LDS ring. Prefixes of several tiles,
+    tails that end mid-tile, a decode row beside the chunks, and NaN in every unused cache slot (a tile's keys
+    past the row's end must never bring one in)."""
+    b, dtype, dim, dev = case
+    cached, new = [3 * 64 + 5, 0, 70, bs - 1], [77, 130, 1, 9]
+    pages = [[6 * r + i for i in range(6)] for r in range(4)]  # scattered: row r's pages are 6r .. 6r + 5
+    width = max(-(-(c + n) // bs) for c, n in zip(cached, new))
+    tables = [pg[:-(-(c + n) // bs)] + [-1] * (width - -(-(c + n) // bs)) for pg, c, n in zip(pages, cached, new)]
+    qs, kf, vf, kn, vn, kc, vc, slots = paged_step(cached, new, tables, 24, heads=H, kv_heads=HKV, dim=dim, bs=bs,
+                                                   device=dev, dtype=dtype, fill=float("nan"))
+    b.store_kvcache(kn, vn, kc, vc, slots)
+    out = b.forward(torch.cat(qs), kn, vn, kc, vc, context_for(cached, new, tables, dev))
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    check(out, dense_expected(qs, kf, vf, SCALE), dtype)
+
+
 def test_prefill_of_a_cold_batch_with_pages(case):
     b, dtype, dim, dev = case
     out, want, _ = run_step(b, dtype, dim, dev, [0, 0], [5, BS + 3], [[0, 1, -1], [2, 3, 4]], 6)
