@@ -143,13 +143,15 @@ def test_merge_of_a_split_equals_the_whole(cuda):
     torch.testing.assert_close(lse_a, whole_lse, atol=1e-4, rtol=1e-4)
 
 
+@pytest.mark.parametrize("dim", [128, 192, 100], ids=["d128", "d192", "d100-scalar"])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("into", [False, True], ids=["in_place", "into_out"])
-def test_merge_matches_the_oracle(cuda, dtype, into):
+def test_merge_matches_the_oracle(cuda, dtype, into, dim):
     """In place or into an output strided as a split's rows, with lse in a transposed layout and a row whose lse
-    is -inf (no cached keys), as tests/test_attention_backends.py:266-287."""
+    is -inf (no cached keys), as tests/test_attention_backends.py:266-287. Widths that are multiples of 8 take
+    16-byte lanes (192: rows of 24 lanes, 10 to a workgroup); 100 takes the element-wise kernel."""
     gen = torch.Generator().manual_seed(6)
-    tokens, heads, dim = 37, 16, 128
+    tokens, heads = 37, 16
     o_a = rnd(tokens, heads, dim, gen=gen, dtype=dtype, device=cuda)
     o_b = rnd(tokens, heads, dim, gen=gen, dtype=dtype, device=cuda)
     lse_a = (torch.randn(heads, tokens, generator=gen) * 3).to(cuda).T
