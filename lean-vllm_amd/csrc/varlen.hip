@@ -1,7 +1,7 @@
 // Attention over packed (unpaged) keys: lean-vLLM's prefill without block tables and varlen_with_lse.
 //
 // Rows are given by cu_seqlens_q / cu_seqlens_k over packed q [T, Hq, DQK], k [Tk, Hkv, DQK], v [Tk, Hkv, DV].
-// Every row runs the MFMA prompt item of attn_common.h; the grid covers (row, tile of query positions, kv head)
+// Every row runs the MFMA prompt item of attn_common.h; the grid covers (kv head, row, tile of query positions)
 // for the longest row and items past a row's queries return at once, so no work list or workspace is needed.
 // Math: TorchAttention.prefill without tables and TorchAttention.varlen_with_lse
 // (lean_vllm/attention/torch_backend.py:62-91), bottom-right causal or unmasked, plus the natural log-sum-exp of
@@ -23,16 +23,25 @@ struct VarlenCfg {
   static constexpr int kWaves = kSmem <= 80 * 1024 && DQK <= 128 ? 2 : 1;
 };
 
+constexpr int kXcds = 8;  // workgroups are dealt round-robin over the XCDs by their linear index
+
+// Item w = (kv head, row, query tile), query tiles innermost. Workgroup b (on XCD b % 8) takes item
+// start(b % 8) + b / 8, so each XCD runs a contiguous range of items: the query tiles of one (row, kv head),
+// which read the same key and value tiles, share an L2 instead of fetching them once per XCD.
 template <typename T, int DQK, int DV>
 __global__ __launch_bounds__(256, (VarlenCfg<DQK, DV>::kWaves)) void varlen_kernel(AttnParams p, int32_t qtiles) {
   __shared__ __attribute__((aligned(16))) char smem[VarlenCfg<DQK, DV>::kSmem];
-  const int row = blockIdx.x / qtiles, qt = blockIdx.x - row * qtiles;
-  prefill_item<T, DQK, DV, true, false, VarlenCfg<DQK, DV>::kRing>(p, row, qt, blockIdx.y, smem);
+  const int n = gridDim.x, b = blockIdx.x, x = b % kXcds;
+  const int w = x * (n / kXcds) + min(x, n % kXcds) + b / kXcds;
+  const int per_head = p.rows * qtiles;
+  const int kvh = w / per_head, rest = w - kvh * per_head;
+  const int row = rest / qtiles, qt = rest - row * qtiles;
+  prefill_item<T, DQK, DV, true, false, VarlenCfg<DQK, DV>::kRing>(p, row, qt, kvh, smem);
 }
 
 template <typename T>
 static int launch_varlen(const AttnParams& p, int dqk, int dv, int qtiles, hipStream_t st) {
-  const dim3 grid(p.rows * qtiles, p.hkv);
+  const dim3 grid(p.rows * qtiles * p.hkv);
   if (dqk == 64 && dv == 64)
     hipLaunchKernelGGL((varlen_kernel<T, 64, 64>), grid, dim3(256), 0, st, p, qtiles);
   else if (dqk == 128 && dv == 128)
@@ -105,7 +114,7 @@ extern "C" int lv_varlen_attention(const void* q, int64_t q_stride_t, int64_t q_
   p.lse_sh = lse_stride_h;
   const int qp = kPrefillRows / p.group;
   const int64_t qtiles = (max_seqlen_q + qp - 1) / qp;
-  LV_REQUIRE(qtiles * num_rows < ((int64_t)1 << 31) && num_kv_heads < 65536, "varlen_attention: grid too large");
+  LV_REQUIRE(qtiles * num_rows * num_kv_heads < ((int64_t)1 << 31), "varlen_attention: grid too large");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   return dtype == LV_DTYPE_BF16 ? launch_varlen<BF16>(p, head_dim_qk, head_dim_v, (int)qtiles, st)
                                 : launch_varlen<F16>(p, head_dim_qk, head_dim_v, (int)qtiles, st);
