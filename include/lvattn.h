@@ -25,7 +25,11 @@ extern "C" {
 #define LV_DTYPE_BF16 0
 #define LV_DTYPE_F16 1
 
-#define LV_ABI_VERSION 3
+#define LV_SCHEDULE_AUTO 0
+#define LV_SCHEDULE_SERIAL 1
+#define LV_SCHEDULE_OVERLAP 2
+
+#define LV_ABI_VERSION 4
 
 /* The last error message of the calling thread ("" if none). */
 const char* lv_last_error(void);
@@ -98,7 +102,12 @@ int lv_store_latents(const void* latent, int64_t latent_stride_t, int32_t num_to
  * max_seqlen_k bounds every row's key length (block-table width * block_size will do); it sizes the split-K grid
  * so a captured graph needs no length read back. num_tokens is T (it sizes the work list).
  * workspace: caller-owned device memory of at least lv_paged_attention_workspace_bytes(...) bytes for the same
- * arguments; its contents need no initialisation. */
+ * arguments; its contents need no initialisation.
+ * schedule (a step with prompt rows): LV_SCHEDULE_OVERLAP runs the prompt tiles on part of the CUs beside the
+ * decode rows' streaming (a second stream, joined back into `stream` by events); LV_SCHEDULE_SERIAL runs the
+ * prompt tiles on the whole GPU, then the decode rows -- the faster choice when the decode rows' bytes take less
+ * time than the prompt tiles' MFMA work (e.g. a step of prompts only). LV_SCHEDULE_AUTO overlaps. The result is
+ * the same either way. */
 size_t lv_paged_attention_workspace_bytes(int32_t num_rows, int32_t num_tokens, int32_t num_heads,
                                           int32_t num_kv_heads, int32_t head_dim, int32_t max_seqlen_k,
                                           int32_t decode_only);
@@ -109,7 +118,7 @@ int lv_paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h, co
                        const int32_t* cu_seqlens_k, int32_t num_rows, int32_t num_tokens, int32_t num_heads,
                        int32_t num_kv_heads, int32_t head_dim, float scale, int32_t max_seqlen_q,
                        int32_t max_seqlen_k, void* out, int64_t out_stride_t, int64_t out_stride_h,
-                       void* workspace, size_t workspace_bytes, int32_t dtype, void* stream);
+                       void* workspace, size_t workspace_bytes, int32_t schedule, int32_t dtype, void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------
  * Attention over packed keys (no pages). Replaces AttentionBackend.prefill without block tables and

@@ -34,7 +34,8 @@ struct AttnParams {
   float* part_o;    // [rows][hq][max_splits][D] normalised partial outputs
   float* part_lse;  // [rows][hq][max_splits] log2-sum-exp2 of the partials
   const int2* items;
-  const int32_t* n_items;
+  const int32_t* n_items;  // [0]: list length, [1]: prompt items at its head
+  int32_t* ticket;         // next decode item of a persistent launch (zeroed by the plan kernel)
 };
 
 __device__ inline int key_len(const AttnParams& p, int row) {

@@ -38,6 +38,12 @@ constexpr int kPlanMaxRows = 4096;  // rows of a step with prompts (the work-lis
 #ifndef LV_OVERLAP_CUS
 #define LV_OVERLAP_CUS 75  // percent of the CUs that hold a prompt workgroup in a mixed step (swept: 60-100)
 #endif
+#ifndef LV_DECODE_WGS
+#define LV_DECODE_WGS 0  // persistent decode workgroups per CU outside the overlap (0: one workgroup per item)
+#endif
+#ifndef LV_OVERLAP_DECODE_WGS
+#define LV_OVERLAP_DECODE_WGS 2  // persistent decode workgroups per CU beside a mixed step's prompt workgroups
+#endif
 #ifndef LV_SPLIT_TARGET
 #define LV_SPLIT_TARGET 4096
 #endif
@@ -68,8 +74,11 @@ __device__ inline float groups_sum(float x) {
   return xor32_sum(xor16_sum(x));
 }
 
+// publish (persistent launches): thread 0 stores publish_value there before the item's merge barrier, and the
+// barrier is met even by an item with nothing to do, so the whole workgroup reads the value after the call.
 template <typename T, int D, int GS>
-__device__ void decode_item(const AttnParams& p, int row, int split, int kvh, int qg, char* smem) {
+__device__ void decode_item(const AttnParams& p, int row, int split, int kvh, int qg, char* smem,
+                            int* publish = nullptr, int publish_value = 0) {
   using E = Elem<T>;
   static_assert(D == 64 || D == 128, "head_dim 64 or 128");
   constexpr int LPT = D / 8;      // lanes per token head row, 16 bytes each
@@ -83,8 +92,9 @@ __device__ void decode_item(const AttnParams& p, int row, int split, int kvh, in
   const int lk = key_len(p, row);
   const int kbeg = split * p.split;
   // Past the row's end (the grid is sized for the longest row), or past the bound the caller gave.
-  if ((split > 0 && kbeg >= lk) || split >= p.max_splits) return;
-  const int kend = min(lk, kbeg + p.split);
+  const bool valid = !((split > 0 && kbeg >= lk) || split >= p.max_splits);
+  if (!valid && !publish) return;
+  const int kend = valid ? min(lk, kbeg + p.split) : kbeg;
   const int nsplit = min((lk + p.split - 1) / p.split, p.max_splits);
   const int tok = p.cu_q ? p.cu_q[row] : row;
   const int head0 = kvh * p.group + qg * GS;
@@ -109,9 +119,17 @@ __device__ void decode_item(const AttnParams& p, int row, int split, int kvh, in
   for (int u = 0; u < U; ++u) loff[u] = (uint32_t)((u * TPI + grp) * p.c_st + part * 16);
   const int32_t* table = p.tables + (int64_t)row * p.t_stride;
 
+  // Page numbers come through the scalar cache, once per page this wave enters: a vector load of the table would
+  // be waited for in order with the K/V loads already in flight.
+  int cached_pg = -1;
+  int64_t cached_base = 0;
   auto tile_base = [&](int t0) {
     const int pg = (int)p.bs.div(t0);
-    return (int64_t)table[pg] * p.c_sb + (int64_t)(t0 - pg * (int)p.bs.d) * p.c_st + (int64_t)kvh * p.c_sh;
+    if (pg != cached_pg) {
+      cached_pg = pg;
+      cached_base = (int64_t)sload(table + pg) * p.c_sb + (int64_t)kvh * p.c_sh;
+    }
+    return cached_base + (int64_t)(t0 - pg * (int)p.bs.d) * p.c_st;
   };
   auto load_rows = [&](const char* cache, int64_t base, u32x4 (&x)[U]) {
     const char* b = cache + base;
@@ -286,7 +304,9 @@ __device__ void decode_item(const AttnParams& p, int row, int split, int kvh, in
       }
     }
   }
+  if (publish && threadIdx.x == 0) *publish = publish_value;
   __syncthreads();
+  if (!valid) return;
   // One thread per 8 output elements.
   for (int c = threadIdx.x; c < GS * D / 8; c += blockDim.x) {
     const int g = c / (D / 8), d0 = (c % (D / 8)) * 8;
@@ -345,6 +365,31 @@ __global__ __launch_bounds__(256) void decode_list_kernel(AttnParams p) {
   if (i >= p.n_items[0]) return;
   const int2 it = p.items[i];
   decode_item<T, D, GS>(p, it.x, it.y, kvh, qg, smem);
+}
+
+// Decode items of the work list on a persistent grid: each workgroup takes items by ticket (an atomic counter the
+// plan kernel zeroes), in list order, so the longest still go first. A fixed number of workgroups per CU lets a
+// mixed step's prompt workgroups stay resident beside them. The next ticket is drawn at the start of an item and
+// published at its merge barrier; the merge alternates between two LDS buffers, so one barrier per item suffices.
+template <typename T, int D, int GS>
+__global__ __launch_bounds__(256, 4) void decode_persistent_kernel(AttnParams p) {
+  __shared__ __attribute__((aligned(16))) char smem[2][SmemBytes<D, GS>::kDecode];
+  __shared__ int s_ticket[2];
+  const int ny = p.hkv * p.qgroups;
+  const int first = p.n_items[1];
+  const int total = (p.n_items[0] - first) * ny;
+  if (threadIdx.x == 0) s_ticket[0] = atomicAdd(p.ticket, 1);
+  __syncthreads();
+  int f = __builtin_amdgcn_readfirstlane(s_ticket[0]);
+  for (int k = 0; f < total; ++k) {
+    int next = 0;
+    if (threadIdx.x == 0) next = atomicAdd(p.ticket, 1);
+    const int bx = f / ny, by = f - bx * ny;
+    const int kvh = by / p.qgroups, qg = by - kvh * p.qgroups;
+    const int2 it = p.items[first + bx];
+    decode_item<T, D, GS>(p, it.x, it.y, kvh, qg, smem[k & 1], &s_ticket[(k + 1) & 1], next);
+    f = __builtin_amdgcn_readfirstlane(s_ticket[(k + 1) & 1]);
+  }
 }
 
 // RING > 0: pages are a multiple of 64 tokens, so prompt tiles stream through an LDS ring of RING stages.
@@ -446,6 +491,7 @@ __global__ __launch_bounds__(kScanThreads) void plan_kernel(const int32_t* __res
   if (tid == 0) {
     n_items[0] = min(npre + nfull + npart, max_items);
     n_items[1] = min(npre, max_items);
+    n_items[2] = 0;  // the persistent decode launch's ticket counter
   }
 }
 
@@ -563,11 +609,40 @@ static SideStream* side_stream() {
   return &s;
 }
 
+// Workgroups of `kernel` (256 threads) that one CU holds at once, from its register and LDS needs (cached).
+template <typename K>
+static int resident_per_cu(K kernel) {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cached[dev] > 0) return cached[dev];
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, 256, 0) != hipSuccess || n <= 0) n = 1;
+  cached[dev] = n;
+  return n;
+}
+
+// The decode items of a listed launch: one workgroup per item (per_cu 0), or a persistent grid of at most per_cu
+// workgroups per CU taking items by ticket -- beside a mixed step's prompt workgroups, where a fixed share of
+// every CU keeps both kernels resident at once.
 template <typename T, int D, int GS>
-static void launch(const AttnParams& p, bool listed, bool mixed, const Shape& s, hipStream_t stream) {
+static void launch_decode(const AttnParams& p, const Shape& s, int per_cu, hipStream_t stream) {
+  const int items = s.max_decode_items * p.hkv * p.qgroups;
+  if (per_cu > 0) {
+    const int fit = resident_per_cu(decode_persistent_kernel<T, D, GS>);
+    const int grid = std::max(1, std::min(items, std::min(per_cu, fit) * device_cus()));
+    hipLaunchKernelGGL((decode_persistent_kernel<T, D, GS>), dim3(grid), dim3(256), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL((decode_list_kernel<T, D, GS>), dim3(items), dim3(256), 0, stream, p);
+  }
+}
+
+template <typename T, int D, int GS>
+static void launch(const AttnParams& p, bool listed, bool mixed, bool overlap, const Shape& s,
+                   hipStream_t stream) {
   const int ny = p.hkv * p.qgroups;
   const bool ring = LV_PROMPT_RING > 0 && p.bs.d % kPrefillKeys == 0;  // every 64-key tile in one page
-  SideStream* side = LV_OVERLAP && listed && mixed ? side_stream() : nullptr;
+  SideStream* side = LV_OVERLAP && overlap && listed && mixed ? side_stream() : nullptr;
   if (side) {
     // Decode items go to the second stream first, then the prompt items to the caller's stream: the prompt
     // workgroups (one per CU) are dispatched as soon as the plan ends, the decode workgroups fill the rest.
@@ -575,8 +650,7 @@ static void launch(const AttnParams& p, bool listed, bool mixed, const Shape& s,
     std::lock_guard<std::mutex> g(side->lock);
     hipEventRecord(side->fork, stream);
     hipStreamWaitEvent(side->stream, side->fork, 0);
-    hipLaunchKernelGGL((decode_list_kernel<T, D, GS>), dim3(s.max_decode_items * ny), dim3(256), 0, side->stream,
-                       p);
+    launch_decode<T, D, GS>(p, s, LV_OVERLAP_DECODE_WGS, side->stream);
     hipEventRecord(side->join, side->stream);
     if (ring) {
       constexpr int pad = std::max(0, kOverlapLds - LV_PROMPT_RING * PromptSmem<D, D>::kBytes);
@@ -592,9 +666,9 @@ static void launch(const AttnParams& p, bool listed, bool mixed, const Shape& s,
                          stream, p);
     else
       hipLaunchKernelGGL((prompt_list_kernel<T, D, 0>), dim3(s.max_prompt_items * p.hkv), dim3(256), 0, stream, p);
-    hipLaunchKernelGGL((decode_list_kernel<T, D, GS>), dim3(s.max_decode_items * ny), dim3(256), 0, stream, p);
+    launch_decode<T, D, GS>(p, s, LV_DECODE_WGS, stream);
   } else if (listed) {
-    hipLaunchKernelGGL((decode_list_kernel<T, D, GS>), dim3(s.max_decode_items * ny), dim3(256), 0, stream, p);
+    launch_decode<T, D, GS>(p, s, LV_DECODE_WGS, stream);
   } else {
     hipLaunchKernelGGL((decode_grid_kernel<T, D, GS>), dim3(p.rows * p.max_splits, ny), dim3(256), 0, stream, p);
   }
@@ -603,18 +677,19 @@ static void launch(const AttnParams& p, bool listed, bool mixed, const Shape& s,
 }
 
 template <typename T, int D>
-static void launch_gs(const AttnParams& p, int gs, bool listed, bool mixed, const Shape& s, hipStream_t stream) {
-  if (gs == 4) launch<T, D, 4>(p, listed, mixed, s, stream);
-  else if (gs == 2) launch<T, D, 2>(p, listed, mixed, s, stream);
-  else launch<T, D, 1>(p, listed, mixed, s, stream);
+static void launch_gs(const AttnParams& p, int gs, bool listed, bool mixed, bool overlap, const Shape& s,
+                      hipStream_t stream) {
+  if (gs == 4) launch<T, D, 4>(p, listed, mixed, overlap, s, stream);
+  else if (gs == 2) launch<T, D, 2>(p, listed, mixed, overlap, s, stream);
+  else launch<T, D, 1>(p, listed, mixed, overlap, s, stream);
 }
 
 template <typename T>
-static int launch_d(const AttnParams& p, int d, int gs, bool listed, bool mixed, const Shape& s,
+static int launch_d(const AttnParams& p, int d, int gs, bool listed, bool mixed, bool overlap, const Shape& s,
                     hipStream_t stream) {
   switch (d) {
-    case 64: launch_gs<T, 64>(p, gs, listed, mixed, s, stream); return LV_OK;
-    case 128: launch_gs<T, 128>(p, gs, listed, mixed, s, stream); return LV_OK;
+    case 64: launch_gs<T, 64>(p, gs, listed, mixed, overlap, s, stream); return LV_OK;
+    case 128: launch_gs<T, 128>(p, gs, listed, mixed, overlap, s, stream); return LV_OK;
     default: set_error("paged_attention: head_dim %d is not 64 or 128", d); return LV_EINVAL;
   }
 }
@@ -639,11 +714,13 @@ extern "C" int lv_paged_attention(const void* q, int64_t q_stride_t, int64_t q_s
                                   const int32_t* cu_seqlens_k, int32_t num_rows, int32_t num_tokens,
                                   int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float scale,
                                   int32_t max_seqlen_q, int32_t max_seqlen_k, void* out, int64_t out_stride_t,
-                                  int64_t out_stride_h, void* workspace, size_t workspace_bytes, int32_t dtype,
-                                  void* stream) {
+                                  int64_t out_stride_h, void* workspace, size_t workspace_bytes, int32_t schedule,
+                                  int32_t dtype, void* stream) {
   LV_REQUIRE(dtype == LV_DTYPE_BF16 || dtype == LV_DTYPE_F16, "paged_attention: dtype %d is not bf16 or fp16",
              dtype);
   LV_REQUIRE(num_rows >= 0 && num_tokens >= 0, "paged_attention: negative row or token count");
+  LV_REQUIRE(schedule == LV_SCHEDULE_AUTO || schedule == LV_SCHEDULE_SERIAL || schedule == LV_SCHEDULE_OVERLAP,
+             "paged_attention: unknown schedule %d", schedule);
   if (num_rows == 0 || num_tokens == 0) return LV_OK;
   LV_REQUIRE(num_heads > 0 && num_kv_heads > 0 && num_heads % num_kv_heads == 0,
              "paged_attention: %d query heads do not group over %d key heads", num_heads, num_kv_heads);
@@ -711,6 +788,7 @@ extern "C" int lv_paged_attention(const void* q, int64_t q_stride_t, int64_t q_s
   p.part_o = s.max_splits > 1 ? reinterpret_cast<float*>(ws + s.o_off) : nullptr;
   p.items = listed ? reinterpret_cast<const int2*>(ws + s.items_off) : nullptr;
   p.n_items = listed ? reinterpret_cast<const int32_t*>(ws + s.count_off) : nullptr;
+  p.ticket = listed ? reinterpret_cast<int32_t*>(ws + s.count_off) + 2 : nullptr;
 
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (listed) {
@@ -720,8 +798,9 @@ extern "C" int lv_paged_attention(const void* q, int64_t q_stride_t, int64_t q_s
                        reinterpret_cast<int32_t*>(ws + s.count_off));
     LV_LAUNCH_CHECK("plan_kernel");
   }
-  const int rc = dtype == LV_DTYPE_BF16 ? launch_d<BF16>(p, head_dim, s.gs, listed, mixed, s, st)
-                                        : launch_d<F16>(p, head_dim, s.gs, listed, mixed, s, st);
+  const bool overlap = schedule != LV_SCHEDULE_SERIAL;
+  const int rc = dtype == LV_DTYPE_BF16 ? launch_d<BF16>(p, head_dim, s.gs, listed, mixed, overlap, s, st)
+                                        : launch_d<F16>(p, head_dim, s.gs, listed, mixed, overlap, s, st);
   if (rc != LV_OK) return rc;
   LV_LAUNCH_CHECK("paged_attention_kernel");
   return LV_OK;

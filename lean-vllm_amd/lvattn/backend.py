@@ -13,6 +13,7 @@ allowed by the contract:
 
 from __future__ import annotations
 
+import numpy as np
 import torch
 
 from . import _capi
@@ -53,6 +54,13 @@ class _Workspace:
 
 
 _WORKSPACE = _Workspace()
+
+# Launch schedules of a step with prompt rows (LV_SCHEDULE_* of lvattn.h).
+SCHEDULE_AUTO, SCHEDULE_SERIAL, SCHEDULE_OVERLAP = 0, 1, 2
+# Measured MI355X rates the schedule choice compares: decode rows stream their KV bytes at about 6.3 TB/s; prompt
+# tiles on the whole GPU run about 0.56 PFLOP/s (bf16, head_dim 128).
+DECODE_BYTES_PER_S = 6.3e12
+PROMPT_FLOPS_PER_S = 5.6e14
 
 
 class MI355XAttention(AttentionBackend):
@@ -129,7 +137,7 @@ class MI355XAttention(AttentionBackend):
 
     # -- attention -----------------------------------------------------------------------------------------
     def _attend(self, q, k_cache, v_cache, out, *, block_tables, cu_seqlens_q, seqlens_k, cu_seqlens_k, rows,
-                max_seqlen_q, max_seqlen_k):
+                max_seqlen_q, max_seqlen_k, schedule=SCHEDULE_AUTO):
         assert q.dtype in _capi.DTYPES and k_cache.dtype == q.dtype == v_cache.dtype
         assert q.stride(-1) == 1 and k_cache.stride() == v_cache.stride() and k_cache.stride(-1) == 1
         assert block_tables is not None and block_tables.dtype == torch.int32 and block_tables.stride(-1) == 1
@@ -146,9 +154,30 @@ class MI355XAttention(AttentionBackend):
                    v_cache.data_ptr(), sb, st, sh, k_cache.size(1), block_tables.data_ptr(), block_tables.stride(0),
                    _capi.ptr(cu_seqlens_q), _capi.ptr(seqlens_k), _capi.ptr(cu_seqlens_k), rows, tokens, heads,
                    self.num_kv_heads, dim, float(self.scale), max_seqlen_q, max_seqlen_k, out.data_ptr(),
-                   out.stride(0), out.stride(1), _capi.ptr(ws), 0 if ws is None else ws.numel(),
+                   out.stride(0), out.stride(1), _capi.ptr(ws), 0 if ws is None else ws.numel(), schedule,
                    _capi.DTYPES[q.dtype], _capi.stream_of(q.device))
         return out
+
+    def _schedule(self, context: Context, elem_bytes: int) -> int:
+        """Overlap a step's prompt tiles with its decode rows only when the decode rows' bytes take at least as
+        long as the prompt tiles' MFMA work; otherwise (a step of prompts, or prompts with a few short decode rows)
+        the prompt tiles run on the whole GPU first. Decided from the host lengths the context carries
+        (``cu_seqlens_*_host``); without them the library's default (overlap) stands."""
+        cu_q, cu_k = context.cu_seqlens_q_host, context.cu_seqlens_k_host
+        if cu_q is None or cu_k is None:
+            return SCHEDULE_AUTO
+        key = ("schedule", self.num_heads, self.num_kv_heads, self.head_dim, elem_bytes)
+        cache = context.attn_metadata if context.attn_metadata is not None else {}
+        context.attn_metadata = cache  # per-step plans shared by every layer
+        if key not in cache:
+            lq = np.diff(np.asarray(cu_q, dtype=np.int64))
+            lk = np.diff(np.asarray(cu_k, dtype=np.int64))
+            decode_bytes = float(lk[lq == 1].sum()) * 2 * self.num_kv_heads * self.head_dim * elem_bytes
+            pq, pk = lq[lq > 1], lk[lq > 1]  # query j of a prompt row sees lk - lq + j + 1 keys
+            prompt_flops = 4.0 * self.num_heads * self.head_dim * float((pq * (pk - pq) + pq * (pq + 1) // 2).sum())
+            overlap = decode_bytes / DECODE_BYTES_PER_S >= prompt_flops / PROMPT_FLOPS_PER_S
+            cache[key] = SCHEDULE_OVERLAP if overlap else SCHEDULE_SERIAL
+        return cache[key]
 
     def decode(self, q, k_cache, v_cache, context: Context, out=None):
         """One query per row against its ``context_lens[b]`` cached keys; q ``[B, Hq, D]``."""
@@ -174,7 +203,8 @@ class MI355XAttention(AttentionBackend):
         max_q = context.max_seqlen_q or q.size(0)
         return self._attend(q, k_cache, v_cache, out, block_tables=bt, cu_seqlens_q=cu_q.to(torch.int32),
                             seqlens_k=None, cu_seqlens_k=cu_k.to(torch.int32), rows=cu_q.numel() - 1,
-                            max_seqlen_q=max_q, max_seqlen_k=max_k)
+                            max_seqlen_q=max_q, max_seqlen_k=max_k,
+                            schedule=self._schedule(context, q.element_size()))
 
     def mla_decode(self, q, latent_cache, v_dim, context: Context, out=None):
         """Each row's last ``Lq`` queries against its paged latents, read as one key head shared by every query

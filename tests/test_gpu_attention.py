@@ -79,6 +79,35 @@ def test_mixed_batch_of_chunks_and_decodes(case):
     check(out, want, dtype)
 
 
+@pytest.mark.parametrize("bs", [16, 64])
+def test_both_launch_schedules_give_the_same_step(case, bs, monkeypatch):
+    """A mixed step (chunks on cached prefixes, decode rows, a cold prompt) under the serial schedule (prompt
+    tiles on the whole GPU, then the decode rows) and the overlapped one (prompt tiles beside the decode rows):
+    both match the oracle and each other bit for bit, since every item runs the same code either way."""
+    from lvattn import backend as B
+
+    b, dtype, dim, dev = case
+    cached, new = [2 * bs + 5, 0, 3 * bs, bs - 1, 7], [9, 70, 1, 1, 1]
+    width = max(-(-(c + n) // bs) for c, n in zip(cached, new))
+    tables, at = [], 0
+    for c, n in zip(cached, new):
+        k = -(-(c + n) // bs)
+        tables.append(list(range(at, at + k)) + [-1] * (width - k))
+        at += k
+    qs, kf, vf, kn, vn, kc, vc, slots = paged_step(cached, new, tables, at, heads=H, kv_heads=HKV, dim=dim, bs=bs,
+                                                   device=dev, dtype=dtype)
+    b.store_kvcache(kn, vn, kc, vc, slots)
+    want = dense_expected(qs, kf, vf, SCALE)
+    outs = {}
+    for sched in (B.SCHEDULE_SERIAL, B.SCHEDULE_OVERLAP):
+        monkeypatch.setattr(b, "_schedule", lambda context, elem_bytes, s=sched: s)
+        out = b.forward(torch.cat(qs), kn, vn, kc, vc, context_for(cached, new, tables, dev))
+        torch.cuda.synchronize()
+        check(out, want, dtype)
+        outs[sched] = out
+    assert torch.equal(outs[B.SCHEDULE_SERIAL], outs[B.SCHEDULE_OVERLAP])
+
+
 def test_decode(case):
     b, dtype, dim, dev = case
     lens = [BS + 3, 3, 4 * BS]

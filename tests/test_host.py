@@ -81,3 +81,25 @@ def test_selection_rules(monkeypatch):
     monkeypatch.setenv("LEAN_VLLM_ATTENTION_BACKEND", "mi355x")
     with pytest.raises(RuntimeError, match="dtype torch.float32"):
         get_attention_backend(LayerSpec(128, 32, 8, torch.float32))
+
+
+def test_prompt_tiles_overlap_decode_rows_only_when_the_decode_bytes_cover_them():
+    """The launch schedule of a step with prompts, from the context's host lengths, cached for every layer."""
+    from lvattn import backend as B
+    from lvattn import workloads as W
+
+    attn = MI355XAttention(32, 128, 128 ** -0.5, 8)
+    mixed = W.qwen3_8b_mixed(0)
+    order = W.batch_order(mixed)
+    new = [mixed.num_new[i] for i in order]
+    ends = [mixed.num_cached[i] + mixed.num_new[i] for i in order]
+    cu_q = [0, *torch.tensor(new).cumsum(0).tolist()]
+    cu_k = [0, *torch.tensor(ends).cumsum(0).tolist()]
+    ctx = Context(cu_seqlens_q_host=cu_q, cu_seqlens_k_host=cu_k)
+    assert attn._schedule(ctx, 2) == B.SCHEDULE_OVERLAP  # 18.7 GB of decode rows hide 387 GFLOP of prompt tiles
+    assert ctx.attn_metadata  # cached on the step's context
+    prompts = Context(cu_seqlens_q_host=[0, 1536, 3072], cu_seqlens_k_host=[0, 2000, 5000])
+    assert attn._schedule(prompts, 2) == B.SCHEDULE_SERIAL  # no decode rows: the prompt tiles take the whole GPU
+    few = Context(cu_seqlens_q_host=[0, 1, 2, 1538], cu_seqlens_k_host=[0, 300, 600, 4000])
+    assert attn._schedule(few, 2) == B.SCHEDULE_SERIAL
+    assert attn._schedule(Context(), 2) == B.SCHEDULE_AUTO  # no host lengths: the library default
