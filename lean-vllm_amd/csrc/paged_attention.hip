@@ -36,10 +36,10 @@ constexpr int kPlanMaxRows = 4096;  // rows of a step with prompts (the work-lis
 #define LV_OVERLAP 1
 #endif
 #ifndef LV_OVERLAP_CUS
-#define LV_OVERLAP_CUS 75  // percent of the CUs that hold a prompt workgroup in a mixed step (swept: 60-100)
+#define LV_OVERLAP_CUS 50  // percent of the CUs that hold a prompt workgroup in a mixed step (swept: 50-100)
 #endif
 #ifndef LV_DECODE_WGS
-#define LV_DECODE_WGS 0  // persistent decode workgroups per CU outside the overlap (0: one workgroup per item)
+#define LV_DECODE_WGS 2  // persistent decode workgroups per CU outside the overlap (0: one workgroup per item)
 #endif
 #ifndef LV_OVERLAP_DECODE_WGS
 #define LV_OVERLAP_DECODE_WGS 2  // persistent decode workgroups per CU beside a mixed step's prompt workgroups
