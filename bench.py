@@ -246,9 +246,9 @@ def attention_op(wl) -> str:
     if wl.is_mla:
         return "lv_mla_decode (mla_run_kernel + mla_run_merge_kernel)"
     if any(n > 1 for n in wl.num_new):
-        return ("lv_paged_attention (plan_kernel + decode_list_kernel on a second stream beside "
+        return ("lv_paged_attention (plan_kernel + decode_persistent_kernel on a second stream beside "
                 "prompt_overlap_kernel + splitk_merge_kernel)")
-    return "lv_paged_attention (plan_kernel + decode_list_kernel + splitk_merge_kernel)"
+    return "lv_paged_attention (plan_kernel + decode_persistent_kernel + splitk_merge_kernel)"
 
 
 def traffic_of(name: str):

@@ -622,15 +622,16 @@ static int resident_per_cu(K kernel) {
   return n;
 }
 
-// The decode items of a listed launch: one workgroup per item (per_cu 0), or a persistent grid of at most per_cu
-// workgroups per CU taking items by ticket -- beside a mixed step's prompt workgroups, where a fixed share of
-// every CU keeps both kernels resident at once.
+// The decode items of a listed launch: a persistent grid of at most per_cu workgroups per CU taking items by
+// ticket (beside a mixed step's prompt workgroups a fixed share of every CU keeps both kernels resident), or one
+// workgroup per item -- for per_cu 0, and for steps whose item bound is under eight items per persistent
+// workgroup, whose few short items finish sooner all at once than in rounds.
 template <typename T, int D, int GS>
 static void launch_decode(const AttnParams& p, const Shape& s, int per_cu, hipStream_t stream) {
-  const int items = s.max_decode_items * p.hkv * p.qgroups;
-  if (per_cu > 0) {
-    const int fit = resident_per_cu(decode_persistent_kernel<T, D, GS>);
-    const int grid = std::max(1, std::min(items, std::min(per_cu, fit) * device_cus()));
+  const int items = s.max_decode_items * p.hkv * p.qgroups;  // a bound: the plan lists no more
+  const int grid = per_cu > 0 ? std::min(per_cu, resident_per_cu(decode_persistent_kernel<T, D, GS>)) * device_cus()
+                              : 0;
+  if (grid > 0 && items >= 8 * grid) {
     hipLaunchKernelGGL((decode_persistent_kernel<T, D, GS>), dim3(grid), dim3(256), 0, stream, p);
   } else {
     hipLaunchKernelGGL((decode_list_kernel<T, D, GS>), dim3(items), dim3(256), 0, stream, p);

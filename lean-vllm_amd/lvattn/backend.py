@@ -13,7 +13,6 @@ allowed by the contract:
 
 from __future__ import annotations
 
-import numpy as np
 import torch
 
 from . import _capi
@@ -170,11 +169,25 @@ class MI355XAttention(AttentionBackend):
         cache = context.attn_metadata if context.attn_metadata is not None else {}
         context.attn_metadata = cache  # per-step plans shared by every layer
         if key not in cache:
-            lq = np.diff(np.asarray(cu_q, dtype=np.int64))
-            lk = np.diff(np.asarray(cu_k, dtype=np.int64))
-            decode_bytes = float(lk[lq == 1].sum()) * 2 * self.num_kv_heads * self.head_dim * elem_bytes
-            pq, pk = lq[lq > 1], lk[lq > 1]  # query j of a prompt row sees lk - lq + j + 1 keys
-            prompt_flops = 4.0 * self.num_heads * self.head_dim * float((pq * (pk - pq) + pq * (pq + 1) // 2).sum())
+            # Rows come decode-first (prepare_batch's order): the leading one-query rows are those with
+            # cu_q[i] == i, found by bisection, and their keys sum to cu_k[n]. The rest are walked one by one.
+            rows = len(cu_q) - 1
+            lo, hi = 0, rows
+            while lo < hi:
+                mid = (lo + hi + 1) // 2
+                if cu_q[mid] == mid:
+                    lo = mid
+                else:
+                    hi = mid - 1
+            decode_keys, pairs = cu_k[lo] - cu_k[0], 0
+            for r in range(lo, rows):
+                lq, lk = cu_q[r + 1] - cu_q[r], cu_k[r + 1] - cu_k[r]
+                if lq == 1:
+                    decode_keys += lk
+                elif lq > 1:  # query j of a prompt row sees lk - lq + j + 1 keys
+                    pairs += lq * (lk - lq) + lq * (lq + 1) // 2
+            decode_bytes = decode_keys * 2 * self.num_kv_heads * self.head_dim * elem_bytes
+            prompt_flops = 4 * self.num_heads * self.head_dim * pairs
             overlap = decode_bytes / DECODE_BYTES_PER_S >= prompt_flops / PROMPT_FLOPS_PER_S
             cache[key] = SCHEDULE_OVERLAP if overlap else SCHEDULE_SERIAL
         return cache[key]

@@ -297,3 +297,67 @@ def test_mixed_step_replays_in_a_graph(cuda):
         eager = b.forward(q, kn, vn, kc, vc, ctx)
         torch.cuda.synchronize()
         torch.testing.assert_close(out, eager, atol=0, rtol=0)
+
+
+def _wide_step(cuda, num_cached, num_new, bs=16, seed=0):
+    """Qwen3-8B head shapes (32/8, d128, bf16) over many rows: each row's pages are consecutive blocks."""
+    width = max(-(-(c + n) // bs) for c, n in zip(num_cached, num_new))
+    tables, at = [], 0
+    for c, n in zip(num_cached, num_new):
+        k = -(-(c + n) // bs)
+        tables.append(list(range(at, at + k)) + [-1] * (width - k))
+        at += k
+    step = paged_step(num_cached, num_new, tables, at, heads=32, kv_heads=8, dim=128, bs=bs, device=cuda,
+                      dtype=torch.bfloat16, seed=seed)
+    return tables, step
+
+
+def test_a_large_decode_batch_on_the_persistent_grid(cuda):
+    """256 decode rows of up to 600 keys split over 512-key items: enough items for the persistent ticket grid.
+    Checked against the oracle, then replayed from a captured graph with new queries and lengths (the plan kernel
+    re-zeroes the ticket counter on every replay), each replay equal to an eager call."""
+    gen = torch.Generator().manual_seed(3)
+    lens = torch.randint(16, 601, (256,), generator=gen).tolist()
+    tables, (qs, kf, vf, kn, vn, kc, vc, slots) = _wide_step(cuda, [n - 1 for n in lens], [1] * 256)
+    b = MI355XAttention(32, 128, 1 / math.sqrt(128), 8)
+    b.store_kvcache(kn, vn, kc, vc, slots)
+    q = torch.cat(qs).clone()
+    ctx = Context(context_lens=torch.tensor(lens, dtype=torch.int32, device=cuda),
+                  block_tables=torch.tensor(tables, dtype=torch.int32, device=cuda))
+    out = torch.empty_like(q)
+    b.decode(q, kc, vc, ctx, out=out)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out.float().cpu(), dense_expected(qs, kf, vf, 1 / math.sqrt(128)), atol=2e-2, rtol=1e-2)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        b.decode(q, kc, vc, ctx, out=out)
+    for step in range(3):
+        q.copy_(torch.randn(q.shape, generator=gen).to(q.dtype))
+        ctx.context_lens.copy_(torch.tensor([max(n - 53 * step, 1) for n in lens], dtype=torch.int32))
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = b.decode(q, kc, vc, ctx)
+        torch.cuda.synchronize()
+        torch.testing.assert_close(out, eager, atol=0, rtol=0)
+
+
+def test_a_mixed_step_of_many_decode_rows_under_both_schedules(cuda, monkeypatch):
+    """Two prompt chunks beside 600 decode rows (persistent decode grid): the overlapped and the serial schedule
+    both match the oracle and each other bit for bit."""
+    from lvattn import backend as B
+
+    gen = torch.Generator().manual_seed(4)
+    dec = torch.randint(16, 601, (600,), generator=gen).tolist()
+    num_cached, num_new = [100, 0] + [n - 1 for n in dec], [40, 70] + [1] * 600
+    tables, (qs, kf, vf, kn, vn, kc, vc, slots) = _wide_step(cuda, num_cached, num_new, seed=1)
+    b = MI355XAttention(32, 128, 1 / math.sqrt(128), 8)
+    b.store_kvcache(kn, vn, kc, vc, slots)
+    want = dense_expected(qs, kf, vf, 1 / math.sqrt(128))
+    outs = {}
+    for sched in (B.SCHEDULE_SERIAL, B.SCHEDULE_OVERLAP):
+        monkeypatch.setattr(b, "_schedule", lambda context, elem_bytes, s=sched: s)
+        out = b.forward(torch.cat(qs), kn, vn, kc, vc, context_for(num_cached, num_new, tables, cuda))
+        torch.cuda.synchronize()
+        torch.testing.assert_close(out.float().cpu(), want, atol=2e-2, rtol=1e-2)
+        outs[sched] = out
+    assert torch.equal(outs[B.SCHEDULE_SERIAL], outs[B.SCHEDULE_OVERLAP])

@@ -103,3 +103,27 @@ def test_prompt_tiles_overlap_decode_rows_only_when_the_decode_bytes_cover_them(
     few = Context(cu_seqlens_q_host=[0, 1, 2, 1538], cu_seqlens_k_host=[0, 300, 600, 4000])
     assert attn._schedule(few, 2) == B.SCHEDULE_SERIAL
     assert attn._schedule(Context(), 2) == B.SCHEDULE_AUTO  # no host lengths: the library default
+
+
+def test_the_schedule_choice_matches_a_per_row_count_in_any_row_order():
+    """The bisection over leading one-query rows plus the walk over the rest equals a plain per-row count, for
+    decode-first steps and for rows in any order."""
+    import random
+
+    from lvattn import backend as B
+
+    attn = MI355XAttention(16, 128, 0.1, 8)
+    rng = random.Random(0)
+    for trial in range(200):
+        rows = rng.randint(1, 40)
+        lq = [1 if rng.random() < 0.7 else rng.randint(2, 3000) for _ in range(rows)]
+        lk = [q + rng.randint(0, 20000 if q == 1 else 4000) for q in lq]
+        if trial % 2 == 0:  # decode-first, as prepare_batch orders rows
+            order = sorted(range(rows), key=lambda r: lq[r] != 1)
+            lq, lk = [lq[r] for r in order], [lk[r] for r in order]
+        cu_q = [0, *torch.tensor(lq).cumsum(0).tolist()]
+        cu_k = [0, *torch.tensor(lk).cumsum(0).tolist()]
+        dec = sum(k for q, k in zip(lq, lk) if q == 1) * 2 * 8 * 128 * 2
+        flops = sum(4 * 16 * 128 * sum(k - q + j + 1 for j in range(q)) for q, k in zip(lq, lk) if q > 1)
+        want = B.SCHEDULE_OVERLAP if dec / B.DECODE_BYTES_PER_S >= flops / B.PROMPT_FLOPS_PER_S else B.SCHEDULE_SERIAL
+        assert attn._schedule(Context(cu_seqlens_q_host=cu_q, cu_seqlens_k_host=cu_k), 2) == want
