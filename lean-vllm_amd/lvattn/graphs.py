@@ -12,6 +12,8 @@ on the device from the lengths in the graph, so nothing has to be refreshed befo
 
 from __future__ import annotations
 
+import itertools
+
 import numpy as np
 import torch
 
@@ -66,7 +68,7 @@ class DecodeGraphs:
         cached = np.full(bs, -q, dtype=np.int32)
         cached[:rows] = num_cached
         lengths = np.zeros(bs, dtype=np.int32)
-        lengths[:rows] = [len(b) for b in block_lists]
+        lengths[:rows] = np.fromiter(map(len, block_lists), np.int32, rows)
         if (lengths > self.max_blocks).any():
             raise ValueError(f"a block list is longer than the {self.max_blocks} blocks the graphs were sized for")
         need = -(-(cached[:rows] + q) // self.block_size)
@@ -78,11 +80,9 @@ class DecodeGraphs:
         indptr = host[2 * bs:3 * bs + 1]
         indptr[0] = 0
         np.cumsum(lengths, out=indptr[1:])
-        ids = host[3 * bs + 1:]
-        at = 0
-        for lst in block_lists:
-            ids[at:at + len(lst)] = lst
-            at += len(lst)
+        at = int(indptr[-1])
+        if at:
+            host[3 * bs + 1:3 * bs + 1 + at] = np.fromiter(itertools.chain.from_iterable(block_lists), np.int32, at)
         n = 3 * bs + 1 + at
         self._inputs[:n].copy_(self._host[:n], non_blocking=True)
         self._copied = torch.cuda.Event()

@@ -10,6 +10,8 @@ from the same per-row ints without touching per-token data.
 
 from __future__ import annotations
 
+import itertools
+
 import numpy as np
 import torch
 
@@ -56,18 +58,26 @@ class StagingBuffers:
             self._device[name] = buf
         return buf[:n]
 
-    def put(self, name: str, values: np.ndarray, dtype: torch.dtype) -> torch.Tensor:
-        """Copy host values into this name's device buffer through its pinned buffer."""
-        n = values.size
+    def host_view(self, name: str, n: int, dtype: torch.dtype) -> np.ndarray:
+        """The first ``n`` elements of this name's pinned host buffer, as a numpy array to fill in place."""
         host = self._pinned.get(name)
-        if host is None or host.numel() < n:
+        if host is None or host.numel() < n or host.dtype != dtype:
             cap = max(n, 2 * (host.numel() if host is not None else 0), MIN_CAPACITY)
             host = torch.empty(cap, dtype=dtype, pin_memory=True)
             self._pinned[name] = host
-        host[:n].numpy()[:] = values.reshape(-1)
+        return host[:n].numpy()
+
+    def upload(self, name: str, n: int, dtype: torch.dtype) -> torch.Tensor:
+        """Copy the first ``n`` elements of this name's pinned buffer to its device buffer (asynchronously)."""
         dev = self.device_buffer(name, n, dtype)
-        dev.copy_(host[:n], non_blocking=True)
+        dev.copy_(self._pinned[name][:n], non_blocking=True)
         return dev
+
+    def put(self, name: str, values: np.ndarray, dtype: torch.dtype) -> torch.Tensor:
+        """Copy host values into this name's device buffer through its pinned buffer."""
+        n = values.size
+        self.host_view(name, n, dtype)[:] = values.reshape(-1)
+        return self.upload(name, n, dtype)
 
 
 class PackPlan:
@@ -114,11 +124,10 @@ class Packer:
         rows = num_new.size
         if rows == 0:
             raise ValueError("pack: a step needs at least one row")
-        lengths = np.fromiter((len(b) for b in block_lists), np.int32, rows)
-        indptr = np.zeros(rows + 1, dtype=np.int32)
-        np.cumsum(lengths, out=indptr[1:])
-        ids = np.concatenate([np.asarray(b, dtype=np.int32) for b in block_lists]) if indptr[-1] else \
-            np.zeros(0, dtype=np.int32)
+        if len(num_cached) != rows or len(block_lists) != rows:
+            raise ValueError("pack: num_cached, num_new and block_lists need one entry per row")
+        lengths = np.fromiter(map(len, block_lists), np.int32, rows)
+        n_ids = int(lengths.sum())
         width = int(lengths.max())
         tokens = int(num_new.sum())
         query_len = decode_query_len(num_new, num_speculative_tokens)
@@ -134,15 +143,25 @@ class Packer:
             cu_seqlens_k_host=[0, *np.cumsum(ends_b).tolist()],
             decode_query_len=query_len,
         )
-        parts = [num_cached, num_new, indptr, ids]
-        logits = -1
+        logits, n_log = -1, None
         if host["is_prefill"]:
             n_log = np.ones(rows, np.int32) if num_logits is None else np.asarray(num_logits, dtype=np.int32)
             if n_log.shape != (rows,) or (n_log < 0).any() or (n_log > num_new).any():
                 raise ValueError("pack: num_logits must give 0 .. num_new logits rows per row")
-            parts.append(n_log)
             logits = int(n_log.sum())
-        inputs = self.buffers.put("inputs", np.concatenate(parts), torch.int32)
+        # One pinned buffer, filled in place: num_cached | num_new | block-list offsets | block ids | logits rows.
+        size = 3 * rows + 1 + n_ids + (rows if n_log is not None else 0)
+        buf = self.buffers.host_view("inputs", size, torch.int32)
+        buf[:rows] = num_cached
+        buf[rows:2 * rows] = num_new
+        buf[2 * rows] = 0
+        np.cumsum(lengths, out=buf[2 * rows + 1:3 * rows + 1])
+        if n_ids:
+            buf[3 * rows + 1:3 * rows + 1 + n_ids] = np.fromiter(itertools.chain.from_iterable(block_lists), np.int32,
+                                                                 n_ids)
+        if n_log is not None:
+            buf[3 * rows + 1 + n_ids:] = n_log
+        inputs = self.buffers.upload("inputs", size, torch.int32)
         slot_count = int(num_new[lengths > 0].sum())
         return PackPlan(rows, tokens, width, slot_count, query_len, inputs, host, logits)
 
