@@ -14,7 +14,8 @@ pages). The line also carries per-kernel times from HIP events on the launch str
 the attention op, a ``cpu_baseline`` (the oracle's restatement of the reference PyTorch backend timed on a bounded
 sample on the host cores) and, under ``workloads``, the same figures for the other shapes this path is measured on
 (Qwen3-8B pure decode at batch 256, long-context split-K decode, DeepSeek-V2-Lite MLA decode, Qwen3-0.6B mixed,
-and DeepSeek-V2-Lite MLA prefill chunks, which are MFMA work and report TFLOP/s against the bf16 peak).
+and two steps of prompts -- the Qwen3-8B mixed step's four chunks alone and DeepSeek-V2-Lite MLA prefill chunks --
+which are MFMA work and report TFLOP/s against the bf16 peak).
 """
 
 from __future__ import annotations
@@ -34,7 +35,9 @@ for _p in (ROOT, ROOT / "lean-vllm_amd"):
 PEAK_HBM_GBS = 8000.0
 PEAK_BF16_TFLOPS = 2500.0
 METRIC = "paged-attn HBM GB/s (% of peak) + tokens/s per layer, Qwen3-8B mixed batch"
-EXTRA = "qwen3_8b_decode,qwen3_8b_long,deepseek_v2_lite_mla,qwen3_0_6b_mixed,deepseek_v2_lite_mla_prefill"
+EXTRA = ("qwen3_8b_decode,qwen3_8b_long,deepseek_v2_lite_mla,qwen3_0_6b_mixed,qwen3_8b_prefill,"
+         "deepseek_v2_lite_mla_prefill")
+RIDGE_FLOP_PER_BYTE = PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)  # above it a step is MFMA-bound
 # Workloads whose whole working set fits the 256 MB Infinity Cache: each timed step starts from a flushed cache.
 FLUSHED = {"qwen3_0_6b_mixed"}
 
@@ -151,7 +154,7 @@ def measure(name: str, steps: int, warmup: int, seed: int, dev):
         "attention_frac_of_peak": round(attn_gbs / PEAK_HBM_GBS, 4),
         "attention_TFLOPs": round(flops / (attn_ms * 1e-3) / 1e12, 2),
         "attention_frac_of_mfma_peak": round(flops / (attn_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
-        "bound": "mfma" if wl.is_mla_prefill else "hbm",
+        "bound": "mfma" if flops / nbytes["attention"] > RIDGE_FLOP_PER_BYTE else "hbm",
         "bytes": nbytes,
         "flops": flops,
         "cache_flushed_each_step": flush is not None,
@@ -245,6 +248,8 @@ def attention_op(wl) -> str:
         return "lv_varlen_attention x2 (causal new tokens, unmasked prefix; varlen_kernel) + lv_merge_attn_states"
     if wl.is_mla:
         return "lv_mla_decode (mla_run_kernel + mla_run_merge_kernel)"
+    if all(n > 1 for n in wl.num_new):  # a step of prompts: the serial schedule, prompt tiles on the whole GPU
+        return "lv_paged_attention (plan_kernel + prompt_list_kernel)"
     if any(n > 1 for n in wl.num_new):
         return ("lv_paged_attention (plan_kernel + decode_persistent_kernel on a second stream beside "
                 "prompt_overlap_kernel + splitk_merge_kernel)")
@@ -318,7 +323,18 @@ def main():
             "kernel": attention_op(wl),
             "algorithmic_bytes_per_launch": primary["bytes"]["attention"],
             "tflops": primary["attention_TFLOPs"],
+        } if primary["bound"] == "hbm" else {
+            "bound": "mfma",
+            "achieved": primary["attention_TFLOPs"],
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": primary["attention_frac_of_mfma_peak"],
+            "traffic": traffic_of(primary["workload"]),
+            "kernel": attention_op(wl),
+            "algorithmic_flops_per_launch": primary["flops"],
+            "GBs": primary["attention_GBs"],
         },
+        "flops": primary["flops"],
         "workloads": extras,
     }
     if cpu is not None:

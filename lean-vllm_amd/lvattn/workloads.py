@@ -11,6 +11,7 @@ device. Key lengths include the token(s) stored this step (``context_lens = num_
 - ``qwen3_8b_decode``: 32/8 heads, d128, bs 256, pool 12,000; 256 decode rows, context U[512, 8192].
 - ``qwen3_8b_mixed``: 32/8 heads, d128, bs 256, pool 24,000; 4 chunks of 1536 new tokens on a cached prefix
   U[0, 6144], plus 2048 decode rows with context U[256, 4096] (8192 tokens).
+- ``qwen3_8b_prefill``: the four prompt chunks of ``qwen3_8b_mixed`` alone (a step of prompts; MFMA-bound).
 - ``qwen3_8b_long``: 32/8 heads, d128, bs 256, pool 10,000; 16 decode rows, context U[32768, 131072].
 - ``deepseek_v2_lite_mla``: 16 heads, latent 576 (512 + 64 rope), values 512, bs 64, pool 34,000; 128 decode
   rows, context U[1024, 16384]; values N(0, 0.5); scale 1/sqrt(192).
@@ -116,6 +117,14 @@ def qwen3_8b_mixed(seed: int = 0) -> Workload:
                     _tables(rng, 24_000, ends, 256), 1 / math.sqrt(128))
 
 
+def qwen3_8b_prefill(seed: int = 0) -> Workload:
+    """The Qwen3-8B mixed step's four prompt chunks alone (same draws): a step of prompts, MFMA-bound."""
+    mixed = qwen3_8b_mixed(seed)
+    rows = [i for i, n in enumerate(mixed.num_new) if n > 1]
+    return Workload("qwen3_8b_prefill", 32, 8, 128, 256, 24_000, [mixed.num_cached[i] for i in rows],
+                    [mixed.num_new[i] for i in rows], [mixed.block_lists[i] for i in rows], 1 / math.sqrt(128))
+
+
 def qwen3_8b_long(seed: int = 0) -> Workload:
     rng = np.random.default_rng(seed)
     ctx = rng.integers(32768, 131072 + 1, size=16)
@@ -147,6 +156,7 @@ WORKLOADS = {
     "qwen3_0_6b_mixed": qwen3_0_6b_mixed,
     "qwen3_8b_decode": qwen3_8b_decode,
     "qwen3_8b_mixed": qwen3_8b_mixed,
+    "qwen3_8b_prefill": qwen3_8b_prefill,
     "qwen3_8b_long": qwen3_8b_long,
     "deepseek_v2_lite_mla": deepseek_v2_lite_mla,
     "deepseek_v2_lite_mla_prefill": deepseek_v2_lite_mla_prefill,
