@@ -23,7 +23,8 @@ namespace lv {
 constexpr int kLatent = 576;              // latent width served: kv_lora_rank 512 + rope 64
 constexpr int kVDim = 512;                // value width: the latents' leading entries
 constexpr int kMlaTile = 32;              // latents per iteration
-constexpr int kMlaPitch = kLatent + 8;    // LDS row pitch in elements (1168 bytes): conflict-free operand reads
+constexpr int kMlaPitch = kLatent + 16;   // LDS row pitch in elements (1184 bytes): conflict-free operand reads and
+                                          // transposing reads (a 1168-byte pitch halves the latter's rate)
 constexpr int kLatChunks = kLatent / 8;   // 16-byte chunks per latent row
 constexpr int kMlaKHalf = kLatent / 64;   // MFMA k-steps (32 wide) per k half: 9
 constexpr int kStageLoads = kMlaTile * kLatChunks / 256;  // 16-byte chunks each thread stages per tile: 9
@@ -227,11 +228,12 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
 // loads is an explicit vmcnt.
 
 constexpr int kDmaTile = 16;                            // latents per stage
-constexpr int kDmaRowSlots = kLatChunks + 1;            // 16-byte slots per LDS row (one pad slot: pitch 1168 B)
-constexpr int kDmaStageSlots = kDmaTile * kDmaRowSlots;  // 1168
+constexpr int kDmaRowSlots = kLatChunks + 2;            // 16-byte slots per LDS row (two pad slots: pitch 1184 B)
+constexpr int kDmaStageSlots = kDmaTile * kDmaRowSlots;  // 1184
 constexpr int kDmaInstr = (kDmaStageSlots + 63) / 64;   // 64-lane loads per stage: 19, 5 per wave (4 for wave 3)
 constexpr int kDmaStageElems = kDmaStageSlots * 8;
 static_assert(kDmaRowSlots * 8 == kMlaPitch, "one LDS row pitch for both variants");
+static_assert(kDmaInstr == 19, "the stage waits count 5 loads for waves 0-2 and 4 for wave 3");
 
 // Wait until at most `ahead` (<= 6) stages of this wave's loads (5 per stage, 4 for wave 3) are outstanding, then meet
 // the other waves. No fence: the stage's LDS writes are exactly the loads waited for, and a fence would wait for
@@ -301,7 +303,7 @@ __global__ __launch_bounds__(256) void mla_decode_dma_kernel(MlaParams p) {
     for (int i = tid; i < npages; i += 256) page_off[i] = (int64_t)table[i] * p.c_sb;
   }
   // This wave's loads j = wave + 4 i (i < 5) of a stage's 19: slot 64 j + lane is 16-byte chunk `part` of latent
-  // row r of the stage. Slot 73 r + 72 of row r is LDS padding, filled with a copy of chunk 71.
+  // row r of the stage. Slots 74 r + 72 and 74 r + 73 of row r are LDS padding, filled with copies of chunk 71.
   int lrow[5], lpart[5];
 #pragma unroll
   for (int i = 0; i < 5; ++i) {
@@ -539,7 +541,7 @@ __global__ __launch_bounds__(256) void mla_run_kernel(MlaParams p) {
   cons = prod;
 
   // This wave's loads j = wave + 4 i (i < 5) of a stage's 19: slot 64 j + lane is 16-byte chunk `part` of row r
-  // (latent or head) of the stage. Slot 73 r + 72 of row r is LDS padding, filled with a copy of chunk 71.
+  // (latent or head) of the stage. Slots 74 r + 72 and 74 r + 73 of row r are LDS padding, filled with copies of chunk 71.
   int lrow[5], lpart[5];
 #pragma unroll
   for (int i = 0; i < 5; ++i) {
