@@ -425,12 +425,20 @@ __global__ __launch_bounds__(256) void mla_decode_dma_kernel(MlaParams p) {
 // every run it touches, and mla_run_merge_kernel combines them; that kernel also writes the zero output of units
 // that see no latents. Every run does equal work, whatever the spread of row lengths, and partials are written
 // only where a row crosses a run boundary.
+//
+// Each stage's work (the score MFMAs, their exchange, the softmax, P.V) runs between two barriers of one
+// workgroup, so a CU streams faster with more workgroups than with deeper rings: three workgroups with a two-stage
+// ring (one stage in flight while one is consumed) beat two with a four-stage ring by 7% on DeepSeek-V2-Lite's step,
+// and one workgroup with five or eight stages is 40% slower.
 
 constexpr int kRunMin = 16;          // stages per run at least (256 latents)
 #ifndef LV_MLA_RUN_STAGES
-#define LV_MLA_RUN_STAGES 4
+#define LV_MLA_RUN_STAGES 2
 #endif
-constexpr int kRunsPerCU = LV_MLA_RUN_STAGES <= 4 ? 2 : 1;  // workgroups that fit a CU's 160 KB of LDS
+#ifndef LV_MLA_RUNS_PER_CU
+#define LV_MLA_RUNS_PER_CU (LV_MLA_RUN_STAGES <= 2 ? 3 : LV_MLA_RUN_STAGES <= 4 ? 2 : 1)
+#endif
+constexpr int kRunsPerCU = LV_MLA_RUNS_PER_CU;  // workgroups that fit a CU's 160 KB of LDS
 constexpr int kRunMaxUnits = 8192;   // units the in-kernel scan serves
 
 __device__ __forceinline__ int unit_latents(const MlaParams& p, int u) {
