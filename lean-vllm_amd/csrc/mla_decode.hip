@@ -458,9 +458,14 @@ __device__ __forceinline__ int unit_stages(const MlaParams& p, int u) {
   return lk > 0 ? (lk + kDmaTile - 1) / kDmaTile : 0;
 }
 
-// Position in a run's stage sequence: unit u (prefix pu, tu stages, lk latents), next tile t (-1: its query).
+// Position in a run's stage sequence: unit u (prefix pu, tu stages, lk latents), next tile t (-1: its query). The
+// unit's query row tq and head tile ht, its block-table row, and the cache page of the last tile loaded are kept
+// here, so a stage's loads need no division and at most one page lookup per page.
 struct RunCursor {
   int u, pu, tu, lk, t;
+  int tq, ht, pg;
+  const int32_t* table;
+  const char* page;
   bool done;
 };
 
@@ -531,6 +536,11 @@ __global__ __launch_bounds__(256) void mla_run_kernel(MlaParams p) {
     r.lk = lk;
     r.tu = (lk + kDmaTile - 1) / kDmaTile;
     r.t = -1;
+    r.tq = u / p.htiles;
+    r.ht = u - r.tq * p.htiles;
+    r.table = p.tables + (int64_t)(r.tq / p.lq) * p.t_stride;
+    r.pg = -1;
+    r.page = nullptr;
     r.done = false;
   };
   auto advance = [&](RunCursor& r) {
@@ -560,23 +570,24 @@ __global__ __launch_bounds__(256) void mla_run_kernel(MlaParams p) {
   // Query stage: head ht 16 + r of the unit's token (heads past the last load the last head; not written).
   // Latent stage: latents t0 .. t0 + 15 of the row, one page (the page size is a multiple of 16); latents at
   // or past lk load latent lk - 1 instead (finite values; their weight is 0).
-  auto fill = [&](const RunCursor& r, uint16_t* stage) {
-    const int tq = r.u / p.htiles, ht = r.u - tq * p.htiles;
+  auto fill = [&](RunCursor& r, uint16_t* stage) {
     if (r.t < 0) {
-      const char* qrow = p.q + tq * p.q_st;
+      const char* qrow = p.q + r.tq * p.q_st;
 #pragma unroll
       for (int i = 0; i < 5; ++i) {
         const int j = wave + 4 * i;
         if (j < kDmaInstr && 64 * j + lane < kDmaStageSlots)
-          lds_dma16(qrow + (int64_t)min(ht * 16 + lrow[i], p.heads - 1) * p.q_sh + lpart[i],
+          lds_dma16(qrow + (int64_t)min(r.ht * 16 + lrow[i], p.heads - 1) * p.q_sh + lpart[i],
                     lds_addr(stage + 64 * 8 * j));
       }
     } else {
-      const int row = tq / p.lq;
       const int t0 = r.t * kDmaTile;
       const int pg = (int)p.bs.div(t0);
-      const int64_t blk = sload(p.tables + (int64_t)row * p.t_stride + pg);
-      const char* base = p.cache + blk * p.c_sb + (int64_t)(t0 - pg * (int)p.bs.d) * p.c_st;
+      if (pg != r.pg) {
+        r.pg = pg;
+        r.page = p.cache + (int64_t)sload(r.table + pg) * p.c_sb;
+      }
+      const char* base = r.page + (int64_t)(t0 - pg * (int)p.bs.d) * p.c_st;
       const int last = r.lk - 1 - t0;
 #pragma unroll
       for (int i = 0; i < 5; ++i) {
@@ -656,7 +667,7 @@ __global__ __launch_bounds__(256) void mla_run_kernel(MlaParams p) {
 
     if (cons.t + 1 == cons.tu || cons.pu + cons.t + 1 == end) {  // the unit's last stage in this run
       const float l = xor32_sum(xor16_sum(lsum));
-      const int tq = cons.u / p.htiles, head = (cons.u - tq * p.htiles) * 16 + n;
+      const int tq = cons.tq, head = cons.ht * 16 + n;
       const float inv = 1.f / l;  // l > 0: each of the run's stages of the unit holds a latent in range
       if (head < p.heads) {
         if (cons.pu >= start && cons.pu + cons.tu <= end) {
