@@ -260,19 +260,28 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
     static_assert(RING >= 2 && RING <= 3, "one or two tiles in flight");
     uint16_t* ring = reinterpret_cast<uint16_t*>(smem);
     const bool hi = wave < NJ % 4 || NJ % 4 == 0;
-    auto base_of = [&](int kt, bool v) -> const char* {  // wave-uniform source of key kt
-      const char* src = v ? p.v_cache : p.k_cache;
-      const int64_t st = v ? p.v_st : p.c_st, sh = v ? p.v_sh : p.c_sh;
-      if (p.paged) {
-        const int pg = (int)p.bs.div(kt);
-        return src + (int64_t)sload(table + pg) * p.c_sb + (int64_t)(kt - pg * (int)p.bs.d) * st + kvh * sh;
-      }
-      return src + (int64_t)(kbase + kt) * st + kvh * sh;
-    };
+    // Stages fill in key order, so the page of the last fill is kept: one page-table lookup per page, shared by
+    // the key and value sources (a page of 256 keys holds four tiles).
+    int cached_pg = -1;
+    int64_t page_off = 0;  // the cached page's byte offset in either cache
     auto fill = [&](int kt, uint16_t* stage) {
       const int last = lk - 1 - kt;
-      const char* kb = base_of(kt, false);
-      const char* vb = base_of(kt, true);
+      int64_t koff, voff;  // wave-uniform byte offsets of key kt of this kv head
+      if (p.paged) {
+        const int pg = (int)p.bs.div(kt);
+        if (pg != cached_pg) {
+          cached_pg = pg;
+          page_off = (int64_t)sload(table + pg) * p.c_sb;
+        }
+        const int in_page = kt - pg * (int)p.bs.d;
+        koff = page_off + (int64_t)in_page * p.c_st + kvh * p.c_sh;
+        voff = page_off + (int64_t)in_page * p.v_st + kvh * p.v_sh;
+      } else {
+        koff = (int64_t)(kbase + kt) * p.c_st + kvh * p.c_sh;
+        voff = (int64_t)(kbase + kt) * p.v_st + kvh * p.v_sh;
+      }
+      const char* kb = p.k_cache + koff;
+      const char* vb = p.v_cache + voff;
 #pragma unroll
       for (int i = 0; i < (NJ + 3) / 4; ++i) {
         const int j = wave + 4 * i;
