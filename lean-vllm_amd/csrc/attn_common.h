@@ -197,7 +197,7 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
       float x = -INFINITY;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
-        x = fmaxf(x, fmaxf(fmaxf(st[kb][nb][0], st[kb][nb][1]), fmaxf(st[kb][nb][2], st[kb][nb][3])));
+        x = vmax(x, vmax(vmax(st[kb][nb][0], st[kb][nb][1]), vmax(st[kb][nb][2], st[kb][nb][3])));
       mx[nb] = xor32_max(xor16_max(x));  // over the row's 64 keys of this tile
     }
     const bool grow = (mx[0] > m[0] && (m[0] == -INFINITY || (mx[0] - m[0]) * c > kRescaleSlack)) ||
@@ -205,7 +205,7 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
     if (__any(grow)) {
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
-        const float mn = fmaxf(m[nb], mx[nb]);
+        const float mn = vmax(m[nb], mx[nb]);
         const float alpha = m[nb] == -INFINITY ? 0.f : fast_exp2((m[nb] - mn) * c);
         m[nb] = mn;
         l[nb] *= alpha;

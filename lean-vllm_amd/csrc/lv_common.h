@@ -200,6 +200,12 @@ __device__ inline u32x2 lds_read_tr16(const uint16_t* p) {
 // ---------------------------------------------------------------------------------------------------------
 // Cross-row lane exchange.
 
+// Maximum of two scores, NaN-propagating (IEEE maximum): gfx950's v_maximum3_f32, which the compiler also fuses
+// into three-input maxima. fmaxf (maxNum) must first quiet a signalling NaN in every operand that is not a known
+// arithmetic result (an MFMA output, a lane swap), one extra instruction per operand. For scores the two agree:
+// a NaN score makes the row's output NaN either way.
+__device__ __forceinline__ float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
 // Sum / max over lanes i and i ^ 16, and over lanes i and i ^ 32, with gfx950's cross-row swaps (no LDS round trip).
 __device__ inline float xor16_sum(float x) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -209,13 +215,16 @@ __device__ inline float xor32_sum(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
+// IEEE: vmax (NaN-propagating), else fmaxf.
+template <bool IEEE = true>
 __device__ inline float xor16_max(float x) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return IEEE ? vmax(__uint_as_float(r[0]), __uint_as_float(r[1])) : fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
+template <bool IEEE = true>
 __device__ inline float xor32_max(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return IEEE ? vmax(__uint_as_float(r[0]), __uint_as_float(r[1])) : fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 // Exclusive prefix sum of a[0, n) in LDS, in place, by a block of kScanThreads threads; a[n] receives the total.
 // wave_tot holds kScanThreads / 64 + 1 ints of LDS. Every thread of the block must call it.

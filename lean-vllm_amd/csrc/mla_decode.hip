@@ -165,9 +165,9 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
         s1[r] = t0 + 16 + 4 * g + r < kend ? s1[r] : -INFINITY;
       }
     }
-    float mx = fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])), fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3])));
+    float mx = vmax(vmax(vmax(s0[0], s0[1]), vmax(s0[2], s0[3])), vmax(vmax(s1[0], s1[1]), vmax(s1[2], s1[3])));
     mx = xor32_max(xor16_max(mx));  // over the 32 latents of head n (finite: the tile holds one in range)
-    const float mn = fmaxf(m, mx);
+    const float mn = vmax(m, mx);
     const float alpha = fast_exp2((m - mn) * c);
     m = mn;
     const float mc = m * c;
@@ -367,10 +367,10 @@ __global__ __launch_bounds__(256) void mla_decode_dma_kernel(MlaParams p) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) sc[r] = t0 + 4 * g + r < kend ? sc[r] : -INFINITY;
       }
-      float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+      float mx = vmax(vmax(sc[0], sc[1]), vmax(sc[2], sc[3]));
       mx = xor32_max(xor16_max(mx));
       if (__any(mx > m && (m == -INFINITY || (mx - m) * c > kRescaleSlack))) {
-        const float mn = fmaxf(m, mx);
+        const float mn = vmax(m, mx);
         const float alpha = m == -INFINITY ? 0.f : fast_exp2((m - mn) * c);
         m = mn;
         lsum *= alpha;
@@ -645,10 +645,10 @@ __global__ __launch_bounds__(256) void mla_run_kernel(MlaParams p) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) sc[r] = t0 + 4 * g + r < cons.lk ? sc[r] : -INFINITY;
     }
-    float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+    float mx = vmax(vmax(sc[0], sc[1]), vmax(sc[2], sc[3]));
     mx = xor32_max(xor16_max(mx));
     if (__any(mx > m && (m == -INFINITY || (mx - m) * c > kRescaleSlack))) {
-      const float mn = fmaxf(m, mx);
+      const float mn = vmax(m, mx);
       const float alpha = m == -INFINITY ? 0.f : fast_exp2((m - mn) * c);
       m = mn;
       lsum *= alpha;

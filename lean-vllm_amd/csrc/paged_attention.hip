@@ -61,11 +61,11 @@ constexpr int kPlanMaxRows = 4096;  // rows of a step with prompts (the work-lis
 // the 16-bit format of the cache (fp32 accumulation), as the MFMA path does with its probability tiles.
 
 // Reduce over the lane groups of a wave that hold different tokens (lanes i, i + LPT, i + 2 LPT, ...).
-template <int LPT>
+template <int LPT, bool IEEE>
 __device__ inline float groups_max(float x) {
   static_assert(LPT == 8 || LPT == 16, "8 or 16 lanes per token");
-  if constexpr (LPT == 8) x = fmaxf(x, dpp_ror8(x));  // lane i and i ^ 8 of each 16-lane row
-  return xor32_max(xor16_max(x));
+  if constexpr (LPT == 8) x = IEEE ? vmax(x, dpp_ror8(x)) : fmaxf(x, dpp_ror8(x));  // lanes i, i ^ 8 of a row
+  return xor32_max<IEEE>(xor16_max<IEEE>(x));
 }
 template <int LPT>
 __device__ inline float groups_sum(float x) {
@@ -76,7 +76,10 @@ __device__ inline float groups_sum(float x) {
 
 // publish (persistent launches): thread 0 stores publish_value there before the item's merge barrier, and the
 // barrier is met even by an item with nothing to do, so the whole workgroup reads the value after the call.
-template <typename T, int D, int GS>
+// BESIDE: the workgroup shares its SIMDs with a mixed step's prompt tiles. Its score maxima then use vmax, which
+// issues about half the VALU instructions of fmaxf (no operand quieting); alone on the GPU the fmaxf build streams
+// 2% faster (its instruction schedule, not its VALU count, decides there).
+template <typename T, int D, int GS, bool BESIDE = false>
 __device__ void decode_item(const AttnParams& p, int row, int split, int kvh, int qg, char* smem,
                             int* publish = nullptr, int publish_value = 0) {
   using E = Elem<T>;
@@ -162,14 +165,14 @@ __device__ void decode_item(const AttnParams& p, int row, int split, int kvh, in
     for (int g = 0; g < GS; ++g) {
       float x = s[0][g];
 #pragma unroll
-      for (int u = 1; u < U; ++u) x = fmaxf(x, s[u][g]);
-      mt[g] = groups_max<LPT>(x);  // finite: every tile holds a token in range
+      for (int u = 1; u < U; ++u) x = BESIDE ? vmax(x, s[u][g]) : fmaxf(x, s[u][g]);
+      mt[g] = groups_max<LPT, BESIDE>(x);  // finite: every tile holds a token in range
       grow |= mt[g] > m[g];
     }
     if (__builtin_amdgcn_readfirstlane(grow)) {
 #pragma unroll
       for (int g = 0; g < GS; ++g) {
-        const float mn = fmaxf(m[g], mt[g]);
+        const float mn = BESIDE ? vmax(m[g], mt[g]) : fmaxf(m[g], mt[g]);
         const float alpha = fast_exp2((m[g] - mn) * c);
         m[g] = mn;
         l[g] *= alpha;
@@ -355,7 +358,7 @@ struct SmemBytes {
 // are dispatched in list order (longest first). The list holds a step's prompt items first (n_items[1] of them),
 // then its decode items (n_items[0] in all). Decode items run in decode_list_kernel at the decode item's register
 // budget; prompt items in prompt_list_kernel, whose MFMA tile needs more registers and LDS.
-template <typename T, int D, int GS>
+template <typename T, int D, int GS, bool BESIDE = false>
 __global__ __launch_bounds__(256) void decode_list_kernel(AttnParams p) {
   __shared__ __attribute__((aligned(16))) char smem[SmemBytes<D, GS>::kDecode];
   const int ny = p.hkv * p.qgroups;
@@ -364,14 +367,14 @@ __global__ __launch_bounds__(256) void decode_list_kernel(AttnParams p) {
   const int i = bx + p.n_items[1];
   if (i >= p.n_items[0]) return;
   const int2 it = p.items[i];
-  decode_item<T, D, GS>(p, it.x, it.y, kvh, qg, smem);
+  decode_item<T, D, GS, BESIDE>(p, it.x, it.y, kvh, qg, smem);
 }
 
 // Decode items of the work list on a persistent grid: each workgroup takes items by ticket (an atomic counter the
 // plan kernel zeroes), in list order, so the longest still go first. A fixed number of workgroups per CU lets a
 // mixed step's prompt workgroups stay resident beside them. The next ticket is drawn at the start of an item and
 // published at its merge barrier; the merge alternates between two LDS buffers, so one barrier per item suffices.
-template <typename T, int D, int GS>
+template <typename T, int D, int GS, bool BESIDE = false>
 __global__ __launch_bounds__(256, 4) void decode_persistent_kernel(AttnParams p) {
   __shared__ __attribute__((aligned(16))) char smem[2][SmemBytes<D, GS>::kDecode];
   __shared__ int s_ticket[2];
@@ -387,7 +390,7 @@ __global__ __launch_bounds__(256, 4) void decode_persistent_kernel(AttnParams p)
     const int bx = f / ny, by = f - bx * ny;
     const int kvh = by / p.qgroups, qg = by - kvh * p.qgroups;
     const int2 it = p.items[first + bx];
-    decode_item<T, D, GS>(p, it.x, it.y, kvh, qg, smem[k & 1], &s_ticket[(k + 1) & 1], next);
+    decode_item<T, D, GS, BESIDE>(p, it.x, it.y, kvh, qg, smem[k & 1], &s_ticket[(k + 1) & 1], next);
     f = __builtin_amdgcn_readfirstlane(s_ticket[(k + 1) & 1]);
   }
 }
@@ -612,15 +615,16 @@ static SideStream* side_stream() {
   return &s;
 }
 
-// Workgroups of `kernel` (256 threads) that one CU holds at once, from its register and LDS needs (cached).
-template <typename K>
-static int resident_per_cu(K kernel) {
+// Workgroups of kernel K (256 threads) that one CU holds at once, from its register and LDS needs (cached per
+// kernel and device).
+template <auto K>
+static int resident_per_cu() {
   static int cached[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
   if (cached[dev] > 0) return cached[dev];
   int n = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, 256, 0) != hipSuccess || n <= 0) n = 1;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, K, 256, 0) != hipSuccess || n <= 0) n = 1;
   cached[dev] = n;
   return n;
 }
@@ -629,15 +633,15 @@ static int resident_per_cu(K kernel) {
 // ticket (beside a mixed step's prompt workgroups a fixed share of every CU keeps both kernels resident), or one
 // workgroup per item -- for per_cu 0, and for steps whose item bound is under eight items per persistent
 // workgroup, whose few short items finish sooner all at once than in rounds.
-template <typename T, int D, int GS>
+template <typename T, int D, int GS, bool BESIDE = false>
 static void launch_decode(const AttnParams& p, const Shape& s, int per_cu, hipStream_t stream) {
   const int items = s.max_decode_items * p.hkv * p.qgroups;  // a bound: the plan lists no more
-  const int grid = per_cu > 0 ? std::min(per_cu, resident_per_cu(decode_persistent_kernel<T, D, GS>)) * device_cus()
-                              : 0;
+  const int grid =
+      per_cu > 0 ? std::min(per_cu, resident_per_cu<decode_persistent_kernel<T, D, GS, BESIDE>>()) * device_cus() : 0;
   if (grid > 0 && items >= 8 * grid) {
-    hipLaunchKernelGGL((decode_persistent_kernel<T, D, GS>), dim3(grid), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((decode_persistent_kernel<T, D, GS, BESIDE>), dim3(grid), dim3(256), 0, stream, p);
   } else {
-    hipLaunchKernelGGL((decode_list_kernel<T, D, GS>), dim3(items), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((decode_list_kernel<T, D, GS, BESIDE>), dim3(items), dim3(256), 0, stream, p);
   }
 }
 
@@ -654,7 +658,7 @@ static void launch(const AttnParams& p, bool listed, bool mixed, bool overlap, c
     std::lock_guard<std::mutex> g(side->lock);
     hipEventRecord(side->fork, stream);
     hipStreamWaitEvent(side->stream, side->fork, 0);
-    launch_decode<T, D, GS>(p, s, LV_OVERLAP_DECODE_WGS, side->stream);
+    launch_decode<T, D, GS, true>(p, s, LV_OVERLAP_DECODE_WGS, side->stream);
     hipEventRecord(side->join, side->stream);
     if (ring) {
       constexpr int pad = std::max(0, kOverlapLds - LV_PROMPT_RING * PromptSmem<D, D>::kBytes);
