@@ -710,25 +710,47 @@ __global__ __launch_bounds__(64) void mla_run_merge_kernel(MlaParams p) {
   if (tu > 0) {
     const int b0 = pu / per, b1 = (pu + tu - 1) / per;
     if (b0 == b1) return;
-    float mmax = -INFINITY;
-    for (int b = b0; b <= b1; ++b) {
-      const int slot = (b * 2 + (b == b0 && pu != b0 * per ? 1 : 0)) * 16 + h;
-      mmax = fmaxf(mmax, p.part_lse[slot]);
-    }
-    float den = 0.f;
-    for (int b = b0; b <= b1; ++b) {
-      const int slot = (b * 2 + (b == b0 && pu != b0 * per ? 1 : 0)) * 16 + h;
-      const float w = fast_exp2(p.part_lse[slot] - mmax);
-      den += w;
-      const f32x4* src = reinterpret_cast<const f32x4*>(p.part_o + (int64_t)slot * kVDim + lane * PER);
+    // The runs' partials, kRunMergeBatch at a time with every load of a batch issued before the first is used;
+    // the max and the sums carry from batch to batch.
+    constexpr int kRunMergeBatch = 4;
+    float m = -INFINITY, den = 0.f;
+    for (int c0 = b0; c0 <= b1; c0 += kRunMergeBatch) {
+      float ls[kRunMergeBatch];
+      f32x4 x[kRunMergeBatch][PER / 4];
 #pragma unroll
-      for (int e = 0; e < PER / 4; ++e) {
-        const f32x4 v = src[e];
+      for (int i = 0; i < kRunMergeBatch; ++i) {
+        const int b = c0 + i;
+        ls[i] = -INFINITY;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) o[4 * e + r] = fmaf(w, v[r], o[4 * e + r]);
+        for (int e = 0; e < PER / 4; ++e) x[i][e] = f32x4{0, 0, 0, 0};
+        if (b <= b1) {  // wave-uniform
+          const int slot = (b * 2 + (b == b0 && pu != b0 * per ? 1 : 0)) * 16 + h;
+          ls[i] = p.part_lse[slot];
+          const f32x4* src = reinterpret_cast<const f32x4*>(p.part_o + (int64_t)slot * kVDim + lane * PER);
+#pragma unroll
+          for (int e = 0; e < PER / 4; ++e) x[i][e] = src[e];
+        }
       }
+      float bm = m;
+#pragma unroll
+      for (int i = 0; i < kRunMergeBatch; ++i) bm = fmaxf(bm, ls[i]);
+      if (bm == -INFINITY) continue;
+      const float alpha = fast_exp2(m - bm);  // 0 while m is -inf
+      den *= alpha;
+#pragma unroll
+      for (int e = 0; e < PER; ++e) o[e] *= alpha;
+#pragma unroll
+      for (int i = 0; i < kRunMergeBatch; ++i) {
+        const float w = fast_exp2(ls[i] - bm);  // 0 past the last run
+        den += w;
+#pragma unroll
+        for (int e = 0; e < PER / 4; ++e)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o[4 * e + r] = fmaf(w, x[i][e][r], o[4 * e + r]);
+      }
+      m = bm;
     }
-    const float inv = 1.f / den;
+    const float inv = den > 0.f ? 1.f / den : 0.f;
 #pragma unroll
     for (int e = 0; e < PER; ++e) o[e] *= inv;
   }

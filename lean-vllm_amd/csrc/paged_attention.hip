@@ -501,7 +501,10 @@ __global__ __launch_bounds__(kScanThreads) void plan_kernel(const int32_t* __res
   }
 }
 
-// Combine a split row's partial outputs: o = sum_s 2^(lse_s - M) o_s / sum_s 2^(lse_s - M).
+// Combine a split row's partial outputs: o = sum_s 2^(lse_s - M) o_s / sum_s 2^(lse_s - M). The partials are read
+// kMergeBatch splits at a time, every load of a batch issued before the first is used, with the max and the sums
+// carried from batch to batch (a long row's 32 splits are two round trips to memory, not 64).
+constexpr int kMergeBatch = 16;
 template <typename T, int D>
 __global__ __launch_bounds__(64) void splitk_merge_kernel(AttnParams p) {
   using E = Elem<T>;
@@ -512,30 +515,48 @@ __global__ __launch_bounds__(64) void splitk_merge_kernel(AttnParams p) {
   if (nsplit <= 1) return;
   const int tok = p.cu_q ? p.cu_q[row] : row;
   const int64_t slot0 = ((int64_t)row * p.hq + head) * p.max_splits;
-  float mmax = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) mmax = fmaxf(mmax, p.part_lse[slot0 + s]);
-  constexpr int PER = D / 64 > 0 ? D / 64 : 1;
-  float o[PER];
+  constexpr int PER = D / 64;  // dims per lane
+  float m = -INFINITY, den = 0.f, o[PER];
 #pragma unroll
   for (int e = 0; e < PER; ++e) o[e] = 0.f;
-  float den = 0.f;
-  for (int s = 0; s < nsplit; ++s) {
-    const float w = fast_exp2(p.part_lse[slot0 + s] - mmax);
-    den += w;
-    const float* src = p.part_o + (slot0 + s) * D;
+  for (int s0 = 0; s0 < nsplit; s0 += kMergeBatch) {
+    float ls[kMergeBatch], x[kMergeBatch][PER];
 #pragma unroll
-    for (int e = 0; e < PER; ++e)
-      if (lane * PER + e < D) o[e] = fmaf(w, src[lane * PER + e], o[e]);
-  }
-  const float inv = 1.f / den;
-  char* dst = p.out + tok * p.o_st + head * p.o_sh;
+    for (int i = 0; i < kMergeBatch; ++i) {
+      ls[i] = -INFINITY;
 #pragma unroll
-  for (int e = 0; e < PER; ++e) {
-    const int d = lane * PER + e;
-    if (d < D) {
-      const uint32_t packed = E::pack(o[e] * inv, 0.f);
-      *reinterpret_cast<uint16_t*>(dst + d * 2) = (uint16_t)(packed & 0xffffu);
+      for (int e = 0; e < PER; ++e) x[i][e] = 0.f;
+      if (s0 + i < nsplit) {  // wave-uniform
+        ls[i] = p.part_lse[slot0 + s0 + i];
+        const float* src = p.part_o + (slot0 + s0 + i) * D;
+#pragma unroll
+        for (int e = 0; e < PER; ++e) x[i][e] = src[lane * PER + e];
+      }
     }
+    float bm = m;
+#pragma unroll
+    for (int i = 0; i < kMergeBatch; ++i) bm = fmaxf(bm, ls[i]);
+    if (bm == -INFINITY) continue;
+    const float alpha = fast_exp2(m - bm);  // 0 while m is -inf
+    den *= alpha;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) o[e] *= alpha;
+#pragma unroll
+    for (int i = 0; i < kMergeBatch; ++i) {
+      const float w = fast_exp2(ls[i] - bm);  // 0 past the last split
+      den += w;
+#pragma unroll
+      for (int e = 0; e < PER; ++e) o[e] = fmaf(w, x[i][e], o[e]);
+    }
+    m = bm;
+  }
+  const float inv = den > 0.f ? 1.f / den : 0.f;
+  char* dst = p.out + tok * p.o_st + head * p.o_sh + (int64_t)lane * PER * 2;
+  if constexpr (PER == 2) {
+    *reinterpret_cast<uint32_t*>(dst) = E::pack(o[0] * inv, o[1] * inv);
+  } else {
+    static_assert(PER == 1, "D = 64 or 128");
+    *reinterpret_cast<uint16_t*>(dst) = (uint16_t)(E::pack(o[0] * inv, 0.f) & 0xffffu);
   }
 }
 
