@@ -226,8 +226,21 @@ __device__ inline float xor32_max(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return IEEE ? vmax(__uint_as_float(r[0]), __uint_as_float(r[1])) : fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ inline int wave_incl_scan(int x) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(x, d, 64);
+    if (lane >= d) x += y;
+  }
+  return x;
+}
+
 // Exclusive prefix sum of a[0, n) in LDS, in place, by a block of kScanThreads threads; a[n] receives the total.
-// wave_tot holds kScanThreads / 64 + 1 ints of LDS. Every thread of the block must call it.
+// wave_tot holds kScanThreads / 64 + 1 ints of LDS. Every thread of the block must call it. Each thread scans its
+// chunk, each wave its threads' chunk totals; every thread then sums the wave totals before its own (16 broadcast
+// LDS reads, issued together) instead of one thread scanning them in sequence between two more barriers.
 constexpr int kScanThreads = 1024;
 __device__ inline void block_scan(int* a, int n, int* wave_tot) {
   const int tid = threadIdx.x;
@@ -236,30 +249,23 @@ __device__ inline void block_scan(int* a, int n, int* wave_tot) {
   int local = 0;
   for (int i = lo; i < hi; ++i) local += a[i];
   const int lane = tid & 63, wave = tid >> 6;
-  int x = local;  // inclusive scan of the chunk totals across the wave
-  for (int d = 1; d < 64; d <<= 1) {
-    const int y = __shfl_up(x, d, 64);
-    if (lane >= d) x += y;
-  }
+  const int x = wave_incl_scan(local);  // inclusive scan of the chunk totals across the wave
   if (lane == 63) wave_tot[wave] = x;
   __syncthreads();
-  if (tid == 0) {
-    int run = 0;
-    for (int w = 0; w < kScanThreads / 64; ++w) {
-      const int v = wave_tot[w];
-      wave_tot[w] = run;
-      run += v;
-    }
-    wave_tot[kScanThreads / 64] = run;
+  int before = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < kScanThreads / 64; ++w) {
+    const int v = wave_tot[w];
+    before += w < wave ? v : 0;
+    total += v;
   }
-  __syncthreads();
-  int run = wave_tot[wave] + x - local;  // exclusive prefix of this thread's chunk
+  int run = before + x - local;  // exclusive prefix of this thread's chunk
   for (int i = lo; i < hi; ++i) {
     const int v = a[i];
     a[i] = run;
     run += v;
   }
-  if (tid == 0) a[n] = wave_tot[kScanThreads / 64];
+  if (tid == 0) a[n] = total;
   __syncthreads();
 }
 

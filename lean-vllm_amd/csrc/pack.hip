@@ -10,7 +10,7 @@
 namespace lv {
 
 constexpr int kPackThreads = kScanThreads;
-constexpr int kPackMaxRows = 4096;  // LDS holds four (rows + 1)-int arrays
+constexpr int kPackMaxRows = 4096;  // LDS holds seven (rows + 1)-int arrays (112 KB)
 
 __global__ __launch_bounds__(kPackThreads) void pack_kernel(
     const int32_t* __restrict__ num_cached, const int32_t* __restrict__ num_new, const int32_t* __restrict__ indptr,
@@ -24,16 +24,29 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
   __shared__ int cu_s[kPackMaxRows + 1];  // slot_mapping offsets (rows with a block list only), batch order
   __shared__ int row_of[kPackMaxRows];    // scheduler row -> batch row (logits only)
   __shared__ int wave_tot[kPackThreads / 64 + 1];
+  __shared__ int s_cached[kPackMaxRows];    // the per-row inputs, staged once: every later read is from LDS
+  __shared__ int s_new[kPackMaxRows];
+  __shared__ int s_ptr[kPackMaxRows + 1];
   const int tid = threadIdx.x;
 
+  // 0. Stage the row inputs (their loads all issued before any is used).
+  for (int i = tid; i <= rows; i += kPackThreads) {
+    s_ptr[i] = indptr[i];
+    if (i < rows) {
+      s_cached[i] = num_cached[i];
+      s_new[i] = num_new[i];
+    }
+  }
+  __syncthreads();
+
   // 1. Stable partition: rows of query_len first, scheduler order kept in each group (model_runner.py:367-374).
-  for (int i = tid; i < rows; i += kPackThreads) cu_q[i] = num_new[i] == query_len ? 1 : 0;
+  for (int i = tid; i < rows; i += kPackThreads) cu_q[i] = s_new[i] == query_len ? 1 : 0;
   __syncthreads();
   block_scan(cu_q, rows, wave_tot);
   const int leading = cu_q[rows];
   for (int i = tid; i < rows; i += kPackThreads) {
     const int before = cu_q[i];  // leading rows before i
-    const bool lead = num_new[i] == query_len;
+    const bool lead = s_new[i] == query_len;
     src[lead ? before : leading + (i - before)] = i;
   }
   __syncthreads();
@@ -41,8 +54,8 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
   // 2. Row prefix sums in batch order (model_runner.py:393-397).
   for (int r = tid; r < rows; r += kPackThreads) {
     const int s = src[r];
-    cu_q[r] = num_new[s];
-    cu_s[r] = dense_slots || indptr[s + 1] > indptr[s] ? num_new[s] : 0;
+    cu_q[r] = s_new[s];
+    cu_s[r] = dense_slots || s_ptr[s + 1] > s_ptr[s] ? s_new[s] : 0;
   }
   __syncthreads();
   block_scan(cu_q, rows, wave_tot);
@@ -54,7 +67,7 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
       const int s = src[r];
       order[r] = s;
       cu_q_out[r] = cu_q[r];
-      context_lens[r] = num_cached[s] + num_new[s];
+      context_lens[r] = s_cached[s] + s_new[s];
     }
     if (tid == 0) cu_q_out[rows] = cu_q[rows];
   }
@@ -69,23 +82,24 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
     }
     const int r = lo, s = src[r];
     const int offset = t - cu_q[r];
-    const int64_t pos = (int64_t)num_cached[s] + offset;
+    const int pos = s_cached[s] + offset;  // a position fits 32 bits (num_cached and num_new are int32)
     positions[t] = pos;
-    const int list = indptr[s], len = indptr[s + 1] - list;
+    const int list = s_ptr[s], len = s_ptr[s + 1] - list;
     if (len > 0) {
-      const int64_t block = blk_ids[list + (int)(pos / bs)];
-      slots[cu_s[r] + offset] = (int32_t)(block * bs + pos % bs);
+      const int page = pos / bs;
+      const int64_t block = blk_ids[list + page];
+      slots[cu_s[r] + offset] = (int32_t)(block * bs + (pos - page * bs));
     } else if (dense_slots) {
       slots[cu_s[r] + offset] = -1;  // a padding row of a captured step: its tokens store nothing
     }
   }
 
   // 5. Padded block tables (model_runner.py:437-439).
-  const int64_t cells = (int64_t)rows * width;
-  for (int64_t e = (int64_t)blockIdx.x * kPackThreads + tid; e < cells; e += stride) {
-    const int r = (int)(e / width), j = (int)(e - (int64_t)r * width);
+  const int cells = rows * width;  // the table's int32 cells (the caller's tensor: under 2^31)
+  for (int e = blockIdx.x * kPackThreads + tid; e < cells; e += stride) {
+    const int r = e / width, j = e - r * width;
     const int s = src[r];
-    const int list = indptr[s], len = indptr[s + 1] - list;
+    const int list = s_ptr[s], len = s_ptr[s + 1] - list;
     tables[e] = j < len ? blk_ids[list + j] : -1;
   }
 
@@ -93,12 +107,12 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
   // last num_logits[s] token rows of its chunk (its drafts, then the next token).
   if (blockIdx.x == 0 && num_logits) {
     __syncthreads();  // this workgroup's tokens are done with cu_s
-    for (int i = tid; i < rows; i += kPackThreads) cu_s[i] = num_new[i] == query_len ? 1 : 0;
+    for (int i = tid; i < rows; i += kPackThreads) cu_s[i] = s_new[i] == query_len ? 1 : 0;
     __syncthreads();
     block_scan(cu_s, rows, wave_tot);
     for (int i = tid; i < rows; i += kPackThreads) {
       const int before = cu_s[i];
-      row_of[i] = num_new[i] == query_len ? before : leading + (i - before);
+      row_of[i] = s_new[i] == query_len ? before : leading + (i - before);
     }
     __syncthreads();
     for (int i = tid; i < rows; i += kPackThreads) cu_s[i] = num_logits[i];
@@ -116,7 +130,7 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
     __syncthreads();
     for (int r = tid; r < rows; r += kPackThreads) {
       const int s = src[r];
-      cu_q[r] = num_cached[s] + num_new[s];
+      cu_q[r] = s_cached[s] + s_new[s];
     }
     __syncthreads();
     block_scan(cu_q, rows, wave_tot);
@@ -138,6 +152,8 @@ extern "C" int lv_pack(const int32_t* num_cached, const int32_t* num_new, const 
              kPackMaxRows);
   LV_REQUIRE(block_size > 0, "pack: block_size must be positive, got %d", block_size);
   LV_REQUIRE(table_width >= 0 && num_tokens >= 0, "pack: negative table width or token count");
+  LV_REQUIRE((int64_t)num_rows * table_width <= INT32_MAX, "pack: a %d x %d block table exceeds 2^31 cells", num_rows,
+             table_width);
   LV_REQUIRE(num_cached && num_new && blk_indptr && order && cu_seqlens_q && cu_seqlens_k && context_lens,
              "pack: null row pointer");
   LV_REQUIRE(num_tokens == 0 || positions, "pack: null positions");

@@ -468,18 +468,15 @@ __global__ __launch_bounds__(kScanThreads) void plan_kernel(const int32_t* __res
     }
   }
   __syncthreads();
-  block_scan(pre, rows, wave_tot);
-  block_scan(full, rows, wave_tot);
-  if (tid == 0) {
-    int run = 0;
-    for (int b = 0; b < kLenBuckets; ++b) {
-      const int v = bucket[b];
-      bucket[b] = run;
-      run += v;
-    }
-    bucket[kLenBuckets] = run;
+  if (tid < kLenBuckets) {  // wave 0: the bucket counts to offsets (one bucket per lane)
+    static_assert(kLenBuckets == 64, "one wave scans the buckets");
+    const int v = bucket[tid];
+    const int x = wave_incl_scan(v);
+    bucket[tid] = x - v;
+    if (tid == kLenBuckets - 1) bucket[kLenBuckets] = x;
   }
-  __syncthreads();
+  block_scan(pre, rows, wave_tot);  // its barriers also publish the bucket offsets
+  block_scan(full, rows, wave_tot);
   const int npre = pre[rows], nfull = full[rows], npart = bucket[kLenBuckets];
   for (int r = tid; r < rows; r += kScanThreads) {
     for (int i = pre[r]; i < pre[r + 1]; ++i)

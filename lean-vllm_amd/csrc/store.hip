@@ -1,6 +1,6 @@
 // store_kvcache / store_latents: scatter this step's new rows into the paged cache by slot.
 //
-// One workgroup per token. Each thread copies VEC-byte pieces of the token's key and value rows to
+// Four tokens per workgroup. Each thread copies VEC-byte pieces of the tokens' key and value rows to
 // (block, offset, head) addressed through the cache's own strides, so NHD caches and HND caches seen through a
 // transposed view take the same kernel. Slot -1 leaves the cache untouched. The copy is bit-exact: bytes move,
 // nothing is converted.
@@ -16,30 +16,43 @@ template <> struct Piece<4> { typedef uint32_t type; };
 template <> struct Piece<2> { typedef uint16_t type; };
 template <> struct Piece<1> { typedef uint8_t type; };
 
+// kStoreTokens tokens per workgroup: their slots, then every piece of theirs that a thread copies, are loaded
+// before the first is used, so a workgroup waits for two round trips to memory, not two per token.
+constexpr int kStoreTokens = 4;
 template <int VEC>
 __global__ __launch_bounds__(256) void store_kv_kernel(const char* __restrict__ key, const char* __restrict__ value,
                                                        int64_t key_row, int64_t value_row, int32_t pieces_per_head,
                                                        int32_t pieces_per_row, char* __restrict__ k_cache,
                                                        char* __restrict__ v_cache, int64_t sb, int64_t st, int64_t sh,
-                                                       int32_t block_size, const int32_t* __restrict__ slots) {
+                                                       int32_t block_size, const int32_t* __restrict__ slots,
+                                                       int32_t tokens) {
   typedef typename Piece<VEC>::type P;
-  const int t = blockIdx.x;
-  const int slot = slots[t];
-  if (slot < 0) return;
-  const int64_t block = slot / block_size;
-  const int64_t offset = slot % block_size;
-  const int64_t base = block * sb + offset * st;
-  const char* krow = key + (int64_t)t * key_row;
-  const char* vrow = value + (int64_t)t * value_row;
+  const int t0 = blockIdx.x * kStoreTokens;
+  int64_t base[kStoreTokens];  // cache byte offset of each token's (block, offset)
+  bool keep[kStoreTokens];     // slot -1, or past the last token: nothing stored
+#pragma unroll
+  for (int k = 0; k < kStoreTokens; ++k) {
+    const int slot = t0 + k < tokens ? slots[t0 + k] : -1;
+    keep[k] = slot >= 0;
+    base[k] = keep[k] ? (int64_t)(slot / block_size) * sb + (int64_t)(slot % block_size) * st : 0;
+  }
   // Pieces [0, pieces_per_row) are the key row, the rest the value row.
   for (int i = threadIdx.x; i < 2 * pieces_per_row; i += blockDim.x) {
     const bool is_v = i >= pieces_per_row;
     const int j = is_v ? i - pieces_per_row : i;
     const int head = j / pieces_per_head;
     const int within = j - head * pieces_per_head;
-    const int64_t dst = base + head * sh + (int64_t)within * VEC;
-    const P piece = *reinterpret_cast<const P*>((is_v ? vrow : krow) + (int64_t)j * VEC);
-    *reinterpret_cast<P*>((is_v ? v_cache : k_cache) + dst) = piece;
+    const int64_t dst = head * sh + (int64_t)within * VEC;
+    const char* src = (is_v ? value : key) + (int64_t)j * VEC;
+    const int64_t row = is_v ? value_row : key_row;
+    char* cache = is_v ? v_cache : k_cache;
+    P piece[kStoreTokens];
+#pragma unroll
+    for (int k = 0; k < kStoreTokens; ++k)
+      if (keep[k]) piece[k] = *reinterpret_cast<const P*>(src + (int64_t)(t0 + k) * row);
+#pragma unroll
+    for (int k = 0; k < kStoreTokens; ++k)
+      if (keep[k]) *reinterpret_cast<P*>(cache + base[k] + dst) = piece[k];
   }
 }
 
@@ -96,10 +109,10 @@ extern "C" int lv_store_kvcache(const void* key, const void* value, int64_t key_
   const int threads = ppr * 2 >= 256 ? 256 : ((ppr * 2 + 63) / 64) * 64;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
 #define LV_STORE_LAUNCH(V)                                                                                     \
-  hipLaunchKernelGGL(store_kv_kernel<V>, dim3(num_tokens), dim3(threads), 0, s, (const char*)key,              \
-                     (const char*)value, key_stride_t * eb, value_stride_t * eb, pph, ppr, (char*)k_cache,     \
-                     (char*)v_cache, cache_stride_block * eb, cache_stride_token * eb, cache_stride_head * eb, \
-                     block_size, slot_mapping)
+  hipLaunchKernelGGL(store_kv_kernel<V>, dim3((num_tokens + kStoreTokens - 1) / kStoreTokens), dim3(threads), 0, \
+                     s, (const char*)key, (const char*)value, key_stride_t * eb, value_stride_t * eb, pph, ppr,  \
+                     (char*)k_cache, (char*)v_cache, cache_stride_block * eb, cache_stride_token * eb,           \
+                     cache_stride_head * eb, block_size, slot_mapping, num_tokens)
   switch (vec) {
     case 16: LV_STORE_LAUNCH(16); break;
     case 8: LV_STORE_LAUNCH(8); break;
