@@ -80,10 +80,13 @@ def test_mixed_batch_of_chunks_and_decodes(case):
 
 
 @pytest.mark.parametrize("bs", [16, 64])
-def test_both_launch_schedules_give_the_same_step(case, bs, monkeypatch):
+@pytest.mark.parametrize("poison", [None, float("nan")], ids=["clean", "nan-slots"])
+def test_both_launch_schedules_give_the_same_step(case, bs, poison, monkeypatch):
     """A mixed step (chunks on cached prefixes, decode rows, a cold prompt) under the serial schedule (prompt
     tiles on the whole GPU, then the decode rows) and the overlapped one (prompt tiles beside the decode rows):
-    both match the oracle and each other bit for bit, since every item runs the same code either way."""
+    both match the oracle and each other bit for bit, since every item computes the same values either way (the
+    decode items beside prompt tiles take their score maxima by IEEE maximum, which agrees with fmaxf on scores).
+    With NaN in every unused cache slot, no NaN may reach a score under either schedule."""
     from lvattn import backend as B
 
     b, dtype, dim, dev = case
@@ -94,8 +97,9 @@ def test_both_launch_schedules_give_the_same_step(case, bs, monkeypatch):
         k = -(-(c + n) // bs)
         tables.append(list(range(at, at + k)) + [-1] * (width - k))
         at += k
-    qs, kf, vf, kn, vn, kc, vc, slots = paged_step(cached, new, tables, at, heads=H, kv_heads=HKV, dim=dim, bs=bs,
-                                                   device=dev, dtype=dtype)
+    fill = {} if poison is None else {"fill": poison}
+    qs, kf, vf, kn, vn, kc, vc, slots = paged_step(cached, new, tables, at + 1, heads=H, kv_heads=HKV, dim=dim, bs=bs,
+                                                   device=dev, dtype=dtype, **fill)
     b.store_kvcache(kn, vn, kc, vc, slots)
     want = dense_expected(qs, kf, vf, SCALE)
     outs = {}
@@ -103,6 +107,7 @@ def test_both_launch_schedules_give_the_same_step(case, bs, monkeypatch):
         monkeypatch.setattr(b, "_schedule", lambda context, elem_bytes, s=sched: s)
         out = b.forward(torch.cat(qs), kn, vn, kc, vc, context_for(cached, new, tables, dev))
         torch.cuda.synchronize()
+        assert torch.isfinite(out).all()
         check(out, want, dtype)
         outs[sched] = out
     assert torch.equal(outs[B.SCHEDULE_SERIAL], outs[B.SCHEDULE_OVERLAP])
