@@ -1,0 +1,127 @@
+// Host side of the ragged-batch packing: the Scheduler's per-row Python ints and block lists into the one int32
+// staging buffer that crosses PCIe (CPython extension module `lvattn._hoststage`).
+//
+// ModelRunner.prepare_batch (lean_vllm/engine/model_runner.py:349-464) walks the rows in Python; the GPU pack
+// kernel now derives everything from (num_cached, num_new, block list) per row, so the host only lays those out:
+//   num_cached[rows] | num_new[rows] | block-list offsets[rows + 1] | block ids[n_ids]
+// Walking the Python lists here costs a few ns per element, against about 28 ns for numpy.fromiter over a chained
+// iterator (0.5 ms for the 18,842 block ids of a 2,052-row step).
+#define PY_SSIZE_T_CLEAN
+#include <Python.h>
+
+#include <cstdint>
+
+namespace {
+
+// Items of a list or tuple without a copy; any other sequence through PySequence_Fast (a new reference in *hold).
+bool items_of(PyObject* seq, PyObject*** items, Py_ssize_t* n, PyObject** hold) {
+  *hold = PySequence_Fast(seq, "expected a sequence");
+  if (!*hold) return false;
+  *items = PySequence_Fast_ITEMS(*hold);
+  *n = PySequence_Fast_GET_SIZE(*hold);
+  return true;
+}
+
+bool to_i32(PyObject* o, int32_t* out) {
+  const long v = PyLong_AsLong(o);
+  if (v == -1 && PyErr_Occurred()) return false;
+  if (v < INT32_MIN || v > INT32_MAX) {
+    PyErr_Format(PyExc_OverflowError, "value %ld does not fit int32", v);
+    return false;
+  }
+  *out = (int32_t)v;
+  return true;
+}
+
+// stage_rows(num_cached, num_new, block_lists, address, capacity) -> (rows, n_ids, width)
+// Writes the layout above into the int32 buffer at `address` (capacity in int32 elements; the caller sizes it
+// with count_ids first or generously). Raises ValueError on mismatched lengths or a buffer too small.
+PyObject* stage_rows(PyObject*, PyObject* args) {
+  PyObject *cached, *fresh, *lists;
+  unsigned long long address;
+  Py_ssize_t capacity;
+  if (!PyArg_ParseTuple(args, "OOOKn", &cached, &fresh, &lists, &address, &capacity)) return nullptr;
+  PyObject *hc = nullptr, *hn = nullptr, *hl = nullptr;
+  PyObject **ic, **in, **il;
+  Py_ssize_t rows, rn, rl;
+  PyObject* result = nullptr;
+  int32_t* buf = reinterpret_cast<int32_t*>(static_cast<uintptr_t>(address));
+  if (!items_of(cached, &ic, &rows, &hc) || !items_of(fresh, &in, &rn, &hn) || !items_of(lists, &il, &rl, &hl))
+    goto done;
+  if (rn != rows || rl != rows) {
+    PyErr_SetString(PyExc_ValueError, "pack: num_cached, num_new and block_lists need one entry per row");
+    goto done;
+  }
+  if (3 * rows + 1 > capacity) {
+    PyErr_SetString(PyExc_ValueError, "pack: staging buffer too small");
+    goto done;
+  }
+  {
+    int32_t* offs = buf + 2 * rows;
+    int32_t* ids = buf + 3 * rows + 1;
+    Py_ssize_t at = 0, width = 0;
+    offs[0] = 0;
+    for (Py_ssize_t r = 0; r < rows; ++r) {
+      if (!to_i32(ic[r], buf + r) || !to_i32(in[r], buf + rows + r)) goto done;
+      PyObject* h = nullptr;
+      PyObject** ib;
+      Py_ssize_t nb;
+      if (!items_of(il[r], &ib, &nb, &h)) goto done;
+      if (3 * rows + 1 + at + nb > capacity) {
+        Py_DECREF(h);
+        PyErr_SetString(PyExc_ValueError, "pack: staging buffer too small");
+        goto done;
+      }
+      for (Py_ssize_t j = 0; j < nb; ++j)
+        if (!to_i32(ib[j], ids + at + j)) {
+          Py_DECREF(h);
+          goto done;
+        }
+      Py_DECREF(h);
+      at += nb;
+      if (nb > width) width = nb;
+      if (at > INT32_MAX) {
+        PyErr_SetString(PyExc_OverflowError, "pack: more than 2^31 block ids");
+        goto done;
+      }
+      offs[r + 1] = (int32_t)at;
+    }
+    result = Py_BuildValue("(nnn)", rows, at, width);
+  }
+done:
+  Py_XDECREF(hc);
+  Py_XDECREF(hn);
+  Py_XDECREF(hl);
+  return result;
+}
+
+// count_ids(block_lists) -> total number of block ids (sizes the staging buffer before stage_rows fills it).
+PyObject* count_ids(PyObject*, PyObject* lists) {
+  PyObject* h = nullptr;
+  PyObject** il;
+  Py_ssize_t rows;
+  if (!items_of(lists, &il, &rows, &h)) return nullptr;
+  Py_ssize_t total = 0;
+  for (Py_ssize_t r = 0; r < rows; ++r) {
+    const Py_ssize_t n = PyObject_Length(il[r]);
+    if (n < 0) {
+      Py_DECREF(h);
+      return nullptr;
+    }
+    total += n;
+  }
+  Py_DECREF(h);
+  return PyLong_FromSsize_t(total);
+}
+
+PyMethodDef methods[] = {
+    {"stage_rows", stage_rows, METH_VARARGS,
+     "stage_rows(num_cached, num_new, block_lists, address, capacity) -> (rows, n_ids, width)"},
+    {"count_ids", count_ids, METH_O, "count_ids(block_lists) -> total block ids"},
+    {nullptr, nullptr, 0, nullptr}};
+
+PyModuleDef module = {PyModuleDef_HEAD_INIT, "_hoststage", "Host staging of the packing inputs.", -1, methods};
+
+}  // namespace
+
+PyMODINIT_FUNC PyInit__hoststage() { return PyModule_Create(&module); }

@@ -10,6 +10,7 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
@@ -72,7 +73,26 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     os.replace(tmp, LIBRARY)
     if verbose:
         print(f"built {LIBRARY}", flush=True)
+    build_host_stage(verbose)
     return LIBRARY
+
+
+def build_host_stage(verbose: bool = False) -> Path:
+    """Compile the CPython extension that lays the packing inputs out on the host (``lvattn._hoststage``)."""
+    cxx = shutil.which("g++") or shutil.which("c++")
+    if not cxx:
+        raise RuntimeError("g++ not found; lvattn._hoststage needs a host C++ compiler")
+    out = PACKAGE_DIR / ("_hoststage" + sysconfig.get_config_var("EXT_SUFFIX"))
+    tmp = out.with_suffix(".tmp")
+    cmd = [cxx, "-O2", "-std=c++17", "-shared", "-fPIC", f"-I{sysconfig.get_paths()['include']}",
+           str(CSRC / "host_stage.cpp"), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"g++ failed on host_stage.cpp:\n{res.stderr[-4000:]}")
+    os.replace(tmp, out)
+    if verbose:
+        print(f"built {out}", flush=True)
+    return out
 
 
 if __name__ == "__main__":

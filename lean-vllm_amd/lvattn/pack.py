@@ -10,14 +10,22 @@ from the same per-row ints without touching per-token data.
 
 from __future__ import annotations
 
-import itertools
-
 import numpy as np
 import torch
 
 from . import _capi
 
 MIN_CAPACITY = 256
+
+
+def _host_stage():
+    """The host staging extension (built beside liblvattn.so); its absence is an error, as the library's is."""
+    try:
+        from . import _hoststage
+    except ImportError as e:
+        raise RuntimeError("lvattn._hoststage is not built; run __graft_entry__.build() (or python -m lvattn._build)"
+                           ) from e
+    return _hoststage
 
 
 def decode_query_len(lens: np.ndarray, num_speculative_tokens: int = 0) -> int:
@@ -118,17 +126,21 @@ class Packer:
 
     def stage(self, num_cached, num_new, block_lists, num_speculative_tokens: int = 0, is_prompt=None,
               num_logits=None) -> PackPlan:
-        """Copy the per-row inputs to the device (one pinned copy) and derive the host-side row ints."""
-        num_cached = np.asarray(num_cached, dtype=np.int32)
-        num_new = np.asarray(num_new, dtype=np.int32)
-        rows = num_new.size
+        """Copy the per-row inputs to the device (one pinned copy) and derive the host-side row ints.
+
+        The rows' Python ints and block lists are laid out straight into the pinned buffer by ``_hoststage``
+        (num_cached | num_new | block-list offsets | block ids, then the logits-row counts); the row ints the
+        host needs are read back from that buffer as numpy views."""
+        rows = len(num_new)
         if rows == 0:
             raise ValueError("pack: a step needs at least one row")
-        if len(num_cached) != rows or len(block_lists) != rows:
-            raise ValueError("pack: num_cached, num_new and block_lists need one entry per row")
-        lengths = np.fromiter(map(len, block_lists), np.int32, rows)
-        n_ids = int(lengths.sum())
-        width = int(lengths.max())
+        hs = _host_stage()
+        n_ids = hs.count_ids(block_lists)
+        base = 3 * rows + 1 + n_ids
+        buf = self.buffers.host_view("inputs", base + rows, torch.int32)  # room for the logits-row counts
+        _, _, width = hs.stage_rows(num_cached, num_new, block_lists, buf.ctypes.data, base)
+        num_cached, num_new = buf[:rows], buf[rows:2 * rows]
+        lengths = np.diff(buf[2 * rows:3 * rows + 1])
         tokens = int(num_new.sum())
         query_len = decode_query_len(num_new, num_speculative_tokens)
         order = np.argsort(num_new != query_len, kind="stable")
@@ -143,24 +155,14 @@ class Packer:
             cu_seqlens_k_host=[0, *np.cumsum(ends_b).tolist()],
             decode_query_len=query_len,
         )
-        logits, n_log = -1, None
+        logits, size = -1, base
         if host["is_prefill"]:
             n_log = np.ones(rows, np.int32) if num_logits is None else np.asarray(num_logits, dtype=np.int32)
             if n_log.shape != (rows,) or (n_log < 0).any() or (n_log > num_new).any():
                 raise ValueError("pack: num_logits must give 0 .. num_new logits rows per row")
             logits = int(n_log.sum())
-        # One pinned buffer, filled in place: num_cached | num_new | block-list offsets | block ids | logits rows.
-        size = 3 * rows + 1 + n_ids + (rows if n_log is not None else 0)
-        buf = self.buffers.host_view("inputs", size, torch.int32)
-        buf[:rows] = num_cached
-        buf[rows:2 * rows] = num_new
-        buf[2 * rows] = 0
-        np.cumsum(lengths, out=buf[2 * rows + 1:3 * rows + 1])
-        if n_ids:
-            buf[3 * rows + 1:3 * rows + 1 + n_ids] = np.fromiter(itertools.chain.from_iterable(block_lists), np.int32,
-                                                                 n_ids)
-        if n_log is not None:
-            buf[3 * rows + 1 + n_ids:] = n_log
+            buf[base:base + rows] = n_log
+            size = base + rows
         inputs = self.buffers.upload("inputs", size, torch.int32)
         slot_count = int(num_new[lengths > 0].sum())
         return PackPlan(rows, tokens, width, slot_count, query_len, inputs, host, logits)

@@ -127,3 +127,34 @@ def test_the_schedule_choice_matches_a_per_row_count_in_any_row_order():
         flops = sum(4 * 16 * 128 * sum(k - q + j + 1 for j in range(q)) for q, k in zip(lq, lk) if q > 1)
         want = B.SCHEDULE_OVERLAP if dec / B.DECODE_BYTES_PER_S >= flops / B.PROMPT_FLOPS_PER_S else B.SCHEDULE_SERIAL
         assert attn._schedule(Context(cu_seqlens_q_host=cu_q, cu_seqlens_k_host=cu_k), 2) == want
+
+
+def test_host_staging_lays_out_the_rows_as_the_pack_kernel_reads_them():
+    """num_cached | num_new | block-list offsets | block ids, from lists, tuples or numpy rows, as the numpy
+    restatement lays them out; mismatched row counts, a short buffer and ids past int32 are refused."""
+    import numpy as np
+
+    from lvattn import _hoststage
+
+    rng = np.random.default_rng(3)
+    rows = 300
+    cached = rng.integers(0, 5000, rows).tolist()
+    new = rng.integers(1, 4, rows).tolist()
+    lists = [rng.integers(0, 10_000, rng.integers(0, 9)).tolist() for _ in range(rows)]
+    lists[7] = tuple(lists[7])
+    lists[8] = np.asarray(lists[8], dtype=np.int64)
+    n = sum(len(x) for x in lists)
+    assert _hoststage.count_ids(lists) == n
+    buf = np.full(3 * rows + 1 + n + 5, -7, np.int32)
+    got = _hoststage.stage_rows(cached, np.asarray(new), lists, buf.ctypes.data, 3 * rows + 1 + n)
+    assert got == (rows, n, max(len(x) for x in lists))
+    lengths = np.array([len(x) for x in lists])
+    want = np.concatenate([cached, new, [0], np.cumsum(lengths), np.concatenate([np.asarray(x) for x in lists])])
+    assert np.array_equal(buf[:3 * rows + 1 + n], want.astype(np.int32))
+    assert (buf[3 * rows + 1 + n:] == -7).all()  # nothing written past the capacity given
+    with pytest.raises(ValueError, match="one entry per row"):
+        _hoststage.stage_rows(cached[:-1], new, lists, buf.ctypes.data, buf.size)
+    with pytest.raises(ValueError, match="too small"):
+        _hoststage.stage_rows(cached, new, lists, buf.ctypes.data, 3 * rows + n)
+    with pytest.raises(OverflowError):
+        _hoststage.stage_rows([0], [1], [[2 ** 31]], buf.ctypes.data, buf.size)
