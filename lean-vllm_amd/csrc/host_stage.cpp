@@ -95,6 +95,70 @@ done:
   return result;
 }
 
+// stage_graph_rows(num_cached, block_lists, address, capacity, bs, q) -> (rows, n_ids, width)
+// The layout a captured step of `bs` rows reads: the `rows` real rows first, then padding rows with num_cached -q
+// (context length 0), no blocks; every row has num_new q.
+//   num_cached[bs] | num_new[bs] | block-list offsets[bs + 1] | block ids[n_ids]
+PyObject* stage_graph_rows(PyObject*, PyObject* args) {
+  PyObject *cached, *lists;
+  unsigned long long address;
+  Py_ssize_t capacity, bs;
+  int q;
+  if (!PyArg_ParseTuple(args, "OOKnni", &cached, &lists, &address, &capacity, &bs, &q)) return nullptr;
+  PyObject *hc = nullptr, *hl = nullptr;
+  PyObject **ic, **il;
+  Py_ssize_t rows, rl;
+  PyObject* result = nullptr;
+  int32_t* buf = reinterpret_cast<int32_t*>(static_cast<uintptr_t>(address));
+  if (!items_of(cached, &ic, &rows, &hc) || !items_of(lists, &il, &rl, &hl)) goto done;
+  if (rl != rows || rows > bs) {
+    PyErr_SetString(PyExc_ValueError, "graph staging: one block list per row, at most bs rows");
+    goto done;
+  }
+  if (3 * bs + 1 > capacity) {
+    PyErr_SetString(PyExc_ValueError, "graph staging: buffer too small");
+    goto done;
+  }
+  {
+    int32_t* offs = buf + 2 * bs;
+    int32_t* ids = buf + 3 * bs + 1;
+    Py_ssize_t at = 0, width = 0;
+    offs[0] = 0;
+    for (Py_ssize_t r = 0; r < bs; ++r) {
+      buf[bs + r] = q;
+      if (r >= rows) {  // padding row
+        buf[r] = -q;
+        offs[r + 1] = (int32_t)at;
+        continue;
+      }
+      if (!to_i32(ic[r], buf + r)) goto done;
+      PyObject* h = nullptr;
+      PyObject** ib;
+      Py_ssize_t nb;
+      if (!items_of(il[r], &ib, &nb, &h)) goto done;
+      if (3 * bs + 1 + at + nb > capacity) {
+        Py_DECREF(h);
+        PyErr_SetString(PyExc_ValueError, "graph staging: buffer too small");
+        goto done;
+      }
+      for (Py_ssize_t j = 0; j < nb; ++j)
+        if (!to_i32(ib[j], ids + at + j)) {
+          Py_DECREF(h);
+          goto done;
+        }
+      Py_DECREF(h);
+      at += nb;
+      if (nb > width) width = nb;
+      offs[r + 1] = (int32_t)at;
+    }
+    result = Py_BuildValue("(nnn)", rows, at, width);
+  }
+done:
+  Py_XDECREF(hc);
+  Py_XDECREF(hl);
+  return result;
+}
+
 // count_ids(block_lists) -> total number of block ids (sizes the staging buffer before stage_rows fills it).
 PyObject* count_ids(PyObject*, PyObject* lists) {
   PyObject* h = nullptr;
@@ -117,6 +181,8 @@ PyObject* count_ids(PyObject*, PyObject* lists) {
 PyMethodDef methods[] = {
     {"stage_rows", stage_rows, METH_VARARGS,
      "stage_rows(num_cached, num_new, block_lists, address, capacity) -> (rows, n_ids, width)"},
+    {"stage_graph_rows", stage_graph_rows, METH_VARARGS,
+     "stage_graph_rows(num_cached, block_lists, address, capacity, bs, q) -> (rows, n_ids, width)"},
     {"count_ids", count_ids, METH_O, "count_ids(block_lists) -> total block ids"},
     {nullptr, nullptr, 0, nullptr}};
 

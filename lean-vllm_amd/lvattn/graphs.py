@@ -12,7 +12,6 @@ on the device from the lengths in the graph, so nothing has to be refreshed befo
 
 from __future__ import annotations
 
-import itertools
 
 import numpy as np
 import torch
@@ -20,6 +19,7 @@ import torch
 from . import _capi
 from .backend import MI355XAttention
 from .context import Context
+from .pack import _host_stage
 
 LV_PACK_DENSE_SLOTS = 1
 
@@ -65,24 +65,15 @@ class DecodeGraphs:
             self._copied.synchronize()
         rows = len(num_cached)
         q = self.query_len
-        cached = np.full(bs, -q, dtype=np.int32)
-        cached[:rows] = num_cached
-        lengths = np.zeros(bs, dtype=np.int32)
-        lengths[:rows] = np.fromiter(map(len, block_lists), np.int32, rows)
-        if (lengths > self.max_blocks).any():
-            raise ValueError(f"a block list is longer than the {self.max_blocks} blocks the graphs were sized for")
-        need = -(-(cached[:rows] + q) // self.block_size)
-        if rows and (lengths[:rows] < need).any():
-            raise ValueError("a row's block list does not cover its context")
         host = self._host.numpy()
-        host[:bs] = cached
-        host[bs:2 * bs] = q
-        indptr = host[2 * bs:3 * bs + 1]
-        indptr[0] = 0
-        np.cumsum(lengths, out=indptr[1:])
-        at = int(indptr[-1])
-        if at:
-            host[3 * bs + 1:3 * bs + 1 + at] = np.fromiter(itertools.chain.from_iterable(block_lists), np.int32, at)
+        # Real rows, then padding rows (num_cached -q: context length 0, no blocks), straight from the Python lists.
+        _, at, width = _host_stage().stage_graph_rows(num_cached, block_lists, host.ctypes.data, host.size, bs, q)
+        if width > self.max_blocks:
+            raise ValueError(f"a block list is longer than the {self.max_blocks} blocks the graphs were sized for")
+        lengths = np.diff(host[2 * bs:2 * bs + rows + 1])
+        need = -(-(host[:rows] + q) // self.block_size)
+        if rows and (lengths < need).any():
+            raise ValueError("a row's block list does not cover its context")
         n = 3 * bs + 1 + at
         self._inputs[:n].copy_(self._host[:n], non_blocking=True)
         self._copied = torch.cuda.Event()

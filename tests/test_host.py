@@ -158,3 +158,23 @@ def test_host_staging_lays_out_the_rows_as_the_pack_kernel_reads_them():
         _hoststage.stage_rows(cached, new, lists, buf.ctypes.data, 3 * rows + n)
     with pytest.raises(OverflowError):
         _hoststage.stage_rows([0], [1], [[2 ** 31]], buf.ctypes.data, buf.size)
+
+
+def test_graph_staging_pads_rows_with_no_context():
+    """A captured step of bs rows: real rows first, then padding rows with num_cached -q (context length 0) and no
+    blocks; every row has q new tokens."""
+    import numpy as np
+
+    from lvattn import _hoststage
+
+    bs, q = 8, 3
+    cached, lists = [4, 0, 9], [[5, 6], [7], [1, 2, 3]]
+    buf = np.full(3 * bs + 1 + 6 + 2, -9, np.int32)
+    assert _hoststage.stage_graph_rows(cached, lists, buf.ctypes.data, 3 * bs + 1 + 6, bs, q) == (3, 6, 3)
+    assert buf[:bs].tolist() == [4, 0, 9] + [-q] * 5
+    assert buf[bs:2 * bs].tolist() == [q] * bs
+    assert buf[2 * bs:3 * bs + 1].tolist() == [0, 2, 3, 6, 6, 6, 6, 6, 6]
+    assert buf[3 * bs + 1:3 * bs + 7].tolist() == [5, 6, 7, 1, 2, 3]
+    assert (buf[3 * bs + 7:] == -9).all()
+    with pytest.raises(ValueError, match="at most bs rows"):
+        _hoststage.stage_graph_rows([0] * 9, [[]] * 9, buf.ctypes.data, buf.size, bs, q)
