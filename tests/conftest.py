@@ -32,7 +32,8 @@ def gpu_ready() -> bool:
 
 @pytest.fixture(scope="session")
 def cuda():
-    """The GPU device; fails (not skips) on a machine with a GPU whose library is missing, so nothing passes silently."""
+    """The GPU device; fails (not skips) on a machine with a GPU whose library is missing, so nothing passes
+    silently."""
     import torch
 
     if not torch.cuda.is_available():
