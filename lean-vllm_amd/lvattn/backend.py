@@ -56,10 +56,13 @@ _WORKSPACE = _Workspace()
 
 # Launch schedules of a step with prompt rows (LV_SCHEDULE_* of lvattn.h).
 SCHEDULE_AUTO, SCHEDULE_SERIAL, SCHEDULE_OVERLAP = 0, 1, 2
-# Measured MI355X rates the schedule choice compares: decode rows stream their KV bytes at about 6.3 TB/s; prompt
-# tiles on the whole GPU run about 0.56 PFLOP/s (bf16, head_dim 128).
-DECODE_BYTES_PER_S = 6.3e12
-PROMPT_FLOPS_PER_S = 5.6e14
+# Measured MI355X rates the schedule choice compares (bf16, head_dim 128). Overlapped, the prompt tiles run at
+# about 0.18 PFLOP/s (one workgroup on half the CUs, beside the decode rows) against 0.84 PFLOP/s alone on the whole
+# GPU, and the decode rows stream about 6.6 TB/s. Overlap wins while the prompt tiles' extra time beside the decode
+# rows, flops x (1/0.18 - 1/0.84 per PFLOP/s), fits in the decode rows' own time: steps of 2048 decode rows with 2
+# to 8 prompt chunks of 1536 tokens ran 6-9% faster overlapped, with 12 and 16 chunks 35% and 65% slower.
+DECODE_BYTES_PER_S = 6.6e12
+PROMPT_FLOPS_PER_S = 1 / (1 / 1.8e14 - 1 / 8.4e14)  # 2.3e14
 
 
 class MI355XAttention(AttentionBackend):

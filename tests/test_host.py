@@ -96,7 +96,16 @@ def test_prompt_tiles_overlap_decode_rows_only_when_the_decode_bytes_cover_them(
     cu_q = [0, *torch.tensor(new).cumsum(0).tolist()]
     cu_k = [0, *torch.tensor(ends).cumsum(0).tolist()]
     ctx = Context(cu_seqlens_q_host=cu_q, cu_seqlens_k_host=cu_k)
-    assert attn._schedule(ctx, 2) == B.SCHEDULE_OVERLAP  # 18.7 GB of decode rows hide 387 GFLOP of prompt tiles
+    assert attn._schedule(ctx, 2) == B.SCHEDULE_OVERLAP  # 18.7 GB of decode rows hide 428 GFLOP of prompt tiles
+    # The same decode rows beside 6 and 12 prompt chunks of 1536 tokens on 3000-token prefixes (569 and 1138
+    # GFLOP): overlapped, the first still wins; the second ran 35% slower overlapped than serially.
+    dec_new, dec_ends = [n for n in new if n == 1], [e for n, e in zip(new, ends) if n == 1]
+    for chunks, want in ((6, B.SCHEDULE_OVERLAP), (12, B.SCHEDULE_SERIAL)):
+        q = dec_new + [1536] * chunks
+        k = dec_ends + [3000 + 1536] * chunks
+        step = Context(cu_seqlens_q_host=[0, *torch.tensor(q).cumsum(0).tolist()],
+                       cu_seqlens_k_host=[0, *torch.tensor(k).cumsum(0).tolist()])
+        assert attn._schedule(step, 2) == want, chunks
     assert ctx.attn_metadata  # cached on the step's context
     prompts = Context(cu_seqlens_q_host=[0, 1536, 3072], cu_seqlens_k_host=[0, 2000, 5000])
     assert attn._schedule(prompts, 2) == B.SCHEDULE_SERIAL  # no decode rows: the prompt tiles take the whole GPU
