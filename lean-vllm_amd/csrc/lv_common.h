@@ -217,14 +217,18 @@ __device__ inline float xor32_sum(float x) {
 }
 // IEEE: vmax (NaN-propagating), else fmaxf.
 template <bool IEEE = true>
+__device__ __forceinline__ float max2(float a, float b) {
+  return IEEE ? vmax(a, b) : fmaxf(a, b);
+}
+template <bool IEEE = true>
 __device__ inline float xor16_max(float x) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return IEEE ? vmax(__uint_as_float(r[0]), __uint_as_float(r[1])) : fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return max2<IEEE>(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 template <bool IEEE = true>
 __device__ inline float xor32_max(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return IEEE ? vmax(__uint_as_float(r[0]), __uint_as_float(r[1])) : fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return max2<IEEE>(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 // Inclusive prefix sum over the 64 lanes of a wave.
 __device__ inline int wave_incl_scan(int x) {
@@ -238,7 +242,7 @@ __device__ inline int wave_incl_scan(int x) {
 }
 
 // Exclusive prefix sum of a[0, n) in LDS, in place, by a block of kScanThreads threads; a[n] receives the total.
-// wave_tot holds kScanThreads / 64 + 1 ints of LDS. Every thread of the block must call it. Each thread scans its
+// wave_tot holds kScanThreads / 64 ints of LDS. Every thread of the block must call it. Each thread scans its
 // chunk, each wave its threads' chunk totals; every thread then sums the wave totals before its own (16 broadcast
 // LDS reads, issued together) instead of one thread scanning them in sequence between two more barriers.
 constexpr int kScanThreads = 1024;

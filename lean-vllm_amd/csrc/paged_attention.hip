@@ -64,7 +64,7 @@ constexpr int kPlanMaxRows = 4096;  // rows of a step with prompts (the work-lis
 template <int LPT, bool IEEE>
 __device__ inline float groups_max(float x) {
   static_assert(LPT == 8 || LPT == 16, "8 or 16 lanes per token");
-  if constexpr (LPT == 8) x = IEEE ? vmax(x, dpp_ror8(x)) : fmaxf(x, dpp_ror8(x));  // lanes i, i ^ 8 of a row
+  if constexpr (LPT == 8) x = max2<IEEE>(x, dpp_ror8(x));  // lanes i and i ^ 8 of each 16-lane row
   return xor32_max<IEEE>(xor16_max<IEEE>(x));
 }
 template <int LPT>
@@ -165,14 +165,14 @@ __device__ void decode_item(const AttnParams& p, int row, int split, int kvh, in
     for (int g = 0; g < GS; ++g) {
       float x = s[0][g];
 #pragma unroll
-      for (int u = 1; u < U; ++u) x = BESIDE ? vmax(x, s[u][g]) : fmaxf(x, s[u][g]);
+      for (int u = 1; u < U; ++u) x = max2<BESIDE>(x, s[u][g]);
       mt[g] = groups_max<LPT, BESIDE>(x);  // finite: every tile holds a token in range
       grow |= mt[g] > m[g];
     }
     if (__builtin_amdgcn_readfirstlane(grow)) {
 #pragma unroll
       for (int g = 0; g < GS; ++g) {
-        const float mn = BESIDE ? vmax(m[g], mt[g]) : fmaxf(m[g], mt[g]);
+        const float mn = max2<BESIDE>(m[g], mt[g]);
         const float alpha = fast_exp2((m[g] - mn) * c);
         m[g] = mn;
         l[g] *= alpha;
