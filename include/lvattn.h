@@ -29,7 +29,7 @@ extern "C" {
 #define LV_SCHEDULE_SERIAL 1
 #define LV_SCHEDULE_OVERLAP 2
 
-#define LV_ABI_VERSION 4
+#define LV_ABI_VERSION 5
 
 /* The last error message of the calling thread ("" if none). */
 const char* lv_last_error(void);
@@ -107,7 +107,10 @@ int lv_store_latents(const void* latent, int64_t latent_stride_t, int32_t num_to
  * decode rows' streaming (a second stream, joined back into `stream` by events); LV_SCHEDULE_SERIAL runs the
  * prompt tiles on the whole GPU, then the decode rows -- the faster choice when the decode rows' bytes take less
  * time than the prompt tiles' MFMA work (e.g. a step of prompts only). LV_SCHEDULE_AUTO overlaps. The result is
- * the same either way. */
+ * the same either way.
+ * prompt_workgroups (overlap only): how many CUs run a prompt workgroup beside the decode rows; 0 picks half of
+ * them. Other values are clamped to [half, three quarters] of the CUs and rounded down to a multiple of 8 (each
+ * kv head's prompt items then stay on one XCD). A step heavy in prompt tiles ends sooner with more. */
 size_t lv_paged_attention_workspace_bytes(int32_t num_rows, int32_t num_tokens, int32_t num_heads,
                                           int32_t num_kv_heads, int32_t head_dim, int32_t max_seqlen_k,
                                           int32_t decode_only);
@@ -118,7 +121,8 @@ int lv_paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h, co
                        const int32_t* cu_seqlens_k, int32_t num_rows, int32_t num_tokens, int32_t num_heads,
                        int32_t num_kv_heads, int32_t head_dim, float scale, int32_t max_seqlen_q,
                        int32_t max_seqlen_k, void* out, int64_t out_stride_t, int64_t out_stride_h,
-                       void* workspace, size_t workspace_bytes, int32_t schedule, int32_t dtype, void* stream);
+                       void* workspace, size_t workspace_bytes, int32_t schedule, int32_t prompt_workgroups,
+                       int32_t dtype, void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------
  * Attention over packed keys (no pages). Replaces AttentionBackend.prefill without block tables and

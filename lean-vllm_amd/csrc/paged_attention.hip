@@ -36,7 +36,10 @@ constexpr int kPlanMaxRows = 4096;  // rows of a step with prompts (the work-lis
 #define LV_OVERLAP 1
 #endif
 #ifndef LV_OVERLAP_CUS
-#define LV_OVERLAP_CUS 50  // percent of the CUs that hold a prompt workgroup in a mixed step (swept: 50-100)
+#define LV_OVERLAP_CUS 50  // percent of the CUs that hold a prompt workgroup in a mixed step by default (swept)
+#endif
+#ifndef LV_OVERLAP_CUS_MAX
+#define LV_OVERLAP_CUS_MAX 75  // at most this percent when the caller sizes the prompt share
 #endif
 #ifndef LV_DECODE_WGS
 #define LV_DECODE_WGS 2  // persistent decode workgroups per CU outside the overlap (0: one workgroup per item)
@@ -663,8 +666,17 @@ static void launch_decode(const AttnParams& p, const Shape& s, int per_cu, hipSt
   }
 }
 
+// CUs that hold a prompt workgroup in an overlapped step: the caller's count clamped to [default, max] and
+// rounded down to a multiple of 8, or the default share for 0; never more than there are prompt items.
+static int prompt_grid(const Shape& s, const AttnParams& p, int requested) {
+  const int cus = device_cus();
+  const int lo = std::max(8, cus * LV_OVERLAP_CUS / 100 / 8 * 8), hi = std::max(lo, cus * LV_OVERLAP_CUS_MAX / 100);
+  const int n = requested > 0 ? std::min(hi, std::max(lo, requested / 8 * 8)) : lo;
+  return std::min(s.max_prompt_items * p.hkv, n);
+}
+
 template <typename T, int D, int GS>
-static void launch(const AttnParams& p, bool listed, bool mixed, bool overlap, const Shape& s,
+static void launch(const AttnParams& p, bool listed, bool mixed, bool overlap, int prompt_wgs, const Shape& s,
                    hipStream_t stream) {
   const int ny = p.hkv * p.qgroups;
   const bool ring = LV_PROMPT_RING > 0 && p.bs.d % kPrefillKeys == 0;  // every 64-key tile in one page
@@ -672,7 +684,7 @@ static void launch(const AttnParams& p, bool listed, bool mixed, bool overlap, c
   if (side) {
     // Decode items go to the second stream first, then the prompt items to the caller's stream: the prompt
     // workgroups (one per CU) are dispatched as soon as the plan ends, the decode workgroups fill the rest.
-    const int grid = std::min(s.max_prompt_items * p.hkv, std::max(1, device_cus() * LV_OVERLAP_CUS / 100));
+    const int grid = prompt_grid(s, p, prompt_wgs);
     std::lock_guard<std::mutex> g(side->lock);
     hipEventRecord(side->fork, stream);
     hipStreamWaitEvent(side->stream, side->fork, 0);
@@ -703,19 +715,19 @@ static void launch(const AttnParams& p, bool listed, bool mixed, bool overlap, c
 }
 
 template <typename T, int D>
-static void launch_gs(const AttnParams& p, int gs, bool listed, bool mixed, bool overlap, const Shape& s,
-                      hipStream_t stream) {
-  if (gs == 4) launch<T, D, 4>(p, listed, mixed, overlap, s, stream);
-  else if (gs == 2) launch<T, D, 2>(p, listed, mixed, overlap, s, stream);
-  else launch<T, D, 1>(p, listed, mixed, overlap, s, stream);
+static void launch_gs(const AttnParams& p, int gs, bool listed, bool mixed, bool overlap, int prompt_wgs,
+                      const Shape& s, hipStream_t stream) {
+  if (gs == 4) launch<T, D, 4>(p, listed, mixed, overlap, prompt_wgs, s, stream);
+  else if (gs == 2) launch<T, D, 2>(p, listed, mixed, overlap, prompt_wgs, s, stream);
+  else launch<T, D, 1>(p, listed, mixed, overlap, prompt_wgs, s, stream);
 }
 
 template <typename T>
-static int launch_d(const AttnParams& p, int d, int gs, bool listed, bool mixed, bool overlap, const Shape& s,
-                    hipStream_t stream) {
+static int launch_d(const AttnParams& p, int d, int gs, bool listed, bool mixed, bool overlap, int prompt_wgs,
+                    const Shape& s, hipStream_t stream) {
   switch (d) {
-    case 64: launch_gs<T, 64>(p, gs, listed, mixed, overlap, s, stream); return LV_OK;
-    case 128: launch_gs<T, 128>(p, gs, listed, mixed, overlap, s, stream); return LV_OK;
+    case 64: launch_gs<T, 64>(p, gs, listed, mixed, overlap, prompt_wgs, s, stream); return LV_OK;
+    case 128: launch_gs<T, 128>(p, gs, listed, mixed, overlap, prompt_wgs, s, stream); return LV_OK;
     default: set_error("paged_attention: head_dim %d is not 64 or 128", d); return LV_EINVAL;
   }
 }
@@ -741,12 +753,13 @@ extern "C" int lv_paged_attention(const void* q, int64_t q_stride_t, int64_t q_s
                                   int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float scale,
                                   int32_t max_seqlen_q, int32_t max_seqlen_k, void* out, int64_t out_stride_t,
                                   int64_t out_stride_h, void* workspace, size_t workspace_bytes, int32_t schedule,
-                                  int32_t dtype, void* stream) {
+                                  int32_t prompt_workgroups, int32_t dtype, void* stream) {
   LV_REQUIRE(dtype == LV_DTYPE_BF16 || dtype == LV_DTYPE_F16, "paged_attention: dtype %d is not bf16 or fp16",
              dtype);
   LV_REQUIRE(num_rows >= 0 && num_tokens >= 0, "paged_attention: negative row or token count");
   LV_REQUIRE(schedule == LV_SCHEDULE_AUTO || schedule == LV_SCHEDULE_SERIAL || schedule == LV_SCHEDULE_OVERLAP,
              "paged_attention: unknown schedule %d", schedule);
+  LV_REQUIRE(prompt_workgroups >= 0, "paged_attention: negative prompt_workgroups %d", prompt_workgroups);
   if (num_rows == 0 || num_tokens == 0) return LV_OK;
   LV_REQUIRE(num_heads > 0 && num_kv_heads > 0 && num_heads % num_kv_heads == 0,
              "paged_attention: %d query heads do not group over %d key heads", num_heads, num_kv_heads);
@@ -825,8 +838,9 @@ extern "C" int lv_paged_attention(const void* q, int64_t q_stride_t, int64_t q_s
     LV_LAUNCH_CHECK("plan_kernel");
   }
   const bool overlap = schedule != LV_SCHEDULE_SERIAL;
-  const int rc = dtype == LV_DTYPE_BF16 ? launch_d<BF16>(p, head_dim, s.gs, listed, mixed, overlap, s, st)
-                                        : launch_d<F16>(p, head_dim, s.gs, listed, mixed, overlap, s, st);
+  const int rc =
+      dtype == LV_DTYPE_BF16 ? launch_d<BF16>(p, head_dim, s.gs, listed, mixed, overlap, prompt_workgroups, s, st)
+                             : launch_d<F16>(p, head_dim, s.gs, listed, mixed, overlap, prompt_workgroups, s, st);
   if (rc != LV_OK) return rc;
   LV_LAUNCH_CHECK("paged_attention_kernel");
   return LV_OK;

@@ -63,6 +63,10 @@ SCHEDULE_AUTO, SCHEDULE_SERIAL, SCHEDULE_OVERLAP = 0, 1, 2
 # to 8 prompt chunks of 1536 tokens ran 6-9% faster overlapped, with 12 and 16 chunks 35% and 65% slower.
 DECODE_BYTES_PER_S = 6.6e12
 PROMPT_FLOPS_PER_S = 1 / (1 / 1.8e14 - 1 / 8.4e14)  # 2.3e14
+# One overlapped prompt workgroup (one per CU) runs about 1.3-1.4 TFLOP/s of prompt tiles beside the decode rows. An
+# overlapped step asks for enough of them that the prompt tiles end with the decode rows; the library keeps the
+# count between half and three quarters of the CUs.
+PROMPT_WORKGROUP_FLOPS_PER_S = 1.3e12
 
 
 class MI355XAttention(AttentionBackend):
@@ -139,7 +143,7 @@ class MI355XAttention(AttentionBackend):
 
     # -- attention -----------------------------------------------------------------------------------------
     def _attend(self, q, k_cache, v_cache, out, *, block_tables, cu_seqlens_q, seqlens_k, cu_seqlens_k, rows,
-                max_seqlen_q, max_seqlen_k, schedule=SCHEDULE_AUTO):
+                max_seqlen_q, max_seqlen_k, schedule=SCHEDULE_AUTO, prompt_workgroups=0):
         assert q.dtype in _capi.DTYPES and k_cache.dtype == q.dtype == v_cache.dtype
         assert q.stride(-1) == 1 and k_cache.stride() == v_cache.stride() and k_cache.stride(-1) == 1
         assert block_tables is not None and block_tables.dtype == torch.int32 and block_tables.stride(-1) == 1
@@ -157,7 +161,7 @@ class MI355XAttention(AttentionBackend):
                    _capi.ptr(cu_seqlens_q), _capi.ptr(seqlens_k), _capi.ptr(cu_seqlens_k), rows, tokens, heads,
                    self.num_kv_heads, dim, float(self.scale), max_seqlen_q, max_seqlen_k, out.data_ptr(),
                    out.stride(0), out.stride(1), _capi.ptr(ws), 0 if ws is None else ws.numel(), schedule,
-                   _capi.DTYPES[q.dtype], _capi.stream_of(q.device))
+                   prompt_workgroups, _capi.DTYPES[q.dtype], _capi.stream_of(q.device))
         return out
 
     def _schedule(self, context: Context, elem_bytes: int) -> int:
@@ -193,7 +197,15 @@ class MI355XAttention(AttentionBackend):
             prompt_flops = 4 * self.num_heads * self.head_dim * pairs
             overlap = decode_bytes / DECODE_BYTES_PER_S >= prompt_flops / PROMPT_FLOPS_PER_S
             cache[key] = SCHEDULE_OVERLAP if overlap else SCHEDULE_SERIAL
+            decode_s = decode_bytes / DECODE_BYTES_PER_S
+            cache[key + ("workgroups",)] = int(prompt_flops / PROMPT_WORKGROUP_FLOPS_PER_S / decode_s) if overlap else 0
         return cache[key]
+
+    def _prompt_workgroups(self, context: Context, elem_bytes: int) -> int:
+        """CUs that hold a prompt workgroup in this step's overlap, as ``_schedule`` sized them (0: the library's
+        default, half of them)."""
+        cache = context.attn_metadata or {}
+        return cache.get(("schedule", self.num_heads, self.num_kv_heads, self.head_dim, elem_bytes, "workgroups"), 0)
 
     def decode(self, q, k_cache, v_cache, context: Context, out=None):
         """One query per row against its ``context_lens[b]`` cached keys; q ``[B, Hq, D]``."""
@@ -220,7 +232,8 @@ class MI355XAttention(AttentionBackend):
         return self._attend(q, k_cache, v_cache, out, block_tables=bt, cu_seqlens_q=cu_q.to(torch.int32),
                             seqlens_k=None, cu_seqlens_k=cu_k.to(torch.int32), rows=cu_q.numel() - 1,
                             max_seqlen_q=max_q, max_seqlen_k=max_k,
-                            schedule=self._schedule(context, q.element_size()))
+                            schedule=self._schedule(context, q.element_size()),
+                            prompt_workgroups=self._prompt_workgroups(context, q.element_size()))
 
     def mla_decode(self, q, latent_cache, v_dim, context: Context, out=None):
         """Each row's last ``Lq`` queries against its paged latents, read as one key head shared by every query

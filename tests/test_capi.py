@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
     lib = _capi.load()
     missing = [n for n in declared() if not hasattr(lib, n)]
     assert not missing, f"declared in lvattn.h but not exported: {missing}"
-    assert lib.lv_abi_version() == 4
+    assert lib.lv_abi_version() == 5
     assert all(n in _capi._PROTOTYPES for n in declared()), "every declared function has a ctypes prototype"
 
 
@@ -40,13 +40,16 @@ def test_bad_arguments_raise_with_the_library_message():
         _capi.call("lv_store_kvcache", None, None, 0, 0, 1, 1, 8, None, None, 0, 0, 0, 0, None, 2, None)
     with pytest.raises(_capi.LvError, match="head_dim 96"):
         _capi.call("lv_paged_attention", 1, 0, 0, 1, 1, 0, 0, 0, 16, 1, 0, None, 1, None, 1, 1, 8, 2, 96, 1.0, 1, 16,
-                   1, 0, 0, None, 0, 0, 0, None)
+                   1, 0, 0, None, 0, 0, 0, 0, None)
     with pytest.raises(_capi.LvError, match="not bf16 or fp16"):
         _capi.call("lv_paged_attention", 1, 0, 0, 1, 1, 0, 0, 0, 16, 1, 0, None, 1, None, 1, 1, 8, 2, 64, 1.0, 1, 16,
-                   1, 0, 0, None, 0, 0, 7, None)
+                   1, 0, 0, None, 0, 0, 0, 7, None)
     with pytest.raises(_capi.LvError, match="unknown schedule 5"):
         _capi.call("lv_paged_attention", 1, 0, 0, 1, 1, 0, 0, 0, 16, 1, 0, None, 1, None, 1, 1, 8, 2, 64, 1.0, 1, 16,
-                   1, 0, 0, None, 0, 5, 0, None)
+                   1, 0, 0, None, 0, 5, 0, 0, None)
+    with pytest.raises(_capi.LvError, match="negative prompt_workgroups"):
+        _capi.call("lv_paged_attention", 1, 0, 0, 1, 1, 0, 0, 0, 16, 1, 0, None, 1, None, 1, 1, 8, 2, 64, 1.0, 1, 16,
+                   1, 0, 0, None, 0, 2, -1, 0, None)
 
 
 def test_workspace_query_sizes():

@@ -103,14 +103,18 @@ def test_both_launch_schedules_give_the_same_step(case, bs, poison, monkeypatch)
     b.store_kvcache(kn, vn, kc, vc, slots)
     want = dense_expected(qs, kf, vf, SCALE)
     outs = {}
-    for sched in (B.SCHEDULE_SERIAL, B.SCHEDULE_OVERLAP):
+    # serial; overlapped on the default share of the CUs; overlapped on as many as the library allows
+    for name, sched, wgs in (("serial", B.SCHEDULE_SERIAL, 0), ("overlap", B.SCHEDULE_OVERLAP, 0),
+                             ("overlap-wide", B.SCHEDULE_OVERLAP, 10_000)):
         monkeypatch.setattr(b, "_schedule", lambda context, elem_bytes, s=sched: s)
+        monkeypatch.setattr(b, "_prompt_workgroups", lambda context, elem_bytes, n=wgs: n)
         out = b.forward(torch.cat(qs), kn, vn, kc, vc, context_for(cached, new, tables, dev))
         torch.cuda.synchronize()
         assert torch.isfinite(out).all()
         check(out, want, dtype)
-        outs[sched] = out
-    assert torch.equal(outs[B.SCHEDULE_SERIAL], outs[B.SCHEDULE_OVERLAP])
+        outs[name] = out
+    assert torch.equal(outs["serial"], outs["overlap"])
+    assert torch.equal(outs["serial"], outs["overlap-wide"])
 
 
 def test_decode(case):

@@ -106,6 +106,8 @@ def test_prompt_tiles_overlap_decode_rows_only_when_the_decode_bytes_cover_them(
         step = Context(cu_seqlens_q_host=[0, *torch.tensor(q).cumsum(0).tolist()],
                        cu_seqlens_k_host=[0, *torch.tensor(k).cumsum(0).tolist()])
         assert attn._schedule(step, 2) == want, chunks
+        if want == B.SCHEDULE_OVERLAP:  # more prompt work than the mixed step: more than half the CUs asked for
+            assert attn._prompt_workgroups(step, 2) > attn._prompt_workgroups(ctx, 2) > 100
     assert ctx.attn_metadata  # cached on the step's context
     prompts = Context(cu_seqlens_q_host=[0, 1536, 3072], cu_seqlens_k_host=[0, 2000, 5000])
     assert attn._schedule(prompts, 2) == B.SCHEDULE_SERIAL  # no decode rows: the prompt tiles take the whole GPU
