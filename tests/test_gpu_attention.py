@@ -370,3 +370,44 @@ def test_a_mixed_step_of_many_decode_rows_under_both_schedules(cuda, monkeypatch
         torch.testing.assert_close(out.float().cpu(), want, atol=2e-2, rtol=1e-2)
         outs[sched] = out
     assert torch.equal(outs[B.SCHEDULE_SERIAL], outs[B.SCHEDULE_OVERLAP])
+
+
+@pytest.mark.parametrize("name", ["qwen3_8b_mixed", "qwen3_8b_decode", "qwen3_8b_long"])
+def test_full_size_steps_on_sampled_rows(cuda, name):
+    """The measured steps at full size (pack, store, attention as the bench runs them): sampled rows against the
+    fp32 oracle on each row's gathered keys -- the shortest, a middle and the longest decode rows, and the first,
+    middle and last queries of every prompt chunk (each query sees its row's keys up to its own position)."""
+    from lvattn import Packer
+    from lvattn import workloads as W
+
+    wl = W.WORKLOADS[name]()
+    t = W.materialize(wl, cuda)
+    b = MI355XAttention(wl.num_heads, wl.head_dim, wl.scale, wl.num_kv_heads)
+    _, fields = Packer(cuda, wl.block_size).pack(wl.num_cached, wl.num_new, wl.block_lists)
+    order = fields.pop("order").cpu().tolist()
+    b.store_kvcache(t.k_new, t.v_new, t.k_cache, t.v_cache, fields["slot_mapping"])
+    ctx = Context(**{k: v for k, v in fields.items() if k in Context.__slots__})
+    out = b.forward(t.q, t.k_new, t.v_new, t.k_cache, t.v_cache, ctx)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    cu_q = fields["cu_seqlens_q"].cpu().tolist()
+    decode = [i for i in range(len(order)) if wl.num_new[order[i]] == 1]
+    by_len = sorted(decode, key=lambda i: wl.num_cached[order[i]])
+    picks = [(i, 0) for i in sorted({by_len[0], by_len[len(by_len) // 2], by_len[-1]})]
+    for i in range(len(order)):
+        lq = wl.num_new[order[i]]
+        if lq > 1:
+            picks += [(i, j) for j in (0, lq // 2, lq - 1)]
+    bs = wl.block_size
+    for i, j in picks:
+        s = order[i]
+        lq, lk = wl.num_new[s], wl.num_cached[s] + wl.num_new[s]
+        n = lk - lq + j + 1  # keys query j of the row sees
+        pos = torch.arange(n, device=cuda)
+        pages = torch.tensor(wl.block_lists[s], dtype=torch.long, device=cuda)[pos // bs]
+        k = t.k_cache[pages, pos % bs].cpu().float()
+        v = t.v_cache[pages, pos % bs].cpu().float()
+        q = t.q[cu_q[i] + j:cu_q[i] + j + 1].cpu().float()
+        want = A.dense_attention(q, k, v, wl.scale, causal=False)
+        got = out[cu_q[i] + j:cu_q[i] + j + 1].float().cpu()
+        torch.testing.assert_close(got, want, **TOL[torch.bfloat16], msg=lambda m: f"{name} row {i} query {j}: {m}")
