@@ -372,7 +372,8 @@ def test_a_mixed_step_of_many_decode_rows_under_both_schedules(cuda, monkeypatch
     assert torch.equal(outs[B.SCHEDULE_SERIAL], outs[B.SCHEDULE_OVERLAP])
 
 
-@pytest.mark.parametrize("name", ["qwen3_8b_mixed", "qwen3_8b_decode", "qwen3_8b_long"])
+@pytest.mark.parametrize("name", ["qwen3_8b_mixed", "qwen3_8b_decode", "qwen3_8b_long", "qwen3_8b_prefill",
+                                  "qwen3_0_6b_mixed"])
 def test_full_size_steps_on_sampled_rows(cuda, name):
     """The measured steps at full size (pack, store, attention as the bench runs them): sampled rows against the
     fp32 oracle on each row's gathered keys -- the shortest, a middle and the longest decode rows, and the first,
@@ -393,7 +394,7 @@ def test_full_size_steps_on_sampled_rows(cuda, name):
     cu_q = fields["cu_seqlens_q"].cpu().tolist()
     decode = [i for i in range(len(order)) if wl.num_new[order[i]] == 1]
     by_len = sorted(decode, key=lambda i: wl.num_cached[order[i]])
-    picks = [(i, 0) for i in sorted({by_len[0], by_len[len(by_len) // 2], by_len[-1]})]
+    picks = [(i, 0) for i in sorted({by_len[0], by_len[len(by_len) // 2], by_len[-1]})] if decode else []
     for i in range(len(order)):
         lq = wl.num_new[order[i]]
         if lq > 1:
