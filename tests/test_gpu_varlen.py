@@ -168,3 +168,36 @@ def test_merge_matches_the_oracle(cuda, dtype, into, dim):
     torch.testing.assert_close(lse_a.cpu(), want_lse)
     if into:
         assert torch.equal(o_a, before)
+
+
+def test_full_size_mla_prefill_step_on_sampled_rows(cuda):
+    """The measured DeepSeek-V2-Lite prefill step at full size (4 chunks of 1536 new tokens on prefixes up to 6144,
+    192-wide q.k and 128-wide values): causal attention over each chunk, unmasked attention over its prefix, and
+    the LSE merge, as the bench runs them. The first, middle and last queries of every chunk are checked against
+    the fp32 oracle over the prefix keys followed by the chunk's keys up to the query."""
+    import numpy as np
+
+    from lvattn import workloads as W
+
+    wl = W.deepseek_v2_lite_mla_prefill()
+    ex = W.materialize(wl, cuda).expanded
+    b = MI355XAttention(wl.num_heads, wl.expanded[0], wl.scale, wl.num_heads)
+    cu_q_host = [0, *np.cumsum(wl.num_new).tolist()]
+    cu_c_host = [0, *np.cumsum(wl.num_cached).tolist()]
+    cu_q = torch.tensor(cu_q_host, dtype=torch.int32, device=cuda)
+    cu_c = torch.tensor(cu_c_host, dtype=torch.int32, device=cuda)
+    max_q, max_c = max(wl.num_new), max(max(wl.num_cached), 1)
+    o, lse = b.varlen_with_lse(ex["q"], ex["k"], ex["v"], cu_q, cu_q, max_q, max_q, True)
+    co, clse = b.varlen_with_lse(ex["q"], ex["k_ctx"], ex["v_ctx"], cu_q, cu_c, max_q, max_c, False)
+    out = torch.empty_like(o)
+    merge_attention_(co, clse, o, lse, out)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    for r in range(len(wl.num_new)):
+        for j in (0, wl.num_new[r] // 2, wl.num_new[r] - 1):
+            t = cu_q_host[r] + j
+            k = torch.cat([ex["k_ctx"][cu_c_host[r]:cu_c_host[r + 1]], ex["k"][cu_q_host[r]:t + 1]]).cpu().float()
+            v = torch.cat([ex["v_ctx"][cu_c_host[r]:cu_c_host[r + 1]], ex["v"][cu_q_host[r]:t + 1]]).cpu().float()
+            want = A.dense_attention(ex["q"][t:t + 1].cpu().float(), k, v, wl.scale, causal=False)
+            torch.testing.assert_close(out[t:t + 1].float().cpu(), want, **TOL[torch.bfloat16],
+                                       msg=lambda m: f"chunk {r} query {j}: {m}")
