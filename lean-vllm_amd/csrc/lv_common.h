@@ -215,20 +215,13 @@ __device__ inline float xor32_sum(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
-// IEEE: vmax (NaN-propagating), else fmaxf.
-template <bool IEEE = true>
-__device__ __forceinline__ float max2(float a, float b) {
-  return IEEE ? vmax(a, b) : fmaxf(a, b);
-}
-template <bool IEEE = true>
 __device__ inline float xor16_max(float x) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return max2<IEEE>(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return vmax(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
-template <bool IEEE = true>
 __device__ inline float xor32_max(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return max2<IEEE>(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return vmax(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 // Inclusive prefix sum over the 64 lanes of a wave.
 __device__ inline int wave_incl_scan(int x) {

@@ -64,11 +64,11 @@ constexpr int kPlanMaxRows = 4096;  // rows of a step with prompts (the work-lis
 // the 16-bit format of the cache (fp32 accumulation), as the MFMA path does with its probability tiles.
 
 // Reduce over the lane groups of a wave that hold different tokens (lanes i, i + LPT, i + 2 LPT, ...).
-template <int LPT, bool IEEE>
+template <int LPT>
 __device__ inline float groups_max(float x) {
   static_assert(LPT == 8 || LPT == 16, "8 or 16 lanes per token");
-  if constexpr (LPT == 8) x = max2<IEEE>(x, dpp_ror8(x));  // lanes i and i ^ 8 of each 16-lane row
-  return xor32_max<IEEE>(xor16_max<IEEE>(x));
+  if constexpr (LPT == 8) x = vmax(x, dpp_ror8(x));  // lanes i and i ^ 8 of each 16-lane row
+  return xor32_max(xor16_max(x));
 }
 template <int LPT>
 __device__ inline float groups_sum(float x) {
@@ -79,10 +79,7 @@ __device__ inline float groups_sum(float x) {
 
 // publish (persistent launches): thread 0 stores publish_value there before the item's merge barrier, and the
 // barrier is met even by an item with nothing to do, so the whole workgroup reads the value after the call.
-// BESIDE: the workgroup shares its SIMDs with a mixed step's prompt tiles. Its score maxima then use vmax, which
-// issues about half the VALU instructions of fmaxf (no operand quieting); alone on the GPU the fmaxf build streams
-// 2% faster (its instruction schedule, not its VALU count, decides there).
-template <typename T, int D, int GS, bool BESIDE = false>
+template <typename T, int D, int GS>
 __device__ void decode_item(const AttnParams& p, int row, int split, int kvh, int qg, char* smem,
                             int* publish = nullptr, int publish_value = 0) {
   using E = Elem<T>;
@@ -168,14 +165,14 @@ __device__ void decode_item(const AttnParams& p, int row, int split, int kvh, in
     for (int g = 0; g < GS; ++g) {
       float x = s[0][g];
 #pragma unroll
-      for (int u = 1; u < U; ++u) x = max2<BESIDE>(x, s[u][g]);
-      mt[g] = groups_max<LPT, BESIDE>(x);  // finite: every tile holds a token in range
+      for (int u = 1; u < U; ++u) x = vmax(x, s[u][g]);
+      mt[g] = groups_max<LPT>(x);  // finite: every tile holds a token in range
       grow |= mt[g] > m[g];
     }
     if (__builtin_amdgcn_readfirstlane(grow)) {
 #pragma unroll
       for (int g = 0; g < GS; ++g) {
-        const float mn = max2<BESIDE>(m[g], mt[g]);
+        const float mn = vmax(m[g], mt[g]);
         const float alpha = fast_exp2((m[g] - mn) * c);
         m[g] = mn;
         l[g] *= alpha;
@@ -361,7 +358,7 @@ struct SmemBytes {
 // are dispatched in list order (longest first). The list holds a step's prompt items first (n_items[1] of them),
 // then its decode items (n_items[0] in all). Decode items run in decode_list_kernel at the decode item's register
 // budget; prompt items in prompt_list_kernel, whose MFMA tile needs more registers and LDS.
-template <typename T, int D, int GS, bool BESIDE = false>
+template <typename T, int D, int GS>
 __global__ __launch_bounds__(256) void decode_list_kernel(AttnParams p) {
   __shared__ __attribute__((aligned(16))) char smem[SmemBytes<D, GS>::kDecode];
   const int ny = p.hkv * p.qgroups;
@@ -370,7 +367,7 @@ __global__ __launch_bounds__(256) void decode_list_kernel(AttnParams p) {
   const int i = bx + p.n_items[1];
   if (i >= p.n_items[0]) return;
   const int2 it = p.items[i];
-  decode_item<T, D, GS, BESIDE>(p, it.x, it.y, kvh, qg, smem);
+  decode_item<T, D, GS>(p, it.x, it.y, kvh, qg, smem);
 }
 
 // Decode items of the work list on a persistent grid: each workgroup takes items by ticket (an atomic counter the
@@ -378,7 +375,7 @@ __global__ __launch_bounds__(256) void decode_list_kernel(AttnParams p) {
 // mixed step's prompt workgroups stay resident beside them. The next ticket is drawn at the start of an item and
 // published at its merge barrier; the merge alternates between two LDS buffers, so one barrier per item suffices.
 // Alone on the GPU the grid holds two workgroups per CU, so their waves may take 256 registers (no spills; 1-2%
-// faster than under the 128 that room for four would leave); beside a mixed step's prompt workgroups, 128.
+// faster than under the 128 that room for four would leave); BESIDE a mixed step's prompt workgroups, 128.
 template <typename T, int D, int GS, bool BESIDE = false>
 __global__ __launch_bounds__(256, BESIDE ? 4 : 2) void decode_persistent_kernel(AttnParams p) {
   __shared__ __attribute__((aligned(16))) char smem[2][SmemBytes<D, GS>::kDecode];
@@ -395,7 +392,7 @@ __global__ __launch_bounds__(256, BESIDE ? 4 : 2) void decode_persistent_kernel(
     const int bx = f / ny, by = f - bx * ny;
     const int kvh = by / p.qgroups, qg = by - kvh * p.qgroups;
     const int2 it = p.items[first + bx];
-    decode_item<T, D, GS, BESIDE>(p, it.x, it.y, kvh, qg, smem[k & 1], &s_ticket[(k + 1) & 1], next);
+    decode_item<T, D, GS>(p, it.x, it.y, kvh, qg, smem[k & 1], &s_ticket[(k + 1) & 1], next);
     f = __builtin_amdgcn_readfirstlane(s_ticket[(k + 1) & 1]);
   }
 }
@@ -664,7 +661,7 @@ static void launch_decode(const AttnParams& p, const Shape& s, int per_cu, hipSt
   if (grid > 0 && items >= 8 * grid) {
     hipLaunchKernelGGL((decode_persistent_kernel<T, D, GS, BESIDE>), dim3(grid), dim3(256), 0, stream, p);
   } else {
-    hipLaunchKernelGGL((decode_list_kernel<T, D, GS, BESIDE>), dim3(items), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((decode_list_kernel<T, D, GS>), dim3(items), dim3(256), 0, stream, p);
   }
 }
 
