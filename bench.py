@@ -36,7 +36,7 @@ PEAK_HBM_GBS = 8000.0
 PEAK_BF16_TFLOPS = 2500.0
 METRIC = "paged-attn HBM GB/s (% of peak) + tokens/s per layer, Qwen3-8B mixed batch"
 EXTRA = ("qwen3_8b_decode,qwen3_8b_long,deepseek_v2_lite_mla,qwen3_0_6b_mixed,qwen3_8b_prefill,"
-         "deepseek_v2_lite_mla_prefill")
+         "deepseek_v2_lite_mla_prefill,qwen3_8b_decode_bs16,deepseek_v2_lite_mla_bs16")
 RIDGE_FLOP_PER_BYTE = PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)  # above it a step is MFMA-bound
 # Workloads whose whole working set fits the 256 MB Infinity Cache: each timed step starts from a flushed cache.
 FLUSHED = {"qwen3_0_6b_mixed"}
@@ -85,7 +85,17 @@ def measure(name: str, steps: int, warmup: int, seed: int, dev):
     head_dim = wl.expanded[0] if wl.is_mla_prefill else wl.latent_dim if wl.is_mla else wl.head_dim
     backend = MI355XAttention(wl.num_heads, head_dim, wl.scale, heads_kv)
     packer = Packer(dev, wl.block_size)
-    plan = packer.stage(wl.num_cached, wl.num_new, wl.block_lists)
+    # Host time of staging a step's per-row ints (the part of packing left on the host), median of 21; outside the
+    # GPU timings, which start from inputs already on the device.
+    host_ms = []
+    for _ in range(21):
+        packer.buffers.begin()
+        t0 = time.perf_counter()
+        plan = packer.stage(wl.num_cached, wl.num_new, wl.block_lists)
+        host_ms.append((time.perf_counter() - t0) * 1e3)
+        packer.buffers.end()
+    torch.cuda.synchronize()
+    host_stage_ms = sorted(host_ms)[len(host_ms) // 2]
     out_dim = wl.expanded[1] if wl.is_mla_prefill else wl.v_dim if wl.is_mla else wl.head_dim
     out = torch.empty(wl.tokens, wl.num_heads, out_dim, dtype=torch.bfloat16, device=dev)
     if wl.is_mla_prefill:  # the cached prefix as one unmasked chunk (layers/attention.py:288-315)
@@ -150,6 +160,7 @@ def measure(name: str, steps: int, warmup: int, seed: int, dev):
         "pct_of_peak_hbm": round(100 * nbytes["total"] / (step_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 2),
         "tokens_per_s_per_layer": round(wl.tokens / (step_ms * 1e-3), 1),
         "kernel_ms": {"pack": round(pack_ms, 4), "store": round(store_ms, 4), "attention": round(attn_ms, 4)},
+        "host_stage_ms": round(host_stage_ms, 4),
         "attention_GBs": round(attn_gbs, 1),
         "attention_frac_of_peak": round(attn_gbs / PEAK_HBM_GBS, 4),
         "attention_TFLOPs": round(flops / (attn_ms * 1e-3) / 1e12, 2),
@@ -162,12 +173,13 @@ def measure(name: str, steps: int, warmup: int, seed: int, dev):
     return figures, wl, t
 
 
-def cpu_baseline(wl, t, dec_sample: int = 4096):
+def cpu_baseline(wl, t, dec_sample: int = 256, passes: int = 5):
     """The oracle's TorchAttention restatement (page gather, zeroed padding, row padding, bottom-right mask,
-    GQA-folded SDPA) in fp32 on the host cores, on a bounded sample of the step: every prompt chunk in full plus
-    up to ``dec_sample`` decode rows (the whole Qwen3-8B mixed step is about 10 s of CPU work), the decode time
-    scaled to all decode rows when sampled. Returns the object for the JSON line,
-    in the same algorithmic-byte GB/s as the GPU figures (and tokens/s per layer)."""
+    GQA-folded SDPA) in fp32 on the host cores, on a bounded sample of the step: every prompt chunk in full plus the
+    first ``dec_sample`` decode rows, with the rows' pages copied to the host beforehand. One warmup pass, whose
+    outputs are first checked against the textbook dense oracle (a few decode rows and prompt queries, max-abs
+    1e-3), then the median of ``passes`` timed passes; the decode time is scaled to all decode rows. Returns the
+    object for the JSON line, in the same algorithmic-byte GB/s as the GPU figures (and tokens/s per layer)."""
     import numpy as np
     import torch
 
@@ -186,12 +198,11 @@ def cpu_baseline(wl, t, dec_sample: int = 4096):
     q_start = np.concatenate([[0], np.cumsum(num_new)])
 
     def compact(rows):
-        """The rows' pages copied to the host as fp32, renumbered 0..n-1 (the oracle reads only these)."""
+        """The rows' pages copied to the host (bf16), renumbered 0..n-1 (the oracle reads only these)."""
         pages = sorted({p for r in rows for p in lists[r]})
         index = {p: i for i, p in enumerate(pages)}
         sel = torch.tensor(pages, dtype=torch.long, device=t.k_cache.device)
-        kc = t.k_cache[sel].float().cpu()
-        vc = t.v_cache[sel].float().cpu()
+        kc, vc = t.k_cache[sel].cpu(), t.v_cache[sel].cpu()
         width = max(len(lists[r]) for r in rows)
         bt = torch.full((len(rows), width), -1, dtype=torch.int32)
         for j, r in enumerate(rows):
@@ -200,32 +211,59 @@ def cpu_baseline(wl, t, dec_sample: int = 4096):
 
     math_ = A.TorchMath(wl.num_heads, wl.head_dim, wl.scale, wl.num_kv_heads)
     q_all = t.q.float().cpu()
-    timings = {}
+    dec = None
     if sample_dec:
-        spent = 0.0
-        for c0 in range(0, len(sample_dec), 128):  # 128 rows' pages on the host at a time
-            rows = sample_dec[c0:c0 + 128]
-            kc, vc, bt = compact(rows)
-            q = q_all[[int(q_start[r]) for r in rows]]
-            lens = torch.tensor([int(num_cached[r] + 1) for r in rows], dtype=torch.int32)
-            t0 = time.perf_counter()
-            A.decode_in_row_chunks(math_, q, kc, vc, lens, bt, rows_per_chunk=16)
-            spent += time.perf_counter() - t0
-            del kc, vc
-        timings["decode"] = spent * len(dec_rows) / len(sample_dec)
+        kc, vc, bt = compact(sample_dec)
+        q = q_all[[int(q_start[r]) for r in sample_dec]]
+        lens = torch.tensor([int(num_cached[r] + 1) for r in sample_dec], dtype=torch.int32)
+        dec = (q, kc, vc, lens, bt)
+    pre = []
     if pre_rows:
         kc, vc, bt = compact(pre_rows)
-        total = 0.0
         for j, r in enumerate(pre_rows):
             lq, lk = int(num_new[r]), int(num_cached[r] + num_new[r])
-            q = q_all[int(q_start[r]): int(q_start[r]) + lq]
             ctx = A.context(cu_seqlens_q=torch.tensor([0, lq], dtype=torch.int32),
                             cu_seqlens_k=torch.tensor([0, lk], dtype=torch.int32), max_seqlen_q=lq, max_seqlen_k=lk,
                             block_tables=bt[j:j + 1])
+            pre.append((q_all[int(q_start[r]): int(q_start[r]) + lq], kc, vc, ctx))
+
+    def one_pass():
+        times, outs = {}, {}
+        if dec is not None:
             t0 = time.perf_counter()
-            math_.prefill(q, None, None, kc, vc, ctx)
-            total += time.perf_counter() - t0
-        timings["prefill"] = total
+            outs["decode"] = A.decode_in_row_chunks(math_, *dec, rows_per_chunk=16)
+            times["decode"] = time.perf_counter() - t0
+        if pre:
+            t0 = time.perf_counter()
+            outs["prefill"] = [math_.prefill(q, None, None, kc, vc, ctx) for q, kc, vc, ctx in pre]
+            times["prefill"] = time.perf_counter() - t0
+        return times, outs
+
+    _, outs = one_pass()  # warmup, and the outputs the check reads
+    worst = 0.0
+    if dec is not None:
+        q, kc, vc, lens, bt = dec
+        for j in sorted({0, len(sample_dec) // 2, len(sample_dec) - 1}):
+            n = int(lens[j])
+            pages = bt[j, : -(-n // wl.block_size)].long()
+            k = kc[pages].flatten(0, 1)[:n].float()
+            v = vc[pages].flatten(0, 1)[:n].float()
+            want = A.dense_attention(q[j:j + 1], k, v, wl.scale, causal=False)
+            worst = max(worst, (outs["decode"][j:j + 1] - want).abs().max().item())
+    for (q, kc, vc, ctx), o in zip(pre, outs.get("prefill", [])):
+        lq, lk = q.size(0), int(ctx.max_seqlen_k)
+        pages = ctx.block_tables[0, : -(-lk // wl.block_size)].long()
+        k = kc[pages].flatten(0, 1)[:lk].float()
+        v = vc[pages].flatten(0, 1)[:lk].float()
+        for j in (0, lq - 1):
+            want = A.dense_attention(q[j:j + 1], k[:lk - lq + j + 1], v[:lk - lq + j + 1], wl.scale, causal=False)
+            worst = max(worst, (o[j:j + 1] - want).abs().max().item())
+    if worst > 1e-3:
+        raise RuntimeError(f"cpu baseline: the timed restatement differs from the dense oracle by {worst:.2e}")
+    runs = [one_pass()[0] for _ in range(passes)]
+    timings = {k: sorted(r[k] for r in runs)[passes // 2] for k in runs[0]}
+    if "decode" in timings:
+        timings["decode"] *= len(dec_rows) / len(sample_dec)
     seconds = sum(timings.values())
     nbytes = W.algorithmic_bytes(wl)["attention"]
     return {
@@ -233,10 +271,11 @@ def cpu_baseline(wl, t, dec_sample: int = 4096):
         "unit": "GB/s",
         "cores": cores,
         "kind": "port",
-        "sample": (f"oracle TorchAttention restatement (attention only), fp32, {cores} threads: all {len(pre_rows)} "
-                   f"prompt chunks in full ({timings.get('prefill', 0):.2f} s) + {len(sample_dec)} of "
-                   f"{len(dec_rows)} decode rows ({timings.get('decode', 0):.2f} s"
-                   f"{'' if len(sample_dec) == len(dec_rows) else ', scaled to all rows'})"),
+        "sample": (f"oracle TorchAttention restatement (attention only), fp32, {cores} threads, checked against the "
+                   f"dense oracle (max abs {worst:.1e}), 1 warmup + median of {passes}: all {len(pre_rows)} prompt "
+                   f"chunks in full ({timings.get('prefill', 0):.2f} s) + {len(sample_dec)} of {len(dec_rows)} "
+                   f"decode rows ({timings.get('decode', 0):.2f} s"
+                   f"{'' if len(sample_dec) == len(dec_rows) else ' scaled to all rows'})"),
         "tokens_per_s_per_layer": round(wl.tokens / seconds, 1),
         "seconds_per_step": round(seconds, 3),
     }
@@ -312,6 +351,7 @@ def main():
         "pct_of_peak_hbm": primary["pct_of_peak_hbm"],
         "tokens_per_s_per_layer": primary["tokens_per_s_per_layer"],
         "kernel_ms": primary["kernel_ms"],
+        "host_stage_ms": primary["host_stage_ms"],
         "bytes": primary["bytes"],
         "roofline": {
             "bound": "hbm",

@@ -29,7 +29,7 @@ extern "C" {
 #define LV_SCHEDULE_SERIAL 1
 #define LV_SCHEDULE_OVERLAP 2
 
-#define LV_ABI_VERSION 5
+#define LV_ABI_VERSION 6
 
 /* The last error message of the calling thread ("" if none). */
 const char* lv_last_error(void);
@@ -59,6 +59,11 @@ int lv_abi_version(void);
  *   logits_indices[L]   int64, L = sum(num_logits): for each sampling row in scheduler order, the last
  *                       num_logits token rows of its chunk, cu_seqlens_q[b+1] - n .. cu_seqlens_q[b+1] - 1
  * (both NULL to skip).
+ * num_back[B] (optional, scheduler order, may be NULL): drafts of the previous step that were rejected, per row;
+ * the row's tokens start that many positions before num_cached (ModelRunner._move_back, model_runner.py:527-551:
+ * positions, slots, context lengths and cu_seqlens_k follow; host-side lengths computed from num_cached remain
+ * upper bounds, as in the reference).
+ * A token whose page lies past its row's block list gets slot -1 (stores nothing).
  * flags: 0, or LV_PACK_DENSE_SLOTS for a step replayed in a captured graph of fixed size: slot_mapping then has
  * one entry per token, -1 for the tokens of rows without a block list (model_runner.py:597-602 pads a graph's
  * rows that way). Such a padding row is given num_cached = -num_new, so its context length is 0.
@@ -69,7 +74,7 @@ int lv_pack(const int32_t* num_cached, const int32_t* num_new, const int32_t* bl
             int32_t num_rows, int32_t query_len, int32_t block_size, int32_t table_width, int32_t num_tokens,
             int32_t* order, int32_t* cu_seqlens_q, int32_t* cu_seqlens_k, int64_t* positions,
             int32_t* slot_mapping, int32_t* context_lens, int32_t* block_tables, const int32_t* num_logits,
-            int64_t* logits_indices, int32_t flags, void* stream);
+            int64_t* logits_indices, const int32_t* num_back, int32_t flags, void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------
  * Scatter new keys/values into the paged cache. Replaces AttentionBackend.store_kvcache

@@ -170,19 +170,11 @@ struct FastDiv {
 // ---------------------------------------------------------------------------------------------------------
 // Global memory.
 
-#ifndef LV_STREAM_NT
-#define LV_STREAM_NT 1
-#endif
-
 __device__ inline u32x4 ld16(const char* ptr) { return *reinterpret_cast<const u32x4*>(ptr); }
 // Streaming load of cache rows that this launch reads once: the non-temporal hint keeps them from displacing
 // reusable lines in L2 and the Infinity Cache (about 7.0 vs 6.2 TB/s for a plain streaming read on MI355X).
 __device__ inline u32x4 ld16_stream(const char* ptr) {
-#if LV_STREAM_NT
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ptr));
-#else
-  return *reinterpret_cast<const u32x4*>(ptr);
-#endif
 }
 __device__ inline void st16(char* ptr, u32x4 v) { *reinterpret_cast<u32x4*>(ptr) = v; }
 
@@ -291,11 +283,6 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 
 // STREAM: rows this launch reads once (non-temporal, as ld16_stream); otherwise cached, for tiles that other
 // workgroups read again.
-#if LV_STREAM_NT
-#define LV_DMA_NT " nt"
-#else
-#define LV_DMA_NT ""
-#endif
 
 // One 16-byte load per lane from base + off into LDS at lds_base + 16 lane (lds_base wave-uniform, set through
 // M0). Issued as inline assembly so that the compiler, which cannot tell which LDS bytes the load writes, adds no
@@ -303,7 +290,7 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 template <bool STREAM = true>
 __device__ __forceinline__ void lds_dma16(const char* base, uint32_t off, uint32_t lds_base) {
   if (STREAM)
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" LV_DMA_NT ::"v"(off), "s"(base),
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(off), "s"(base),
                  "s"(lds_base)
                  : "memory", "m0");
   else
@@ -316,7 +303,7 @@ __device__ __forceinline__ void lds_dma16(const char* base, uint32_t off, uint32
 template <bool STREAM = true>
 __device__ __forceinline__ void lds_dma16(const char* src, uint32_t lds_base) {
   if (STREAM)
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" LV_DMA_NT ::"v"(src),
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src),
                  "s"(lds_base)
                  : "memory", "m0");
   else

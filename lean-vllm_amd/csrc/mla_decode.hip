@@ -6,14 +6,16 @@
 // 576 (kv_lora_rank 512 + rope 64) and v_dim 512: query j of a row with lq queries and L cached latents sees
 // latents 0 .. L - lq + j.
 //
-// Work item = (row, query, 16-head tile, split of the row's latents); one workgroup of 4 waves. Per iteration a
-// 32-latent tile (36 KB) is staged row-major in LDS while the next tile's loads are in flight in registers.
-//   S^T = Lat Q^T     (32 latents x 16 heads, K = 576) on MFMA 16x16x32: wave (token half th, k half kh) takes
-//                     9 k-steps of one 16-latent half; the two k halves are summed through LDS.
-//   online softmax    per head over the tile; every wave holds the same P^T.
-//   O^T += V^T P^T    (512 dims x 16 heads, K = 32 latents) on MFMA 16x16x32: wave w owns dims [128 w, 128 w + 128).
-//                     V^T operands come from the row-major tile by gfx950's transposing LDS read (ds_read_b64_tr_b16).
-// Rows whose latents were split are combined by log-sum-exp in mla_merge_kernel.
+// Two schedules, both streaming latents from HBM straight into an LDS ring (global_load_lds_dwordx4):
+//   balanced runs (mla_run_kernel)  pages a multiple of 16 latents: the units' 16-latent stages, end to end, are cut
+//                                   into equal runs, one per workgroup; units cut by run boundaries are merged by
+//                                   log-sum-exp in mla_run_merge_kernel.
+//   split schedule (mla_decode_dma_kernel)  other page sizes, or more units than the runs' in-kernel scan holds:
+//                                   one workgroup per (row, split of <= 4096 latents, query, 16-head tile); split
+//                                   rows are merged by log-sum-exp in mla_merge_kernel.
+// Per 16-latent stage: S^T = Lat Q^T (16 latents x 16 heads, K = 576) on MFMA 16x16x32, the online softmax per
+// head, and O^T += V^T P^T (512 dims x 16 heads) on MFMA 16x16x16 with V^T operands from gfx950's transposing LDS
+// read (ds_read_b64_tr_b16).
 #include <algorithm>
 
 #include "lv_common.h"
@@ -22,29 +24,15 @@ namespace lv {
 
 constexpr int kLatent = 576;              // latent width served: kv_lora_rank 512 + rope 64
 constexpr int kVDim = 512;                // value width: the latents' leading entries
-constexpr int kMlaTile = 32;              // latents per iteration
 constexpr int kMlaPitch = kLatent + 16;   // LDS row pitch in elements (1184 bytes): conflict-free operand reads and
                                           // transposing reads (a 1168-byte pitch halves the latter's rate)
 constexpr int kLatChunks = kLatent / 8;   // 16-byte chunks per latent row
-constexpr int kMlaKHalf = kLatent / 64;   // MFMA k-steps (32 wide) per k half: 9
-constexpr int kStageLoads = kMlaTile * kLatChunks / 256;  // 16-byte chunks each thread stages per tile: 9
-static_assert(kMlaTile * kLatChunks % 256 == 0, "tile chunks split evenly over 256 threads");
 
 constexpr int kMlaMaxSplit = 4096;        // latents per work item at most
 constexpr int kMlaMaxBlocks = kMlaMaxSplit / 16 + 2;  // pages one work item touches at most (pages >= 16 latents)
 
-#ifndef LV_MLA_STAGES
-#define LV_MLA_STAGES 4
-#endif
-#ifndef LV_MLA_DMA
-#define LV_MLA_DMA 1
-#endif
-#ifndef LV_MLA_RUNS
-#define LV_MLA_RUNS 1
-#endif
-#ifndef LV_MLA_SPLIT_TARGET
-#define LV_MLA_SPLIT_TARGET 4096
-#endif
+constexpr int kMlaSplitStages = 4;    // ring depth of the split schedule
+constexpr int kMlaSplitTarget = 4096;  // split-schedule items (x queries x head tiles) a grid aims for
 
 struct MlaParams {
   const char* q;
@@ -66,163 +54,9 @@ struct MlaParams {
   int32_t* prefix;  // runs: [units + 2] stage prefix over units, then the stage total and the run length
 };
 
-template <typename T>
-__global__ __launch_bounds__(256) void mla_decode_kernel(MlaParams p) {
-  using E = Elem<T>;
-  __shared__ __attribute__((aligned(16))) uint16_t lat[kMlaTile * kMlaPitch];
-  __shared__ __attribute__((aligned(16))) f32x4 spart[4][64];
-  __shared__ int64_t page_off[kMlaMaxBlocks];  // byte offsets of the work item's pages, in order
-  const int row = blockIdx.x / p.max_splits, split = blockIdx.x % p.max_splits;
-  const int qj = blockIdx.y / p.htiles, ht = blockIdx.y % p.htiles;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int n = lane & 15, g = lane >> 4;
-
-  const int lk = p.lens[row] - p.lq + qj + 1;  // latents this query sees
-  const int kbeg = split * p.split;
-  if ((split > 0 && kbeg >= lk) || split >= p.max_splits) return;
-  const int kend = min(lk, kbeg + p.split);
-  const int nsplit = lk > 0 ? min((lk + p.split - 1) / p.split, p.max_splits) : 0;
-  const int tokq = row * p.lq + qj;
-  const int head = ht * 16 + n;  // the head of this lane's S / O columns
-  const bool hvalid = head < p.heads;
-  const float c = p.scale_log2;
-
-  // Q^T operand for this wave's k half: lane holds dims 32 s + 8 g .. + 7 of head n.
-  const int th = wave >> 1, kh = wave & 1;
-  u32x4 qb[kMlaKHalf];
-  {
-    const char* qrow = p.q + tokq * p.q_st + (int64_t)head * p.q_sh;
-#pragma unroll
-    for (int s = 0; s < kMlaKHalf; ++s)
-      qb[s] = hvalid ? ld16(qrow + (int64_t)(32 * (kMlaKHalf * kh + s) + 8 * g) * 2) : u32x4{0, 0, 0, 0};
-  }
-
-  float m = -INFINITY, lsum = 0.f;
-  f32x4 o[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) o[j] = f32x4{0, 0, 0, 0};
-
-  // The work item's pages, looked up once: tile loads then wait on no table read.
-  const int page0 = kend > kbeg ? (int)p.bs.div(kbeg) : 0;
-  const int npages = kend > kbeg ? (int)p.bs.div(kend - 1) - page0 + 1 : 0;
-  {
-    const int32_t* table = p.tables + (int64_t)row * p.t_stride + page0;
-    for (int i = tid; i < npages; i += 256) page_off[i] = (int64_t)table[i] * p.c_sb;
-  }
-  __syncthreads();
-  // Latents past the range are staged as zeros: their weight is 0 and 0 * NaN must not happen.
-  auto fetch = [&](int t0, u32x4 (&st)[kStageLoads]) {
-#pragma unroll
-    for (int i = 0; i < kStageLoads; ++i) {
-      const int ch = tid + 256 * i;
-      const int tt = ch / kLatChunks, part = ch - tt * kLatChunks;
-      const int tok = t0 + tt;
-      u32x4 v = {0, 0, 0, 0};
-      if (tok < kend) {
-        const int pg = (int)p.bs.div(tok);
-        const int64_t off = page_off[pg - page0] + (int64_t)(tok - pg * (int)p.bs.d) * p.c_st + part * 16;
-        v = ld16_stream(p.cache + off);
-      }
-      st[i] = v;
-    }
-  };
-  auto stash = [&](const u32x4 (&st)[kStageLoads]) {
-#pragma unroll
-    for (int i = 0; i < kStageLoads; ++i) {
-      const int ch = tid + 256 * i;
-      const int tt = ch / kLatChunks, part = ch - tt * kLatChunks;
-      *reinterpret_cast<u32x4*>(lat + tt * kMlaPitch + part * 8) = st[i];
-    }
-  };
-
-  const int ntiles = kend > kbeg ? (kend - kbeg + kMlaTile - 1) / kMlaTile : 0;
-  u32x4 st[kStageLoads];
-  if (ntiles > 0) fetch(kbeg, st);
-  for (int it = 0; it < ntiles; ++it) {
-    const int t0 = kbeg + it * kMlaTile;
-    __syncthreads();  // the previous tile's LDS reads are done
-    stash(st);
-    __syncthreads();
-    if (it + 1 < ntiles) fetch(t0 + kMlaTile, st);
-
-    // Partial S^T over this wave's k half: lane holds latents 16 th + 4 g + r of head n.
-    f32x4 sacc = {0, 0, 0, 0};
-    const uint16_t* arow = lat + (16 * th + n) * kMlaPitch + 8 * g;
-#pragma unroll
-    for (int s = 0; s < kMlaKHalf; ++s) {
-      const u32x4 a = *reinterpret_cast<const u32x4*>(arow + 32 * (kMlaKHalf * kh + s));
-      sacc = E::mfma16x16x32(a, qb[s], sacc);
-    }
-    spart[wave][lane] = sacc;
-    __syncthreads();
-    f32x4 s0 = spart[0][lane] + spart[1][lane];  // latents t0 + 4 g + r
-    f32x4 s1 = spart[2][lane] + spart[3][lane];  // latents t0 + 16 + 4 g + r
-    if (t0 + kMlaTile > kend) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        s0[r] = t0 + 4 * g + r < kend ? s0[r] : -INFINITY;
-        s1[r] = t0 + 16 + 4 * g + r < kend ? s1[r] : -INFINITY;
-      }
-    }
-    float mx = vmax(vmax(vmax(s0[0], s0[1]), vmax(s0[2], s0[3])), vmax(vmax(s1[0], s1[1]), vmax(s1[2], s1[3])));
-    mx = xor32_max(xor16_max(mx));  // over the 32 latents of head n (finite: the tile holds one in range)
-    const float mn = vmax(m, mx);
-    const float alpha = fast_exp2((m - mn) * c);
-    m = mn;
-    const float mc = m * c;
-    float pr[8];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      pr[r] = fast_exp2(fmaf(s0[r], c, -mc));
-      pr[4 + r] = fast_exp2(fmaf(s1[r], c, -mc));
-    }
-    float ps = 0.f;
-#pragma unroll
-    for (int r = 0; r < 8; ++r) ps += pr[r];
-    lsum = lsum * alpha + ps;
-    // P^T operand: k slots 8 g .. 8 g + 7 = latents 4 g + 0..3, then 16 + 4 g + 0..3, of head n.
-    const u32x4 pb = {E::pack(pr[0], pr[1]), E::pack(pr[2], pr[3]), E::pack(pr[4], pr[5]), E::pack(pr[6], pr[7])};
-
-    // O^T tiles of this wave's dims: V^T operand rows (dims) 128 w + 16 j + n, k slots as pb.
-    const uint16_t* v0 = lat + (4 * g + (n >> 2)) * kMlaPitch + 128 * wave + 4 * (n & 3);
-    const uint16_t* v1 = v0 + 16 * kMlaPitch;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const u32x2 lo = lds_read_tr16(v0 + 16 * j);
-      const u32x2 hi = lds_read_tr16(v1 + 16 * j);
-      o[j] = o[j] * alpha;
-      o[j] = E::mfma16x16x32(u32x4{lo[0], lo[1], hi[0], hi[1]}, pb, o[j]);
-    }
-  }
-
-  // Row sums of head n: each lane summed its own latents; add the four lane groups.
-  lsum = xor32_sum(xor16_sum(lsum));
-  if (!hvalid) return;
-  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-  if (nsplit <= 1) {
-    char* dst = p.out + tokq * p.o_st + (int64_t)head * p.o_sh;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int d = 128 * wave + 16 * j + 4 * g;
-      const u32x2 v = {E::pack(o[j][0] * inv, o[j][1] * inv), E::pack(o[j][2] * inv, o[j][3] * inv)};
-      *reinterpret_cast<u32x2*>(dst + d * 2) = v;
-    }
-  } else {
-    const int64_t slot = ((int64_t)tokq * p.heads + head) * p.max_splits + split;
-    float* dst = p.part_o + slot * kVDim;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int d = 128 * wave + 16 * j + 4 * g;
-      *reinterpret_cast<f32x4*>(dst + d) = o[j] * inv;
-    }
-    if (wave == 0 && g == 0) p.part_lse[slot] = lsum > 0.f ? m * c + fast_log2(lsum) : -INFINITY;
-  }
-}
-
 // ---------------------------------------------------------------------------------------------------------
-// Streaming variant: latents move from HBM straight into LDS (global_load_lds_dwordx4), a ring of three 16-latent
-// stages with two in flight while the third is consumed; no registers stage data. Each wave computes the stage's
+// Split schedule: latents move from HBM straight into LDS (global_load_lds_dwordx4), a ring of kMlaSplitStages
+// 16-latent stages with all but one in flight while one is consumed; no registers stage data. Each wave computes the stage's
 // whole S^T (16 latents x 16 heads, K = 576) from LDS, then O^T for its 128 output dims with MFMA 16x16x16 whose
 // V^T operands come from one transposing LDS read each. One unfenced barrier per stage; every wait on the stage
 // loads is an explicit vmcnt.
@@ -432,13 +266,8 @@ __global__ __launch_bounds__(256) void mla_decode_dma_kernel(MlaParams p) {
 // and one workgroup with five or eight stages is 40% slower.
 
 constexpr int kRunMin = 16;          // stages per run at least (256 latents)
-#ifndef LV_MLA_RUN_STAGES
-#define LV_MLA_RUN_STAGES 2
-#endif
-#ifndef LV_MLA_RUNS_PER_CU
-#define LV_MLA_RUNS_PER_CU (LV_MLA_RUN_STAGES <= 2 ? 3 : LV_MLA_RUN_STAGES <= 4 ? 2 : 1)
-#endif
-constexpr int kRunsPerCU = LV_MLA_RUNS_PER_CU;  // workgroups that fit a CU's 160 KB of LDS
+constexpr int kRunStages = 2;        // ring depth of a run
+constexpr int kRunsPerCU = 3;        // run workgroups per CU (three 2-stage rings fit a CU's 160 KB of LDS)
 constexpr int kRunMaxUnits = 8192;   // units the in-kernel scan serves
 
 __device__ __forceinline__ int unit_latents(const MlaParams& p, int u) {
@@ -807,9 +636,9 @@ struct MlaShape {
 template <typename T>
 static void launch_dma(const MlaParams& p, bool one_page, dim3 grid, hipStream_t st) {
   if (one_page)
-    hipLaunchKernelGGL((mla_decode_dma_kernel<T, LV_MLA_STAGES, true>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((mla_decode_dma_kernel<T, kMlaSplitStages, true>), grid, dim3(256), 0, st, p);
   else
-    hipLaunchKernelGGL((mla_decode_dma_kernel<T, LV_MLA_STAGES, false>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((mla_decode_dma_kernel<T, kMlaSplitStages, false>), grid, dim3(256), 0, st, p);
 }
 
 static MlaShape mla_shape(int32_t rows, int32_t lq, int32_t heads, int32_t max_k) {
@@ -818,7 +647,7 @@ static MlaShape mla_shape(int32_t rows, int32_t lq, int32_t heads, int32_t max_k
   const int64_t keys = max_k > 0 ? max_k : 1;
   // Split schedule (pages not a multiple of 16 latents, or too many units for the in-kernel scan).
   int64_t split = 256;
-  while (split < kMlaMaxSplit && split < keys && units * ((keys + split - 1) / split) > LV_MLA_SPLIT_TARGET)
+  while (split < kMlaMaxSplit && split < keys && units * ((keys + split - 1) / split) > kMlaSplitTarget)
     split *= 2;
   s.split = (int32_t)split;
   s.max_splits = (int32_t)((keys + split - 1) / split);
@@ -839,7 +668,7 @@ static MlaShape mla_shape(int32_t rows, int32_t lq, int32_t heads, int32_t max_k
 
 template <typename T>
 static void launch_runs(const MlaParams& p, int runs, hipStream_t st) {
-  hipLaunchKernelGGL((mla_run_kernel<T, LV_MLA_RUN_STAGES>), dim3(runs), dim3(256), 0, st, p);
+  hipLaunchKernelGGL((mla_run_kernel<T, kRunStages>), dim3(runs), dim3(256), 0, st, p);
   hipLaunchKernelGGL(mla_run_merge_kernel<T>, dim3(p.units, 16), dim3(64), 0, st, p);
 }
 
@@ -911,7 +740,7 @@ extern "C" int lv_mla_decode(const void* q, int64_t q_stride_t, int64_t q_stride
   const bool one_page = block_size % kDmaTile == 0 && p.c_st * kDmaTile < ((int64_t)1 << 31);
   // The run schedule counts stages in 32 bits on the device.
   const int64_t stage_bound = (int64_t)s.units * (((int64_t)std::max(max_seqlen_k, 1) + kDmaTile - 1) / kDmaTile);
-  if (LV_MLA_RUNS && one_page && s.units <= kRunMaxUnits && stage_bound < ((int64_t)1 << 30)) {
+  if (one_page && s.units <= kRunMaxUnits && stage_bound < ((int64_t)1 << 30)) {
     p.units = s.units;
     p.part_lse = reinterpret_cast<float*>(ws + s.lse_off);
     p.part_o = reinterpret_cast<float*>(ws + s.o_off);
@@ -924,17 +753,11 @@ extern "C" int lv_mla_decode(const void* q, int64_t q_stride_t, int64_t q_stride
     return LV_OK;
   }
   const dim3 grid(num_rows * s.max_splits, queries_per_row * p.htiles);
-  if (LV_MLA_DMA) {
-    if (dtype == LV_DTYPE_BF16)
-      launch_dma<BF16>(p, one_page, grid, st);
-    else
-      launch_dma<F16>(p, one_page, grid, st);
-  } else if (dtype == LV_DTYPE_BF16) {
-    hipLaunchKernelGGL(mla_decode_kernel<BF16>, grid, dim3(256), 0, st, p);
-  } else {
-    hipLaunchKernelGGL(mla_decode_kernel<F16>, grid, dim3(256), 0, st, p);
-  }
-  LV_LAUNCH_CHECK("mla_decode_kernel");
+  if (dtype == LV_DTYPE_BF16)
+    launch_dma<BF16>(p, one_page, grid, st);
+  else
+    launch_dma<F16>(p, one_page, grid, st);
+  LV_LAUNCH_CHECK("mla_decode_dma_kernel");
   if (s.max_splits > 1) {
     const dim3 mgrid(num_rows * queries_per_row, num_heads);
     if (dtype == LV_DTYPE_BF16)

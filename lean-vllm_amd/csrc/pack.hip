@@ -5,6 +5,10 @@
 // Workgroup 0 also writes the row-level outputs. No grid-wide synchronisation, no atomics, no host read back.
 // The integer arithmetic mirrors ModelRunner.prepare_batch (lean_vllm/engine/model_runner.py:367-446).
 // num_logits[s] <= num_new[s] is the caller's contract (a row samples at most its own token rows).
+// num_back (optional): per scheduler row, drafts of the previous step that were rejected; the row's tokens start
+// that many positions earlier (ModelRunner._move_back, model_runner.py:527-551, applied before any output is
+// formed, so positions, slots, context lengths and cu_seqlens_k all follow).
+// A token whose page lies past its row's block list gets slot -1 (stores nothing) rather than another row's page.
 #include "lv_common.h"
 
 namespace lv {
@@ -18,7 +22,7 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
     int32_t* __restrict__ order, int32_t* __restrict__ cu_q_out, int32_t* __restrict__ cu_k_out,
     int64_t* __restrict__ positions, int32_t* __restrict__ slots, int32_t* __restrict__ context_lens,
     int32_t* __restrict__ tables, const int32_t* __restrict__ num_logits, int64_t* __restrict__ logits,
-    bool dense_slots) {
+    const int32_t* __restrict__ num_back, bool dense_slots) {
   __shared__ int src[kPackMaxRows];       // batch row -> scheduler row
   __shared__ int cu_q[kPackMaxRows + 1];  // token offsets, batch order
   __shared__ int cu_s[kPackMaxRows + 1];  // slot_mapping offsets (rows with a block list only), batch order
@@ -33,7 +37,7 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
   for (int i = tid; i <= rows; i += kPackThreads) {
     s_ptr[i] = indptr[i];
     if (i < rows) {
-      s_cached[i] = num_cached[i];
+      s_cached[i] = num_cached[i] - (num_back ? num_back[i] : 0);
       s_new[i] = num_new[i];
     }
   }
@@ -87,8 +91,8 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(
     const int list = s_ptr[s], len = s_ptr[s + 1] - list;
     if (len > 0) {
       const int page = pos / bs;
-      const int64_t block = blk_ids[list + page];
-      slots[cu_s[r] + offset] = (int32_t)(block * bs + (pos - page * bs));
+      const int64_t block = page < len ? blk_ids[list + page] : -1;
+      slots[cu_s[r] + offset] = block < 0 ? -1 : (int32_t)(block * bs + (pos - page * bs));
     } else if (dense_slots) {
       slots[cu_s[r] + offset] = -1;  // a padding row of a captured step: its tokens store nothing
     }
@@ -146,8 +150,8 @@ extern "C" int lv_pack(const int32_t* num_cached, const int32_t* num_new, const 
                        const int32_t* blk_ids, int32_t num_rows, int32_t query_len, int32_t block_size,
                        int32_t table_width, int32_t num_tokens, int32_t* order, int32_t* cu_seqlens_q,
                        int32_t* cu_seqlens_k, int64_t* positions, int32_t* slot_mapping, int32_t* context_lens,
-                       int32_t* block_tables, const int32_t* num_logits, int64_t* logits_indices, int32_t flags,
-                       void* stream) {
+                       int32_t* block_tables, const int32_t* num_logits, int64_t* logits_indices,
+                       const int32_t* num_back, int32_t flags, void* stream) {
   LV_REQUIRE(num_rows > 0 && num_rows <= kPackMaxRows, "pack: %d rows; 1 to %d are supported", num_rows,
              kPackMaxRows);
   LV_REQUIRE(block_size > 0, "pack: block_size must be positive, got %d", block_size);
@@ -168,7 +172,7 @@ extern "C" int lv_pack(const int32_t* num_cached, const int32_t* num_new, const 
   hipLaunchKernelGGL(pack_kernel, dim3(grid), dim3(kPackThreads), 0, reinterpret_cast<hipStream_t>(stream),
                      num_cached, num_new, blk_indptr, blk_ids, num_rows, query_len, block_size, table_width,
                      num_tokens, order, cu_seqlens_q, cu_seqlens_k, positions, slot_mapping, context_lens,
-                     block_tables, num_logits, logits_indices, dense);
+                     block_tables, num_logits, logits_indices, num_back, dense);
   LV_LAUNCH_CHECK("pack_kernel");
   return LV_OK;
 }

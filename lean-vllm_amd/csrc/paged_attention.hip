@@ -23,36 +23,13 @@ constexpr int kTile = 16;          // decode tokens per tile; block sizes are mu
 constexpr int kWaves = 4;          // waves per workgroup
 constexpr int kPlanMaxRows = 4096;  // rows of a step with prompts (the work-list scan lives in LDS)
 
-#ifndef LV_DECODE_PIPE
-#define LV_DECODE_PIPE 2
-#endif
-#ifndef LV_PROMPT_RING
-#define LV_PROMPT_RING 2  // LDS stages of the prompt tiles' ring (0: register staging for every page size)
-#endif
-#ifndef LV_PROMPT_PREFETCH
-#define LV_PROMPT_PREFETCH true
-#endif
-#ifndef LV_OVERLAP
-#define LV_OVERLAP 1
-#endif
-#ifndef LV_OVERLAP_CUS
-#define LV_OVERLAP_CUS 50  // percent of the CUs that hold a prompt workgroup in a mixed step by default (swept)
-#endif
-#ifndef LV_OVERLAP_CUS_MAX
-#define LV_OVERLAP_CUS_MAX 75  // at most this percent when the caller sizes the prompt share
-#endif
-#ifndef LV_DECODE_WGS
-#define LV_DECODE_WGS 2  // persistent decode workgroups per CU outside the overlap (0: one workgroup per item)
-#endif
-#ifndef LV_OVERLAP_DECODE_WGS
-#define LV_OVERLAP_DECODE_WGS 2  // persistent decode workgroups per CU beside a mixed step's prompt workgroups
-#endif
-#ifndef LV_SPLIT_TARGET
-#define LV_SPLIT_TARGET 4096
-#endif
-#ifndef LV_MIN_SPLIT
-#define LV_MIN_SPLIT 256
-#endif
+constexpr int kPromptRing = 2;        // LDS stages of the prompt tiles' ring (pages a multiple of 64 tokens)
+constexpr int kOverlapCusPct = 50;    // percent of the CUs that hold a prompt workgroup in a mixed step by default
+constexpr int kOverlapCusMaxPct = 75;  // at most this percent when the caller sizes the prompt share
+constexpr int kDecodeWgs = 2;         // persistent decode workgroups per CU outside the overlap
+constexpr int kOverlapDecodeWgs = 2;  // persistent decode workgroups per CU beside a mixed step's prompt workgroups
+constexpr int kSplitTarget = 4096;    // decode items (x kv heads x query-head groups) a split-K grid aims for
+constexpr int kMinSplit = 256;        // keys per decode item at least
 
 // ---------------------------------------------------------------------------------------------------------
 // Decode item.
@@ -219,35 +196,6 @@ __device__ void decode_item(const AttnParams& p, int row, int split, int kvh, in
   constexpr int kStride = kTile * kWaves;
   int t0 = kbeg + kTile * wave;
   if (t0 < kend) {
-#if LV_DECODE_PIPE == 1
-    // Two register buffers: the next tile's loads are in flight while this one is consumed.
-    u32x4 ka[U], va[U], kb[U], vb[U];
-    uint32_t pp[GS][U / 2];
-    int64_t base = tile_base(t0);
-    load_rows(p.k_cache, base, ka);
-    load_rows(p.v_cache, base, va);
-    while (true) {
-      const int t1 = t0 + kStride;
-      if (t1 < kend) {
-        base = tile_base(t1);
-        load_rows(p.k_cache, base, kb);
-        load_rows(p.v_cache, base, vb);
-      }
-      qk(t0, ka, pp);
-      pv(t0, va, pp);
-      if (t1 >= kend) break;
-      const int t2 = t1 + kStride;
-      if (t2 < kend) {
-        base = tile_base(t2);
-        load_rows(p.k_cache, base, ka);
-        load_rows(p.v_cache, base, va);
-      }
-      qk(t1, kb, pp);
-      pv(t1, vb, pp);
-      if (t2 >= kend) break;
-      t0 = t2;
-    }
-#elif LV_DECODE_PIPE == 2
     // Staggered: the next tile's keys load during this tile's p.v, its values during its own q.k.
     u32x4 kv[U], vv[U];
     uint32_t pp[GS][U / 2];
@@ -267,17 +215,6 @@ __device__ void decode_item(const AttnParams& p, int row, int split, int kvh, in
       load_rows(p.v_cache, next, vv);
       t0 = t1;
     }
-#else
-    for (; t0 < kend; t0 += kStride) {
-      u32x4 kv[U], vv[U];
-      uint32_t pp[GS][U / 2];
-      const int64_t base = tile_base(t0);
-      load_rows(p.k_cache, base, kv);
-      load_rows(p.v_cache, base, vv);
-      qk(t0, kv, pp);
-      pv(t0, vv, pp);
-    }
-#endif
   }
 
   // Sum the token groups of the wave (they share m); m moves to the log2 domain of the merges.
@@ -404,7 +341,7 @@ __global__ __launch_bounds__(256, 2) void prompt_list_kernel(AttnParams p) {
   const int bx = blockIdx.x / p.hkv, kvh = blockIdx.x - bx * p.hkv;
   if (bx >= p.n_items[1]) return;
   const int2 it = p.items[bx];
-  prefill_item<T, D, D, LV_PROMPT_PREFETCH, false, RING>(p, it.x, -1 - it.y, kvh, smem);
+  prefill_item<T, D, D, true, false, RING>(p, it.x, -1 - it.y, kvh, smem);
 }
 
 // Prompt items of a mixed step, run at the same time as its decode items: one workgroup per CU, each walking the
@@ -422,7 +359,7 @@ __global__ __launch_bounds__(256, 2) void prompt_overlap_kernel(AttnParams p) {
   for (int f = blockIdx.x; f < n; f += gridDim.x) {
     const int bx = f / p.hkv, kvh = f - bx * p.hkv;
     const int2 it = p.items[bx];
-    prefill_item<T, D, D, LV_PROMPT_PREFETCH, true, RING>(p, it.x, -1 - it.y, kvh, smem);
+    prefill_item<T, D, D, true, true, RING>(p, it.x, -1 - it.y, kvh, smem);
     __syncthreads();  // the next item restages the LDS tiles
   }
 }
@@ -581,8 +518,8 @@ static Shape plan_shape(int32_t rows, int32_t tokens, int32_t hq, int32_t hkv, i
   const int64_t units = (int64_t)rows * hkv * (group / s.gs);
   const int64_t keys = max_k > 0 ? max_k : 1;
   // Keys per decode item: enough items to fill the chip several times over, at least 256 keys each.
-  const int64_t target = LV_SPLIT_TARGET;
-  int64_t split = LV_MIN_SPLIT;
+  const int64_t target = kSplitTarget;
+  int64_t split = kMinSplit;
   while (split < keys && units * ((keys + split - 1) / split) > target) split *= 2;
   s.split = (int32_t)split;
   s.max_splits = (int32_t)((keys + split - 1) / split);
@@ -624,10 +561,16 @@ static SideStream* side_stream() {
   if (!s.stream) {  // default priority, non-blocking with respect to the legacy stream
     hipStream_t st = nullptr;
     hipEvent_t f = nullptr, j = nullptr;
-    if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) != hipSuccess ||
-        hipEventCreateWithFlags(&f, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&j, hipEventDisableTiming) != hipSuccess)
+    if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) != hipSuccess) return nullptr;
+    if (hipEventCreateWithFlags(&f, hipEventDisableTiming) != hipSuccess) {
+      (void)hipStreamDestroy(st);
       return nullptr;
+    }
+    if (hipEventCreateWithFlags(&j, hipEventDisableTiming) != hipSuccess) {
+      (void)hipEventDestroy(f);
+      (void)hipStreamDestroy(st);
+      return nullptr;
+    }
     s.fork = f;
     s.join = j;
     s.stream = st;
@@ -669,90 +612,98 @@ static void launch_decode(const AttnParams& p, const Shape& s, int per_cu, hipSt
 // rounded down to a multiple of 8, or the default share for 0; never more than there are prompt items.
 static int prompt_grid(const Shape& s, const AttnParams& p, int requested) {
   const int cus = device_cus();
-  const int lo = std::max(8, cus * LV_OVERLAP_CUS / 100 / 8 * 8), hi = std::max(lo, cus * LV_OVERLAP_CUS_MAX / 100);
+  const int lo = std::max(8, cus * kOverlapCusPct / 100 / 8 * 8), hi = std::max(lo, cus * kOverlapCusMaxPct / 100);
   const int n = requested > 0 ? std::min(hi, std::max(lo, requested / 8 * 8)) : lo;
   return std::min(s.max_prompt_items * p.hkv, n);
 }
 
+// The prompt items of a step with prompts, one workgroup per item, on the whole GPU.
+template <typename T, int D>
+static void launch_prompt_list(const AttnParams& p, const Shape& s, bool ring, hipStream_t stream) {
+  const dim3 grid(s.max_prompt_items * p.hkv);
+  if (ring)
+    hipLaunchKernelGGL((prompt_list_kernel<T, D, kPromptRing>), grid, dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL((prompt_list_kernel<T, D, 0>), grid, dim3(256), 0, stream, p);
+}
+
+// A step's kernels after the plan. An overlapped mixed step forks the decode items onto the device's second stream
+// and joins it back into `stream` with events; if the second stream cannot be set up, or the fork's record or wait
+// fails before anything is launched, the step runs serially instead (the same results). A failure after the decode
+// launch leaves the two streams unordered and is returned as LV_EHIP.
 template <typename T, int D, int GS>
-static void launch(const AttnParams& p, bool listed, bool mixed, bool overlap, int prompt_wgs, const Shape& s,
-                   hipStream_t stream) {
+static int launch(const AttnParams& p, bool listed, bool mixed, bool overlap, int prompt_wgs, const Shape& s,
+                  hipStream_t stream) {
   const int ny = p.hkv * p.qgroups;
-  const bool ring = LV_PROMPT_RING > 0 && p.bs.d % kPrefillKeys == 0;  // every 64-key tile in one page
-  SideStream* side = LV_OVERLAP && overlap && listed && mixed ? side_stream() : nullptr;
+  const bool ring = p.bs.d % kPrefillKeys == 0;  // every 64-key tile in one page
+  SideStream* side = overlap && listed && mixed ? side_stream() : nullptr;
+  bool forked = false;
   if (side) {
     // Decode items go to the second stream first, then the prompt items to the caller's stream: the prompt
     // workgroups (one per CU) are dispatched as soon as the plan ends, the decode workgroups fill the rest.
     const int grid = prompt_grid(s, p, prompt_wgs);
     std::lock_guard<std::mutex> g(side->lock);
-    hipEventRecord(side->fork, stream);
-    hipStreamWaitEvent(side->stream, side->fork, 0);
-    launch_decode<T, D, GS, true>(p, s, LV_OVERLAP_DECODE_WGS, side->stream);
-    hipEventRecord(side->join, side->stream);
-    if (ring) {
-      constexpr int pad = std::max(0, kOverlapLds - LV_PROMPT_RING * PromptSmem<D, D>::kBytes);
-      hipLaunchKernelGGL((prompt_overlap_kernel<T, D, LV_PROMPT_RING>), dim3(grid), dim3(256), pad, stream, p);
+    if (hipEventRecord(side->fork, stream) == hipSuccess &&
+        hipStreamWaitEvent(side->stream, side->fork, 0) == hipSuccess) {
+      forked = true;
+      launch_decode<T, D, GS, true>(p, s, kOverlapDecodeWgs, side->stream);
+      LV_LAUNCH_CHECK("decode_persistent_kernel");
+      LV_HIP_CHECK(hipEventRecord(side->join, side->stream));
+      if (ring) {
+        constexpr int pad = std::max(0, kOverlapLds - kPromptRing * PromptSmem<D, D>::kBytes);
+        hipLaunchKernelGGL((prompt_overlap_kernel<T, D, kPromptRing>), dim3(grid), dim3(256), pad, stream, p);
+      } else {
+        constexpr int pad = kOverlapLds - PromptSmem<D, D>::kBytes;
+        hipLaunchKernelGGL((prompt_overlap_kernel<T, D, 0>), dim3(grid), dim3(256), pad, stream, p);
+      }
+      LV_LAUNCH_CHECK("prompt_overlap_kernel");
+      LV_HIP_CHECK(hipStreamWaitEvent(stream, side->join, 0));
     } else {
-      constexpr int pad = kOverlapLds - PromptSmem<D, D>::kBytes;
-      hipLaunchKernelGGL((prompt_overlap_kernel<T, D, 0>), dim3(grid), dim3(256), pad, stream, p);
+      (void)hipGetLastError();  // the failed record or wait: fall back to the serial schedule
     }
-    hipStreamWaitEvent(stream, side->join, 0);
+  }
+  if (forked) {
   } else if (listed && mixed) {
-    if (ring)
-      hipLaunchKernelGGL((prompt_list_kernel<T, D, LV_PROMPT_RING>), dim3(s.max_prompt_items * p.hkv), dim3(256), 0,
-                         stream, p);
-    else
-      hipLaunchKernelGGL((prompt_list_kernel<T, D, 0>), dim3(s.max_prompt_items * p.hkv), dim3(256), 0, stream, p);
-    launch_decode<T, D, GS>(p, s, LV_DECODE_WGS, stream);
+    launch_prompt_list<T, D>(p, s, ring, stream);
+    launch_decode<T, D, GS>(p, s, kDecodeWgs, stream);
   } else if (listed) {
-    launch_decode<T, D, GS>(p, s, LV_DECODE_WGS, stream);
+    launch_decode<T, D, GS>(p, s, kDecodeWgs, stream);
   } else {
     hipLaunchKernelGGL((decode_grid_kernel<T, D, GS>), dim3(p.rows * p.max_splits, ny), dim3(256), 0, stream, p);
   }
   if (p.max_splits > 1)
     hipLaunchKernelGGL((splitk_merge_kernel<T, D>), dim3(p.rows, p.hq), dim3(64), 0, stream, p);
+  return LV_OK;
 }
 
 template <typename T, int D>
-static void launch_gs(const AttnParams& p, int gs, bool listed, bool mixed, bool overlap, int prompt_wgs,
-                      const Shape& s, hipStream_t stream) {
-  if (gs == 4) launch<T, D, 4>(p, listed, mixed, overlap, prompt_wgs, s, stream);
-  else if (gs == 2) launch<T, D, 2>(p, listed, mixed, overlap, prompt_wgs, s, stream);
-  else launch<T, D, 1>(p, listed, mixed, overlap, prompt_wgs, s, stream);
+static int launch_gs(const AttnParams& p, int gs, bool listed, bool mixed, bool overlap, int prompt_wgs,
+                     const Shape& s, hipStream_t stream) {
+  if (gs == 4) return launch<T, D, 4>(p, listed, mixed, overlap, prompt_wgs, s, stream);
+  if (gs == 2) return launch<T, D, 2>(p, listed, mixed, overlap, prompt_wgs, s, stream);
+  return launch<T, D, 1>(p, listed, mixed, overlap, prompt_wgs, s, stream);
 }
 
 template <typename T>
 static int launch_d(const AttnParams& p, int d, int gs, bool listed, bool mixed, bool overlap, int prompt_wgs,
                     const Shape& s, hipStream_t stream) {
   switch (d) {
-    case 64: launch_gs<T, 64>(p, gs, listed, mixed, overlap, prompt_wgs, s, stream); return LV_OK;
-    case 128: launch_gs<T, 128>(p, gs, listed, mixed, overlap, prompt_wgs, s, stream); return LV_OK;
+    case 64: return launch_gs<T, 64>(p, gs, listed, mixed, overlap, prompt_wgs, s, stream);
+    case 128: return launch_gs<T, 128>(p, gs, listed, mixed, overlap, prompt_wgs, s, stream);
     default: set_error("paged_attention: head_dim %d is not 64 or 128", d); return LV_EINVAL;
   }
 }
 
-}  // namespace lv
-
-using namespace lv;
-
-extern "C" size_t lv_paged_attention_workspace_bytes(int32_t num_rows, int32_t num_tokens, int32_t num_heads,
-                                                     int32_t num_kv_heads, int32_t head_dim, int32_t max_seqlen_k,
-                                                     int32_t decode_only) {
-  if (num_rows <= 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads) return 0;
-  const bool mixed = decode_only == 0;
-  const bool listed = mixed || num_rows <= kPlanMaxRows;
-  return plan_shape(num_rows, num_tokens, num_heads, num_kv_heads, head_dim, max_seqlen_k, listed).bytes;
-}
-
-extern "C" int lv_paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_cache,
-                                  const void* v_cache, int64_t cache_stride_block, int64_t cache_stride_token,
-                                  int64_t cache_stride_head, int32_t block_size, const int32_t* block_tables,
-                                  int64_t table_stride, const int32_t* cu_seqlens_q, const int32_t* seqlens_k,
-                                  const int32_t* cu_seqlens_k, int32_t num_rows, int32_t num_tokens,
-                                  int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float scale,
-                                  int32_t max_seqlen_q, int32_t max_seqlen_k, void* out, int64_t out_stride_t,
-                                  int64_t out_stride_h, void* workspace, size_t workspace_bytes, int32_t schedule,
-                                  int32_t prompt_workgroups, int32_t dtype, void* stream) {
+// One step, with the caller's workspace.
+static int paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_cache,
+                           const void* v_cache, int64_t cache_stride_block, int64_t cache_stride_token,
+                           int64_t cache_stride_head, int32_t block_size, const int32_t* block_tables,
+                           int64_t table_stride, const int32_t* cu_seqlens_q, const int32_t* seqlens_k,
+                           const int32_t* cu_seqlens_k, int32_t num_rows, int32_t num_tokens, int32_t num_heads,
+                           int32_t num_kv_heads, int32_t head_dim, float scale, int32_t max_seqlen_q,
+                           int32_t max_seqlen_k, void* out, int64_t out_stride_t, int64_t out_stride_h,
+                           void* workspace, size_t workspace_bytes, int32_t schedule,
+                           int32_t prompt_workgroups, int32_t dtype, void* stream) {
   LV_REQUIRE(dtype == LV_DTYPE_BF16 || dtype == LV_DTYPE_F16, "paged_attention: dtype %d is not bf16 or fp16",
              dtype);
   LV_REQUIRE(num_rows >= 0 && num_tokens >= 0, "paged_attention: negative row or token count");
@@ -843,4 +794,33 @@ extern "C" int lv_paged_attention(const void* q, int64_t q_stride_t, int64_t q_s
   if (rc != LV_OK) return rc;
   LV_LAUNCH_CHECK("paged_attention_kernel");
   return LV_OK;
+}
+
+}  // namespace lv
+
+using namespace lv;
+
+extern "C" size_t lv_paged_attention_workspace_bytes(int32_t num_rows, int32_t num_tokens, int32_t num_heads,
+                                                     int32_t num_kv_heads, int32_t head_dim, int32_t max_seqlen_k,
+                                                     int32_t decode_only) {
+  if (num_rows <= 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads) return 0;
+  const bool mixed = decode_only == 0;
+  const bool listed = mixed || num_rows <= kPlanMaxRows;
+  return plan_shape(num_rows, num_tokens, num_heads, num_kv_heads, head_dim, max_seqlen_k, listed).bytes;
+}
+
+extern "C" int lv_paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_cache,
+                                  const void* v_cache, int64_t cache_stride_block, int64_t cache_stride_token,
+                                  int64_t cache_stride_head, int32_t block_size, const int32_t* block_tables,
+                                  int64_t table_stride, const int32_t* cu_seqlens_q, const int32_t* seqlens_k,
+                                  const int32_t* cu_seqlens_k, int32_t num_rows, int32_t num_tokens,
+                                  int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float scale,
+                                  int32_t max_seqlen_q, int32_t max_seqlen_k, void* out, int64_t out_stride_t,
+                                  int64_t out_stride_h, void* workspace, size_t workspace_bytes, int32_t schedule,
+                                  int32_t prompt_workgroups, int32_t dtype, void* stream) {
+  return paged_attention(q, q_stride_t, q_stride_h, k_cache, v_cache, cache_stride_block, cache_stride_token,
+                         cache_stride_head, block_size, block_tables, table_stride, cu_seqlens_q, seqlens_k,
+                         cu_seqlens_k, num_rows, num_tokens, num_heads, num_kv_heads, head_dim, scale, max_seqlen_q,
+                         max_seqlen_k, out, out_stride_t, out_stride_h, workspace, workspace_bytes, schedule,
+                         prompt_workgroups, dtype, stream);
 }

@@ -10,15 +10,11 @@
 
 namespace lv {
 
-#ifndef LV_VARLEN_RING
-#define LV_VARLEN_RING 2
-#endif
-
 // Keys are packed, so every 64-key tile is contiguous: tiles stream through an LDS ring. Two workgroups fit a CU
 // up to 128-wide q.k; wider tiles take one (and its registers).
 template <int DQK, int DV>
 struct VarlenCfg {
-  static constexpr int kRing = LV_VARLEN_RING;
+  static constexpr int kRing = 2;
   static constexpr int kSmem = (kRing > 0 ? kRing : 1) * PromptSmem<DQK, DV>::kBytes;
   static constexpr int kWaves = kSmem <= 80 * 1024 && DQK <= 128 ? 2 : 1;
 };

@@ -21,7 +21,7 @@ _PROTOTYPES = {
     "lv_last_error": (ctypes.c_char_p, []),
     "lv_abi_version": (ctypes.c_int, []),
     "lv_pack": (ctypes.c_int, [_P, _P, _P, _P, c_int32, c_int32, c_int32, c_int32, c_int32,
-                               _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int32, _P]),
+                               _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int32, _P]),
     "lv_store_kvcache": (ctypes.c_int, [_P, _P, c_int64, c_int64, c_int32, c_int32, c_int32, _P, _P,
                                         c_int64, c_int64, c_int64, c_int32, _P, c_int32, _P]),
     "lv_store_latents": (ctypes.c_int, [_P, c_int64, c_int32, c_int32, _P, _P, c_int32, _P]),

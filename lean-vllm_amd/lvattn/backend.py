@@ -15,7 +15,7 @@ from __future__ import annotations
 
 import torch
 
-from . import _capi
+from . import _capi, checks
 from .abstract import AttentionBackend
 from .context import Context
 
@@ -127,6 +127,8 @@ class MI355XAttention(AttentionBackend):
         assert k_cache.stride() == v_cache.stride() and k_cache.stride(-1) == 1
         assert slot_mapping.numel() == num_tokens
         assert key.dtype == value.dtype == k_cache.dtype == v_cache.dtype
+        if checks.enabled():
+            checks.check_slots(slot_mapping, k_cache.size(0), k_cache.size(1))
         slot_mapping = slot_mapping if slot_mapping.dtype == torch.int32 else slot_mapping.to(torch.int32)
         sb, st, sh, _ = k_cache.stride()
         _capi.call("lv_store_kvcache", key.data_ptr(), value.data_ptr(), key.stride(0), value.stride(0), num_tokens,
@@ -137,6 +139,8 @@ class MI355XAttention(AttentionBackend):
         num_tokens, dim = latent.shape
         assert latent.stride(-1) == 1 and latent_cache.stride(-2) == dim and latent_cache.stride(-1) == 1
         assert slot_mapping.numel() == num_tokens and latent.dtype == latent_cache.dtype
+        if checks.enabled():
+            checks.check_slots(slot_mapping, latent_cache.numel() // dim, 1)
         slot_mapping = slot_mapping if slot_mapping.dtype == torch.int32 else slot_mapping.to(torch.int32)
         _capi.call("lv_store_latents", latent.data_ptr(), latent.stride(0), num_tokens, dim, latent_cache.data_ptr(),
                    slot_mapping.data_ptr(), latent.element_size(), _capi.stream_of(latent.device))
@@ -211,6 +215,12 @@ class MI355XAttention(AttentionBackend):
         """One query per row against its ``context_lens[b]`` cached keys; q ``[B, Hq, D]``."""
         bt, lens = context.block_tables, context.context_lens
         assert bt is not None and lens is not None
+        assert lens.numel() == q.size(0) == bt.size(0), (
+            f"decode takes one query per row: {q.size(0)} queries, {lens.numel()} context lengths, {bt.size(0)} table "
+            "rows (a step whose rows carry drafts is is_prefill and goes to prefill)")
+        if checks.enabled():
+            checks.check_tables(bt, k_cache.size(0))
+            checks.check_key_lengths(lens, bt, k_cache.size(1))
         lens = lens if lens.dtype == torch.int32 else lens.to(torch.int32)
         # The table's width bounds every length, so nothing is read back (torch_backend.py:98).
         max_k = bt.size(1) * k_cache.size(1)
@@ -227,6 +237,10 @@ class MI355XAttention(AttentionBackend):
             o, _ = self._varlen(q, k, v, cu_q, cu_k, max_q, causal=True, want_lse=False, out=out)
             return o
         bt = context.block_tables
+        if checks.enabled():
+            checks.check_query_rows(cu_q, cu_k, q.size(0))
+            checks.check_tables(bt, k_cache.size(0))
+            checks.check_key_lengths(cu_k[1:] - cu_k[:-1], bt, k_cache.size(1), what="cu_seqlens_k row length")
         max_k = context.max_seqlen_k or bt.size(1) * k_cache.size(1)
         max_q = context.max_seqlen_q or q.size(0)
         return self._attend(q, k_cache, v_cache, out, block_tables=bt, cu_seqlens_q=cu_q.to(torch.int32),
@@ -250,6 +264,9 @@ class MI355XAttention(AttentionBackend):
         rows = lens.numel()
         tokens, heads, dim = q.shape
         assert tokens % rows == 0, "every row has the same number of queries"
+        if checks.enabled():
+            checks.check_tables(bt, latent_cache.size(0))
+            checks.check_key_lengths(lens, bt, latent_cache.size(1))
         lq = tokens // rows
         max_k = bt.size(1) * latent_cache.size(1)
         if out is None:

@@ -87,7 +87,7 @@ class DecodeGraphs:
         _capi.call("lv_pack", d.data_ptr(), d[bs:].data_ptr(), d[2 * bs:].data_ptr(), d[3 * bs + 1:].data_ptr(),
                    bs, q, self.block_size, w, tokens, self.order.data_ptr(), self.cu_seqlens_q.data_ptr(),
                    self.cu_seqlens_k.data_ptr(), self.positions.data_ptr(), self.slot_mapping.data_ptr(),
-                   self.context_lens.data_ptr(), self.block_tables.data_ptr(), None, None, LV_PACK_DENSE_SLOTS,
+                   self.context_lens.data_ptr(), self.block_tables.data_ptr(), None, None, None, LV_PACK_DENSE_SLOTS,
                    _capi.stream_of(self.device))
         self.backend.store_kvcache(self.k[:tokens], self.v[:tokens], self.k_cache, self.v_cache,
                                    self.slot_mapping[:tokens])

@@ -99,28 +99,52 @@ class PackPlan:
         self.logits = logits  # logits rows gathered, or -1 for none (the whole batch samples)
 
 
-class Packer:
-    """Builds a step's attention ``Context`` fields on the GPU from per-row scheduler state."""
+def check_block_lists(num_cached, num_new, lengths, block_size: int) -> None:
+    """Every row with a block list must hold a block for each of its ``num_cached + num_new`` tokens (a row without
+    one stores nothing, as in warmup); lengths must not be negative. Raises ``ValueError`` naming the first bad row
+    (scheduler order). Arrays are numpy."""
+    if (num_cached < 0).any() or (num_new < 0).any():
+        i = int(np.flatnonzero((num_cached < 0) | (num_new < 0))[0])
+        raise ValueError(f"pack: row {i} has num_cached {int(num_cached[i])}, num_new {int(num_new[i])}")
+    need = -(-(num_cached.astype(np.int64) + num_new) // block_size)
+    short = (lengths > 0) & (lengths < need)
+    if short.any():
+        i = int(np.flatnonzero(short)[0])
+        raise ValueError(f"pack: row {i}'s block list holds {int(lengths[i])} blocks; its "
+                         f"{int(num_cached[i])} + {int(num_new[i])} tokens need {int(need[i])}")
 
-    def __init__(self, device, block_size: int):
+
+class Packer:
+    """Builds a step's attention ``Context`` fields on the GPU from per-row scheduler state.
+
+    ``decodes_latents``: the model's attention layers decode cached MLA latents (the runner's ``decodes_latents``,
+    ``model_runner.py:380-384``); a step whose rows all carry the same number of drafts is then a decode step."""
+
+    def __init__(self, device, block_size: int, decodes_latents: bool = False):
         self.block_size = block_size
+        self.decodes_latents = decodes_latents
         self.buffers = StagingBuffers(device)
 
     def pack(self, num_cached, num_new, block_lists, num_speculative_tokens: int = 0,
-             is_prompt=None, num_logits=None) -> tuple[torch.Tensor, dict]:
+             is_prompt=None, num_logits=None, num_back=None) -> tuple[torch.Tensor, dict]:
         """Per-row ``num_cached``, ``num_new`` (scheduler order) and block lists -> ``(positions, context)``.
 
         ``context`` has the keys of ``prepare_batch``'s context dict (``model_runner.py:448-462``) that attention
         and the logits gather read, plus ``order`` (batch row -> scheduler row). ``is_prompt`` marks prompt rows
-        (default: rows with more than one new token), which makes the step ``is_prefill``. ``num_logits``
-        (scheduler order) is the number of logits rows each row samples: its drafts + 1, or 0 for a chunk that
-        does not sample (default: 1 per row). As in the reference, ``logits_indices`` is gathered only for an
-        ``is_prefill`` step and is None otherwise (every row samples). The returned tensors live in buffers the
-        next call reuses.
+        (default: rows with more than one new token and no drafts allowed, i.e. ``num_new > 1 +
+        num_speculative_tokens``); a row that is not a prompt carries ``num_new - 1`` drafts. The step is
+        ``is_prefill`` as the reference decides it (``:380-384``): any prompt row, or any drafts unless the model
+        decodes latents and every row has the same query length. ``num_logits`` (scheduler order) is the number of
+        logits rows each row samples: its drafts + 1, or 0 for a chunk that does not sample (default: drafts + 1
+        for every row). As in the reference, ``logits_indices`` is gathered only for an ``is_prefill`` step and is
+        None otherwise (every row samples). ``num_back`` (device int32 ``[B]``, scheduler order, optional): drafts
+        of the previous step that were rejected, per row; the row's tokens start that many positions earlier
+        (``_move_back``, ``:527-551``), and the host lengths stay upper bounds. The returned tensors live in
+        buffers the next call reuses.
         """
         self.buffers.begin()
         plan = self.stage(num_cached, num_new, block_lists, num_speculative_tokens, is_prompt, num_logits)
-        out = self.run(plan)
+        out = self.run(plan, num_back)
         self.buffers.end()
         return out
 
@@ -141,14 +165,17 @@ class Packer:
         _, _, width = hs.stage_rows(num_cached, num_new, block_lists, buf.ctypes.data, base)
         num_cached, num_new = buf[:rows], buf[rows:2 * rows]
         lengths = np.diff(buf[2 * rows:3 * rows + 1])
+        check_block_lists(num_cached, num_new, lengths, self.block_size)
         tokens = int(num_new.sum())
         query_len = decode_query_len(num_new, num_speculative_tokens)
         order = np.argsort(num_new != query_len, kind="stable")
         lens_b, ends_b = num_new[order], (num_cached + num_new)[order]
-        if is_prompt is None:
-            is_prompt = num_new > 1
+        is_prompt = num_new > 1 + num_speculative_tokens if is_prompt is None else np.asarray(is_prompt, bool)
+        drafts = np.where(is_prompt, 0, num_new - 1)
+        has_prompt = bool(is_prompt.any())
+        uniform = not has_prompt and self.decodes_latents and bool((num_new == query_len).all())
         host = dict(
-            is_prefill=bool(np.any(is_prompt)),
+            is_prefill=has_prompt or (bool(drafts.any()) and not uniform),
             max_seqlen_q=int(lens_b.max()),
             max_seqlen_k=int(ends_b.max()),
             cu_seqlens_q_host=[0, *np.cumsum(lens_b).tolist()],
@@ -157,7 +184,7 @@ class Packer:
         )
         logits, size = -1, base
         if host["is_prefill"]:
-            n_log = np.ones(rows, np.int32) if num_logits is None else np.asarray(num_logits, dtype=np.int32)
+            n_log = (drafts + 1).astype(np.int32) if num_logits is None else np.asarray(num_logits, dtype=np.int32)
             if n_log.shape != (rows,) or (n_log < 0).any() or (n_log > num_new).any():
                 raise ValueError("pack: num_logits must give 0 .. num_new logits rows per row")
             logits = int(n_log.sum())
@@ -167,9 +194,11 @@ class Packer:
         slot_count = int(num_new[lengths > 0].sum())
         return PackPlan(rows, tokens, width, slot_count, query_len, inputs, host, logits)
 
-    def run(self, plan: PackPlan) -> tuple[torch.Tensor, dict]:
+    def run(self, plan: PackPlan, num_back: torch.Tensor | None = None) -> tuple[torch.Tensor, dict]:
         """Launch the pack kernel on staged inputs; returns ``(positions, context)``."""
         buf, rows, width = self.buffers, plan.rows, plan.width
+        if num_back is not None:
+            assert num_back.dtype == torch.int32 and num_back.shape == (rows,) and num_back.is_contiguous()
         d_cached = plan.inputs[:rows]
         d_new = plan.inputs[rows:2 * rows]
         d_indptr = plan.inputs[2 * rows:3 * rows + 1]
@@ -191,7 +220,8 @@ class Packer:
                    slots.data_ptr() if has_tables else None, context_lens.data_ptr(),
                    tables.data_ptr() if has_tables else None,
                    d_nlog.data_ptr() if plan.logits > 0 else None,
-                   logits.data_ptr() if plan.logits > 0 else None, 0, _capi.stream_of(buf.device))
+                   logits.data_ptr() if plan.logits > 0 else None, _capi.ptr(num_back), 0,
+                   _capi.stream_of(buf.device))
         context = dict(
             plan.host,
             cu_seqlens_q=cu_q,

@@ -15,6 +15,9 @@ device. Key lengths include the token(s) stored this step (``context_lens = num_
 - ``qwen3_8b_long``: 32/8 heads, d128, bs 256, pool 10,000; 16 decode rows, context U[32768, 131072].
 - ``deepseek_v2_lite_mla``: 16 heads, latent 576 (512 + 64 rope), values 512, bs 64, pool 34,000; 128 decode
   rows, context U[1024, 16384]; values N(0, 0.5); scale 1/sqrt(192).
+- ``qwen3_8b_decode_bs16``, ``deepseek_v2_lite_mla_bs16``: the same two decode steps (same lengths) on 16-token
+  pages, lean-vLLM's default ``kvcache_block_size`` (``lean_vllm/config.py:46``; MLA layers keep it when the backend
+  names no page size, ``:85-89``), over pools of the same bytes (192,000 and 136,000 pages).
 - ``deepseek_v2_lite_mla_prefill``: the same layer's prompt chunks as ``MLAAttention._prefill`` runs them
   (``lean_vllm/layers/attention.py:265-317``) on expanded heads (q.k 192, values 128): 4 chunks of 1536 new tokens
   on a cached prefix U[0, 6144]; the new tokens attend each other causally, the prefix unmasked, merged by lse.
@@ -96,13 +99,15 @@ def qwen3_0_6b_mixed(seed: int = 0) -> Workload:
                     1 / math.sqrt(128))
 
 
-def qwen3_8b_decode(seed: int = 0, batch: int = 256) -> Workload:
+def qwen3_8b_decode(seed: int = 0, batch: int = 256, block_size: int = 256) -> Workload:
     rng = np.random.default_rng(seed)
     ctx = rng.integers(512, 8192 + 1, size=batch)
     num_cached = [int(c) - 1 for c in ctx]
     num_new = [1] * batch
-    return Workload("qwen3_8b_decode", 32, 8, 128, 256, 12_000, num_cached, num_new,
-                    _tables(rng, 12_000, ctx, 256), 1 / math.sqrt(128))
+    pool = 12_000 * 256 // block_size
+    name = "qwen3_8b_decode" if block_size == 256 else f"qwen3_8b_decode_bs{block_size}"
+    return Workload(name, 32, 8, 128, block_size, pool, num_cached, num_new, _tables(rng, pool, ctx, block_size),
+                    1 / math.sqrt(128))
 
 
 def qwen3_8b_mixed(seed: int = 0) -> Workload:
@@ -133,12 +138,14 @@ def qwen3_8b_long(seed: int = 0) -> Workload:
                     _tables(rng, 10_000, ctx, 256), 1 / math.sqrt(128))
 
 
-def deepseek_v2_lite_mla(seed: int = 0) -> Workload:
+def deepseek_v2_lite_mla(seed: int = 0, block_size: int = 64) -> Workload:
     rng = np.random.default_rng(seed)
     ctx = rng.integers(1024, 16384 + 1, size=128)
     num_cached = [int(c) - 1 for c in ctx]
-    return Workload("deepseek_v2_lite_mla", 16, 1, 576, 64, 34_000, num_cached, [1] * 128,
-                    _tables(rng, 34_000, ctx, 64), 1 / math.sqrt(192), value_std=0.5, latent_dim=576, v_dim=512)
+    pool = 34_000 * 64 // block_size
+    name = "deepseek_v2_lite_mla" if block_size == 64 else f"deepseek_v2_lite_mla_bs{block_size}"
+    return Workload(name, 16, 1, 576, block_size, pool, num_cached, [1] * 128, _tables(rng, pool, ctx, block_size),
+                    1 / math.sqrt(192), value_std=0.5, latent_dim=576, v_dim=512)
 
 
 def deepseek_v2_lite_mla_prefill(seed: int = 0) -> Workload:
@@ -160,6 +167,8 @@ WORKLOADS = {
     "qwen3_8b_long": qwen3_8b_long,
     "deepseek_v2_lite_mla": deepseek_v2_lite_mla,
     "deepseek_v2_lite_mla_prefill": deepseek_v2_lite_mla_prefill,
+    "qwen3_8b_decode_bs16": lambda seed=0: qwen3_8b_decode(seed, block_size=16),
+    "deepseek_v2_lite_mla_bs16": lambda seed=0: deepseek_v2_lite_mla(seed, block_size=16),
 }
 
 

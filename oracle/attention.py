@@ -15,7 +15,9 @@ Pinned by (``tests/test_oracle_attention.py``): closed forms (one key returns it
 mean of the values; a zero query averages), brute force against ``attention_loops``, the reference's invariants
 (decode == one-token prefill, mixed == separate, bottom-right differs from top-left, NaN/inf in unused slots is
 ignored, merge of a split == unsplit, rows with no keys give lse = -inf), and planted mistakes (dropped scale,
-top-left mask, ``repeat`` for ``repeat_interleave``) that each check must reject.
+top-left mask, ``repeat`` for ``repeat_interleave``) that each check must reject. ``decode_in_row_chunks`` is
+pinned against ``TorchMath.decode`` of the whole batch and the dense oracle, with a planted page-count floor and a
+planted one-row table shift rejected.
 """
 
 from __future__ import annotations

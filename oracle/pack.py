@@ -14,7 +14,11 @@ Pinned by (``tests/test_oracle_pack.py``):
   (``tests/test_model_runner.py:509-533``) driven by a restatement of ``random_batch`` (``:536-554``), compared
   field by field as ``check_batch`` does (``:571-596``);
 - closed-form invariants (``cu`` differences equal the lengths, every slot lies in its row's own pages, a row
-  with d drafts samples the last d + 1 token rows of its chunk).
+  with d drafts samples the last d + 1 token rows of its chunk);
+- for rows whose previous drafts were rejected (``num_back``): ``move_back``, a restatement of the reference's
+  device-side correction ``ModelRunner._move_back`` (``model_runner.py:527-551``) applied to the uncorrected
+  packing, must equal the host-side correction ``starts[moved] -= num_rejected`` (``:379-385``) that
+  ``pack_numpy`` applies.
 """
 
 from __future__ import annotations
@@ -40,6 +44,7 @@ def pack_numpy(
     num_speculative_tokens: int = 0,
     num_logits=None,
     dense_slots: bool = False,
+    num_back=None,
 ) -> dict:
     """Vectorised restatement of ``prepare_batch``'s packing (``model_runner.py:356-446``, ``:448-462``).
 
@@ -48,9 +53,16 @@ def pack_numpy(
     that does not sample this step; then ``logits_indices`` follows ``model_runner.py:424-430``.
     ``dense_slots``: one slot per token, -1 for rows without a block list, as a captured graph's padded rows
     carry (``model_runner.py:597-602``), instead of the compacted eager form (``:442-445``).
+    ``num_back`` (scheduler order, optional): drafts of the previous step that were rejected, per row; the row's
+    tokens start that many positions earlier (``model_runner.py:379-385``). The host maxima and
+    ``cu_seqlens_*_host`` keep the uncorrected lengths, upper bounds as in the reference's device-side path.
     """
     num_cached = np.asarray(num_cached, dtype=np.int64)
     num_new = np.asarray(num_new, dtype=np.int64)
+    host_ends = None
+    if num_back is not None:
+        host_ends = (num_cached + num_new)
+        num_cached = num_cached - np.asarray(num_back, dtype=np.int64)
     rows = num_new.size
     query_len = decode_query_len(num_new, num_speculative_tokens)
     # Stable: rows whose length equals query_len first, scheduler order kept in each group (:367-374).
@@ -89,6 +101,7 @@ def pack_numpy(
         last_index = cu_q[1:] - 1
         offsets = np.arange(int(n.sum())) - np.repeat(np.cumsum(n) - n, n)
         logits_indices = (np.repeat(last_index[row_of[sampling]] - (n - 1), n) + offsets).astype(np.int64)
+    host_k = ends if host_ends is None else host_ends[order]
     return dict(
         logits_indices=logits_indices,
         order=order.astype(np.int32),
@@ -99,11 +112,30 @@ def pack_numpy(
         context_lens=ends.astype(np.int32),
         block_tables=block_tables,
         max_seqlen_q=int(lens.max()) if rows else 0,
-        max_seqlen_k=int(ends.max()) if rows else 0,
+        max_seqlen_k=int(host_k.max()) if rows else 0,
         cu_seqlens_q_host=[int(x) for x in cu_q],
-        cu_seqlens_k_host=[int(x) for x in cu_k],
+        cu_seqlens_k_host=[0, *np.cumsum(host_k).tolist()],
         decode_query_len=query_len,
     )
+
+
+def move_back(packed: dict, num_back, block_size: int) -> dict:
+    """``ModelRunner._move_back`` (``model_runner.py:527-551``) on an uncorrected packing: each moved row's tokens
+    shift back by its rejected-draft count; positions, context lengths, ``cu_seqlens_k`` and the slots (looked up
+    again in the padded block table) follow. ``num_back`` is in scheduler order; every row has a block list."""
+    out = dict(packed)
+    order = packed["order"].astype(np.int64)
+    back = np.asarray(num_back, dtype=np.int64)[order]  # batch order
+    cu_q = packed["cu_seqlens_q"].astype(np.int64)
+    token_rows = np.repeat(np.arange(order.size), np.diff(cu_q))
+    positions = packed["positions"] - back[token_rows]
+    context_lens = packed["context_lens"].astype(np.int64) - back
+    out["positions"] = positions
+    out["context_lens"] = context_lens.astype(np.int32)
+    out["cu_seqlens_k"] = np.concatenate([[0], np.cumsum(context_lens)]).astype(np.int32)
+    blocks = packed["block_tables"][token_rows, positions // block_size].astype(np.int64)
+    out["slot_mapping"] = (blocks * block_size + positions % block_size).astype(np.int32)
+    return out
 
 
 def pack_loops(num_cached, num_new, block_lists: list[list[int]], block_size: int, sampling=None) -> dict:

@@ -29,13 +29,13 @@ def test_library_exports_every_declared_symbol():
     lib = _capi.load()
     missing = [n for n in declared() if not hasattr(lib, n)]
     assert not missing, f"declared in lvattn.h but not exported: {missing}"
-    assert lib.lv_abi_version() == 5
+    assert lib.lv_abi_version() == 6
     assert all(n in _capi._PROTOTYPES for n in declared()), "every declared function has a ctypes prototype"
 
 
 def test_bad_arguments_raise_with_the_library_message():
     with pytest.raises(_capi.LvError, match="rows; 1 to 4096"):
-        _capi.call("lv_pack", None, None, None, None, 0, 1, 16, 0, 0, *[None] * 9, 0, None)
+        _capi.call("lv_pack", None, None, None, None, 0, 1, 16, 0, 0, *[None] * 10, 0, None)
     with pytest.raises(_capi.LvError, match="block_size must be positive"):
         _capi.call("lv_store_kvcache", None, None, 0, 0, 1, 1, 8, None, None, 0, 0, 0, 0, None, 2, None)
     with pytest.raises(_capi.LvError, match="head_dim 96"):
@@ -58,3 +58,4 @@ def test_workspace_query_sizes():
     big = _capi.query("lv_paged_attention_workspace_bytes", 16, 16, 32, 8, 128, 131072, 1)
     assert small <= 512 and big > 1 << 20
     assert _capi.query("lv_paged_attention_workspace_bytes", 0, 0, 8, 2, 64, 64, 1) == 0
+

@@ -277,10 +277,17 @@ def test_decode_replays_in_a_graph(cuda):
         torch.testing.assert_close(out, eager, atol=0, rtol=0)
 
 
-def test_mixed_step_replays_in_a_graph(cuda):
+@pytest.mark.parametrize("schedule", ["serial", "overlap"])
+def test_mixed_step_replays_in_a_graph(cuda, schedule, monkeypatch):
     """A captured mixed step (work-list plan, prompt kernel, decode kernel, split-K merge) replays with new queries
-    and cache contents; each replay equals an eager call, with eager work between replays."""
+    and cache contents; each replay equals an eager call, with eager work between replays. Under the overlapped
+    schedule the decode items run on the library's second stream, forked from and joined back into the capturing
+    stream by events, so the capture holds both branches."""
+    from lvattn import backend as B
+
+    sched = B.SCHEDULE_OVERLAP if schedule == "overlap" else B.SCHEDULE_SERIAL
     b = MI355XAttention(32, 128, 1 / math.sqrt(128), 8)
+    monkeypatch.setattr(b, "_schedule", lambda context, elem_bytes: sched)
     bs, width = 256, 24
     num_cached, num_new = [300, 5000, 0, 1999], [1, 1, 700, 64]
     tables = [[r * width + j for j in range(width)] for r in range(4)]
@@ -306,6 +313,74 @@ def test_mixed_step_replays_in_a_graph(cuda):
         eager = b.forward(q, kn, vn, kc, vc, ctx)
         torch.cuda.synchronize()
         torch.testing.assert_close(out, eager, atol=0, rtol=0)
+
+
+def test_decode_of_more_rows_than_the_planner_holds(cuda):
+    """A decode step of 5000 short rows (over the 4096 rows the device work list holds): one workgroup per (row,
+    split, head group) without a plan, checked against the oracle, beside rows of 0 and 1 keys."""
+    gen = torch.Generator().manual_seed(12)
+    rows = 5000
+    lens = torch.randint(1, 70, (rows,), generator=gen).tolist()
+    lens[17], lens[4999] = 1, 69
+    b = MI355XAttention(H, 64, SCALE, HKV)
+    width = max(-(-n // BS) for n in lens)
+    perm = torch.randperm(rows * width, generator=gen).tolist()
+    tables = [perm[r * width:r * width + -(-n // BS)] + [-1] * (width - -(-n // BS)) for r, n in enumerate(lens)]
+    qs, kf, vf, kn, vn, kc, vc, slots = paged_step([n - 1 for n in lens], [1] * rows, tables, rows * width, heads=H,
+                                                   kv_heads=HKV, dim=64, bs=BS, device=cuda, dtype=torch.bfloat16)
+    b.store_kvcache(kn, vn, kc, vc, slots)
+    ctx = Context(context_lens=torch.tensor(lens, dtype=torch.int32, device=cuda),
+                  block_tables=torch.tensor(tables, dtype=torch.int32, device=cuda))
+    out = b.decode(torch.cat(qs), kc, vc, ctx)
+    torch.cuda.synchronize()
+    math_ = A.TorchMath(H, 64, SCALE, HKV)
+    want = A.decode_in_row_chunks(math_, torch.cat(qs).cpu(), kc.cpu(), vc.cpu(), ctx.context_lens.cpu(),
+                                  ctx.block_tables.cpu(), rows_per_chunk=500)
+    check(out, want, torch.bfloat16)
+
+
+def test_a_decoder_step_whose_rows_all_carry_drafts(cuda):
+    """Rows verifying drafts (three queries each) in a decoder model: the packer marks the step is_prefill, as the
+    reference does (model_runner.py:380-384), so the mixed kernel attends each row's queries causally over its
+    keys; some rows also had drafts of the previous step rejected, and the pack kernel moves them back
+    (_move_back, model_runner.py:527-551). Checked against the dense oracle on the keys each query sees."""
+    from lvattn import Packer
+
+    gen = torch.Generator().manual_seed(13)
+    k = 2
+    num_cached = [40, 7, 100, 63]
+    back = [0, 2, 1, 0]  # drafts of the previous step rejected, per row
+    num_new = [1 + k] * 4
+    bs = BS
+    lists, at = [], 0
+    for c, n in zip(num_cached, num_new):
+        need = -(-(c + n) // bs)
+        lists.append(list(range(at, at + need)))
+        at += need
+    packer = Packer(cuda, bs)
+    back_dev = torch.tensor(back, dtype=torch.int32, device=cuda)
+    positions, fields = packer.pack(num_cached, num_new, lists, num_speculative_tokens=k, num_back=back_dev)
+    assert fields["is_prefill"] and fields["logits_indices"].numel() == 4 * (k + 1)
+    order = fields.pop("order").cpu().tolist()
+    starts = [c - r for c, r in zip(num_cached, back)]  # where each row's tokens really start
+    assert positions.cpu().tolist() == [starts[s] + j for s in order for j in range(num_new[s])]
+    b = MI355XAttention(H, 64, SCALE, HKV)
+    kc = torch.zeros(at, bs, HKV, 64, dtype=torch.bfloat16, device=cuda)
+    vc = torch.zeros_like(kc)
+    keys = [randn(starts[s] + num_new[s], HKV, 64, gen=gen, device=cuda, dtype=torch.bfloat16) for s in order]
+    vals = [randn(starts[s] + num_new[s], HKV, 64, gen=gen, device=cuda, dtype=torch.bfloat16) for s in order]
+    for r, s in enumerate(order):  # the prefix the previous steps stored
+        pre = torch.tensor(slots_for(lists[s], bs, 0, starts[s]), dtype=torch.long, device=cuda)
+        kc.view(-1, HKV, 64)[pre] = keys[r][:starts[s]]
+        vc.view(-1, HKV, 64)[pre] = vals[r][:starts[s]]
+    k_new = torch.cat([kk[starts[s]:] for kk, s in zip(keys, order)])
+    v_new = torch.cat([vv[starts[s]:] for vv, s in zip(vals, order)])
+    qs = [randn(num_new[s], H, 64, gen=gen, device=cuda, dtype=torch.bfloat16) for s in order]
+    b.store_kvcache(k_new, v_new, kc, vc, fields["slot_mapping"])
+    ctx = Context(**{kk: vv for kk, vv in fields.items() if kk in Context.__slots__})
+    out = b.forward(torch.cat(qs), k_new, v_new, kc, vc, ctx)
+    torch.cuda.synchronize()
+    check(out, dense_expected(qs, keys, vals, SCALE), torch.bfloat16)
 
 
 def _wide_step(cuda, num_cached, num_new, bs=16, seed=0):
@@ -370,45 +445,3 @@ def test_a_mixed_step_of_many_decode_rows_under_both_schedules(cuda, monkeypatch
         torch.testing.assert_close(out.float().cpu(), want, atol=2e-2, rtol=1e-2)
         outs[sched] = out
     assert torch.equal(outs[B.SCHEDULE_SERIAL], outs[B.SCHEDULE_OVERLAP])
-
-
-@pytest.mark.parametrize("name", ["qwen3_8b_mixed", "qwen3_8b_decode", "qwen3_8b_long", "qwen3_8b_prefill",
-                                  "qwen3_0_6b_mixed"])
-def test_full_size_steps_on_sampled_rows(cuda, name):
-    """The measured steps at full size (pack, store, attention as the bench runs them): sampled rows against the
-    fp32 oracle on each row's gathered keys -- the shortest, a middle and the longest decode rows, and the first,
-    middle and last queries of every prompt chunk (each query sees its row's keys up to its own position)."""
-    from lvattn import Packer
-    from lvattn import workloads as W
-
-    wl = W.WORKLOADS[name]()
-    t = W.materialize(wl, cuda)
-    b = MI355XAttention(wl.num_heads, wl.head_dim, wl.scale, wl.num_kv_heads)
-    _, fields = Packer(cuda, wl.block_size).pack(wl.num_cached, wl.num_new, wl.block_lists)
-    order = fields.pop("order").cpu().tolist()
-    b.store_kvcache(t.k_new, t.v_new, t.k_cache, t.v_cache, fields["slot_mapping"])
-    ctx = Context(**{k: v for k, v in fields.items() if k in Context.__slots__})
-    out = b.forward(t.q, t.k_new, t.v_new, t.k_cache, t.v_cache, ctx)
-    torch.cuda.synchronize()
-    assert torch.isfinite(out).all()
-    cu_q = fields["cu_seqlens_q"].cpu().tolist()
-    decode = [i for i in range(len(order)) if wl.num_new[order[i]] == 1]
-    by_len = sorted(decode, key=lambda i: wl.num_cached[order[i]])
-    picks = [(i, 0) for i in sorted({by_len[0], by_len[len(by_len) // 2], by_len[-1]})] if decode else []
-    for i in range(len(order)):
-        lq = wl.num_new[order[i]]
-        if lq > 1:
-            picks += [(i, j) for j in (0, lq // 2, lq - 1)]
-    bs = wl.block_size
-    for i, j in picks:
-        s = order[i]
-        lq, lk = wl.num_new[s], wl.num_cached[s] + wl.num_new[s]
-        n = lk - lq + j + 1  # keys query j of the row sees
-        pos = torch.arange(n, device=cuda)
-        pages = torch.tensor(wl.block_lists[s], dtype=torch.long, device=cuda)[pos // bs]
-        k = t.k_cache[pages, pos % bs].cpu().float()
-        v = t.v_cache[pages, pos % bs].cpu().float()
-        q = t.q[cu_q[i] + j:cu_q[i] + j + 1].cpu().float()
-        want = A.dense_attention(q, k, v, wl.scale, causal=False)
-        got = out[cu_q[i] + j:cu_q[i] + j + 1].float().cpu()
-        torch.testing.assert_close(got, want, **TOL[torch.bfloat16], msg=lambda m: f"{name} row {i} query {j}: {m}")

@@ -88,3 +88,45 @@ def test_many_rows(cuda):
 def test_config_steps(cuda, name):
     wl = W.WORKLOADS[name]()
     check(Packer(cuda, wl.block_size), wl.num_cached, wl.num_new, wl.block_lists, wl.block_size)
+
+
+@pytest.mark.parametrize("seed", [4, 5])
+def test_rows_moved_back_by_rejected_drafts_match_the_oracle(cuda, seed):
+    """Per-row rejected-draft counts handed over on the device (num_back): positions, slots, context lengths and
+    cu_seqlens_k follow the corrected starts (model_runner.py:379-385, 527-551); host lengths stay upper bounds."""
+    rng = random.Random(seed)
+    bs, k = 8, 3
+    packer = Packer(cuda, bs)
+    for _ in range(5):
+        cached, new, lists = P.random_rows(rng, bs)
+        new = [n if n > 1 else 1 + k for n in new]
+        lists = [lst + [lst[-1]] * 2 if lst else lst for lst in lists]
+        back = [rng.randint(0, min(k, c)) if n == 1 + k else 0 for c, n in zip(cached, new)]
+        is_prompt = [n != 1 + k for n in new]
+        positions, ctx = packer.pack(cached, new, lists, num_speculative_tokens=k, is_prompt=is_prompt,
+                                     num_back=torch.tensor(back, dtype=torch.int32, device=cuda))
+        torch.cuda.synchronize()
+        want = P.pack_numpy(cached, new, lists, bs, k, num_back=back)
+        assert positions.tolist() == want["positions"].tolist()
+        for key in ("cu_seqlens_q", "cu_seqlens_k", "context_lens", "slot_mapping", "order"):
+            assert ctx[key].tolist() == want[key].tolist(), key
+        assert ctx["cu_seqlens_k_host"] == want["cu_seqlens_k_host"] and ctx["max_seqlen_k"] == want["max_seqlen_k"]
+
+
+def test_a_page_past_a_short_block_list_stores_nothing(cuda):
+    """Called through the C ABI with a block list shorter than its row (which Packer refuses on the host), the pack
+    kernel gives the uncovered tokens slot -1 instead of reading the next row's blocks."""
+    from lvattn import _capi
+
+    i32 = dict(dtype=torch.int32, device=cuda)
+    cached, new = torch.tensor([14, 0], **i32), torch.tensor([4, 2], **i32)
+    indptr, ids = torch.tensor([0, 1, 2], **i32), torch.tensor([5, 9], **i32)  # row 0 needs 3 blocks of 8, has 1
+    out = {n: torch.full((8,), -7, **i32) for n in ("order", "cu_q", "cu_k", "slots", "lens", "tables")}
+    positions = torch.zeros(6, dtype=torch.int64, device=cuda)
+    _capi.call("lv_pack", cached.data_ptr(), new.data_ptr(), indptr.data_ptr(), ids.data_ptr(), 2, 1, 8, 1, 6,
+               out["order"].data_ptr(), out["cu_q"].data_ptr(), out["cu_k"].data_ptr(), positions.data_ptr(),
+               out["slots"].data_ptr(), out["lens"].data_ptr(), out["tables"].data_ptr(), None, None, None, 0,
+               _capi.stream_of(cuda))
+    torch.cuda.synchronize()
+    assert positions.tolist() == [14, 15, 16, 17, 0, 1]
+    assert out["slots"][:6].tolist() == [-1, -1, -1, -1, 72, 73]  # row 0's page 1 and 2 are past its list

@@ -69,3 +69,78 @@ def test_store_at_config_size(cuda, name):
     other = torch.ones(flat_k.size(0), dtype=torch.bool, device=cuda)
     other[slots.long()] = False
     assert torch.equal(after_k[other], before_k[other]) and torch.equal(after_v[other], before_v[other])
+
+
+def _snapshot_check(cache_before, cache_after, pages, oracle_write):
+    """The touched pages after the GPU store equal the oracle's scatter applied to their snapshot, bit for bit."""
+    want = cache_before.clone()
+    oracle_write(want)
+    assert torch.equal(cache_after, want)
+
+
+@pytest.mark.parametrize("name", ["qwen3_8b_mixed", "qwen3_0_6b_mixed"])
+def test_store_of_a_mixed_step_matches_the_oracle_on_its_pages(cuda, name):
+    """A mixed step's new K/V at full size (the Qwen3-8B step's 8,192 tokens: 2048 decode rows and four 1536-token
+    chunks, 32 MiB each of K and V into a 24,000-page pool): the slots come from the packing oracle; every page the
+    step touches is copied to the host before and after the GPU store, and the after-copy must equal the oracle's
+    scatter (TorchAttention.store_kvcache, torch_backend.py:34-48) applied to the before-copy, bit for bit. The rest
+    of the pool is checked unchanged by per-row checksums."""
+    import numpy as np
+
+    from oracle import pack as P
+
+    wl = W.WORKLOADS[name]()
+    t = W.materialize(wl, cuda)
+    bs = wl.block_size
+    packed = P.pack_numpy(wl.num_cached, wl.num_new, wl.block_lists, bs)
+    slots = packed["slot_mapping"].astype(np.int64)
+    order = packed["order"]
+    # the step's new tokens in batch order (the pack kernel's token order), as the bench hands them over
+    k_new, v_new = t.k_new, t.v_new
+    pages = np.unique(slots // bs)
+    remap = {int(p): i for i, p in enumerate(pages)}
+    local = torch.tensor([remap[int(s // bs)] * bs + int(s % bs) for s in slots], dtype=torch.long)
+    sel = torch.tensor(pages, dtype=torch.long, device=cuda)
+    k_before, v_before = t.k_cache[sel].cpu(), t.v_cache[sel].cpu()
+    others = torch.ones(wl.pool, dtype=torch.bool, device=cuda)
+    others[sel] = False
+    sum_k = t.k_cache[others].view(int(others.sum()), -1).sum(dim=1, dtype=torch.float64)
+    sum_v = t.v_cache[others].view(int(others.sum()), -1).sum(dim=1, dtype=torch.float64)
+    slot_dev = torch.tensor(slots, dtype=torch.int32, device=cuda)
+    MI355XAttention(wl.num_heads, wl.head_dim, wl.scale, wl.num_kv_heads).store_kvcache(
+        k_new, v_new, t.k_cache, t.v_cache, slot_dev)
+    torch.cuda.synchronize()
+    k_host, v_host = k_new.cpu(), v_new.cpu()
+    _snapshot_check(k_before, t.k_cache[sel].cpu(), pages, lambda c: S.store_kvcache(k_host, v_host, c, c.clone(),
+                                                                                      local.numpy()))
+    _snapshot_check(v_before, t.v_cache[sel].cpu(), pages, lambda c: S.store_kvcache(v_host, k_host, c, c.clone(),
+                                                                                      local.numpy()))
+    assert torch.equal(t.k_cache[others].view(int(others.sum()), -1).sum(dim=1, dtype=torch.float64), sum_k)
+    assert torch.equal(t.v_cache[others].view(int(others.sum()), -1).sum(dim=1, dtype=torch.float64), sum_v)
+    assert len(order) == wl.rows and slots.size == wl.tokens
+
+
+def test_store_latents_of_the_deepseek_v2_lite_step(cuda):
+    """DeepSeek-V2-Lite's decode step at full size: 128 latents of 576 entries into a 34,000-page pool of 64-latent
+    pages, plus a -1 slot; the touched pages after the GPU store equal the oracle's scatter
+    (torch_backend.py:50-60) on their snapshot, bit for bit, and the rest of the pool is unchanged."""
+    wl = W.deepseek_v2_lite_mla()
+    t = W.materialize(wl, cuda)
+    bs = wl.block_size
+    ends = wl.context_lens
+    slots = [wl.block_lists[r][(e - 1) // bs] * bs + (e - 1) % bs for r, e in enumerate(ends)]
+    slots[5] = -1  # a padding token stores nothing
+    pages = sorted({s // bs for s in slots if s >= 0})
+    remap = {p: i for i, p in enumerate(pages)}
+    local = [remap[s // bs] * bs + s % bs if s >= 0 else -1 for s in slots]
+    sel = torch.tensor(pages, dtype=torch.long, device=cuda)
+    before = t.k_cache[sel].cpu()
+    others = torch.ones(wl.pool, dtype=torch.bool, device=cuda)
+    others[sel] = False
+    checksum = t.k_cache[others].view(int(others.sum()), -1).sum(dim=1, dtype=torch.float64)
+    MI355XAttention(wl.num_heads, wl.latent_dim, wl.scale, wl.num_heads).store_latents(
+        t.k_new, t.k_cache, torch.tensor(slots, dtype=torch.int32, device=cuda))
+    torch.cuda.synchronize()
+    latent = t.k_new.cpu()
+    _snapshot_check(before, t.k_cache[sel].cpu(), pages, lambda c: S.store_latents(latent, c, local))
+    assert torch.equal(t.k_cache[others].view(int(others.sum()), -1).sum(dim=1, dtype=torch.float64), checksum)

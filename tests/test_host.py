@@ -189,3 +189,127 @@ def test_graph_staging_pads_rows_with_no_context():
     assert (buf[3 * bs + 7:] == -9).all()
     with pytest.raises(ValueError, match="at most bs rows"):
         _hoststage.stage_graph_rows([0] * 9, [[]] * 9, buf.ctypes.data, buf.size, bs, q)
+
+
+class _HostBuffers:
+    """StagingBuffers on plain host memory (no pinned memory, no device): Packer.stage's host logic on a CPU."""
+
+    def __init__(self):
+        self._host = {}
+
+    def host_view(self, name, n, dtype):
+        buf = self._host.get(name)
+        if buf is None or buf.numel() < n:
+            buf = self._host[name] = torch.empty(max(n, 256), dtype=dtype)
+        return buf[:n].numpy()
+
+    def upload(self, name, n, dtype):
+        return self._host[name][:n].clone()
+
+
+def host_packer(block_size, decodes_latents=False):
+    from lvattn import Packer
+
+    packer = Packer.__new__(Packer)
+    packer.block_size, packer.decodes_latents, packer.buffers = block_size, decodes_latents, _HostBuffers()
+    return packer
+
+
+def test_a_block_list_that_does_not_cover_its_row_is_refused():
+    """A row whose block list is shorter than its num_cached + num_new tokens need would make the pack kernel read
+    another row's blocks; the packer refuses it on the host (rows without a list, as in warmup, are fine)."""
+    packer = host_packer(16)
+    plan = packer.stage([0, 31, 5], [16, 1, 3], [[4], [7, 8], []])
+    assert plan.rows == 3 and plan.slot_count == 17
+    with pytest.raises(ValueError, match="row 1's block list holds 1 blocks; its 31 \\+ 2 tokens need 3"):
+        packer.stage([0, 31, 5], [16, 2, 3], [[4], [7, 8][:1], []])
+    with pytest.raises(ValueError, match="row 0's block list holds 1 blocks; its 0 \\+ 17 tokens need 2"):
+        packer.stage([0], [17], [[4]])
+    with pytest.raises(ValueError, match="row 1 has num_cached -1"):
+        packer.stage([0, -1], [1, 1], [[4], [5]])
+
+
+def test_the_step_kind_follows_the_reference_rule_for_drafts():
+    """model_runner.py:380-384: a step is is_prefill with any prompt row, or with drafts unless the model decodes
+    latents and every row has the same query length. Draft rows sample drafts + 1 logits rows by default."""
+    k = 2
+    packer = host_packer(16)
+    plan = packer.stage([10, 20], [3, 3], [[0], [1, 2]], num_speculative_tokens=k)  # both rows verify 2 drafts
+    assert plan.host["is_prefill"] and plan.logits == 6  # a decoder model: drafts go to the prefill path
+    plan = packer.stage([10, 20], [1, 1], [[0], [1, 2]], num_speculative_tokens=k)
+    assert not plan.host["is_prefill"] and plan.logits == -1
+    plan = packer.stage([10, 0], [3, 3], [[0], [1]], num_speculative_tokens=k, is_prompt=[False, True])
+    assert plan.host["is_prefill"] and plan.logits == 4  # the prompt samples one row, the draft row three
+    mla = host_packer(16, decodes_latents=True)
+    plan = mla.stage([10, 20], [3, 3], [[0], [1, 2]], num_speculative_tokens=k)
+    assert not plan.host["is_prefill"]  # uniform drafts: latent decode with 3 queries per row
+    plan = mla.stage([10, 20], [3, 2], [[0], [1, 2]], num_speculative_tokens=k)
+    assert plan.host["is_prefill"]  # ragged drafts: the prefill path
+
+
+def test_the_opt_in_index_checks(monkeypatch):
+    """LVATTN_CHECK=1: slots past the pool, table entries past the pool, key lengths a table does not cover and
+    inconsistent cu_seqlens raise ValueError before any launch (CPU tensors; nothing reaches the library)."""
+    from lvattn import checks
+
+    i32 = dict(dtype=torch.int32)
+    checks.check_slots(torch.tensor([-1, 0, 63], **i32), 4, 16)
+    with pytest.raises(ValueError, match=r"slot_mapping\[2\] = 64 is outside \[-1, 64\)"):
+        checks.check_slots(torch.tensor([-1, 0, 64], **i32), 4, 16)
+    with pytest.raises(ValueError, match=r"slot_mapping\[0\] = -2"):
+        checks.check_slots(torch.tensor([-2], **i32), 4, 16)
+    checks.check_tables(torch.tensor([[0, 3], [2, -1]], **i32), 4)
+    with pytest.raises(ValueError, match=r"block_tables\[1, 1\] = 4 is outside \[-1, 4\)"):
+        checks.check_tables(torch.tensor([[0, 3], [2, 4]], **i32), 4)
+    bt = torch.tensor([[0, 3], [2, -1]], **i32)
+    checks.check_key_lengths(torch.tensor([32, 16], **i32), bt, 16)
+    with pytest.raises(ValueError, match=r"row 1 needs 2 blocks for its 17 keys but block_tables\[1, 1\] is -1"):
+        checks.check_key_lengths(torch.tensor([32, 17], **i32), bt, 16)
+    with pytest.raises(ValueError, match=r"context_lens\[0\] = 33 is outside \[0, 32\]"):
+        checks.check_key_lengths(torch.tensor([33, 1], **i32), bt, 16)
+    checks.check_query_rows(torch.tensor([0, 1, 4], **i32), torch.tensor([0, 9, 13], **i32), 4)
+    with pytest.raises(ValueError, match="row 1 has 3 queries but only 2 keys"):
+        checks.check_query_rows(torch.tensor([0, 1, 4], **i32), torch.tensor([0, 9, 11], **i32), 4)
+    with pytest.raises(ValueError, match="ends at 4, but there are 5"):
+        checks.check_query_rows(torch.tensor([0, 1, 4], **i32), torch.tensor([0, 9, 13], **i32), 5)
+
+    monkeypatch.setenv("LVATTN_CHECK", "1")
+    b = MI355XAttention(8, 64, 0.1, 2)
+    k_cache = torch.zeros(4, 16, 2, 64, dtype=torch.bfloat16)
+    key = torch.zeros(2, 2, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="outside"):
+        b.store_kvcache(key, key, k_cache, k_cache.clone(), torch.tensor([5, 70], **i32))
+    ctx = Context(context_lens=torch.tensor([40], **i32), block_tables=torch.tensor([[0, 1]], **i32))
+    with pytest.raises(ValueError, match="outside"):
+        b.decode(torch.zeros(1, 8, 64, dtype=torch.bfloat16), k_cache, k_cache.clone(), ctx)
+    ctx = Context(cu_seqlens_q=torch.tensor([0, 3], **i32), cu_seqlens_k=torch.tensor([0, 2], **i32),
+                  block_tables=torch.tensor([[0]], **i32), max_seqlen_q=3, max_seqlen_k=2)
+    with pytest.raises(ValueError, match="3 queries but only 2 keys"):
+        b.prefill(torch.zeros(3, 8, 64, dtype=torch.bfloat16), None, None, k_cache, k_cache.clone(), ctx)
+    lat = torch.zeros(2, 16, 576, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="outside"):
+        MI355XAttention(16, 576, 0.1, 16).store_latents(torch.zeros(1, 576, dtype=torch.bfloat16), lat,
+                                                         torch.tensor([32], **i32))
+
+
+def test_decode_refuses_rows_that_carry_drafts():
+    """decode takes one query per row; a step with drafts is is_prefill (the reference sends it to prefill)."""
+    b = MI355XAttention(8, 64, 0.1, 2)
+    ctx = Context(context_lens=torch.tensor([5, 6], dtype=torch.int32),
+                  block_tables=torch.tensor([[0], [1]], dtype=torch.int32))
+    cache = torch.zeros(2, 16, 2, 64, dtype=torch.bfloat16)
+    with pytest.raises(AssertionError, match="one query per row"):
+        b.decode(torch.zeros(6, 8, 64, dtype=torch.bfloat16), cache, cache, ctx)
+
+
+def test_the_merge_keeps_the_reference_signature():
+    """lvattn.merge_attention_ / merge_attention replace lean_vllm.attention.merge's (merge.py:8,18): same
+    parameters, same defaults, same return convention (None for the in-place form)."""
+    import inspect
+
+    from lvattn import merge_attention, merge_attention_
+
+    sig = inspect.signature(merge_attention_)
+    assert list(sig.parameters) == ["o_a", "lse_a", "o_b", "lse_b", "out"]
+    assert sig.parameters["out"].default is None
+    assert list(inspect.signature(merge_attention).parameters) == ["o_a", "lse_a", "o_b", "lse_b"]

@@ -280,3 +280,52 @@ def test_planted_mistakes_are_rejected(gen, mutant):
     want = expected(qs, ks, vs)
     torch.testing.assert_close(good, want, atol=TOL, rtol=TOL)
     assert not torch.allclose(bad, want, atol=5 * TOL)
+
+
+# ------------------------------------------------------------------------------ decode over slices of rows
+
+def _chunked_width_floor(math_, q, k_cache, v_cache, context_lens, block_tables, rows_per_chunk):
+    """A planted mistake: each slice's table narrowed to floor(longest / bs) pages (at least one) instead of ceil."""
+    outs, bs = [], k_cache.size(1)
+    for r0 in range(0, q.size(0), rows_per_chunk):
+        lens = context_lens[r0:r0 + rows_per_chunk]
+        sub = A.context(context_lens=lens, block_tables=block_tables[r0:r0 + rows_per_chunk, :max(1, int(lens.max()) // bs)])
+        outs.append(math_.decode(q[r0:r0 + rows_per_chunk], k_cache, v_cache, sub))
+    return torch.cat(outs)
+
+
+def _chunked_tables_shifted(math_, q, k_cache, v_cache, context_lens, block_tables, rows_per_chunk):
+    """A planted mistake: each slice reads the table rows of the slice one row later."""
+    outs, bs = [], k_cache.size(1)
+    for r0 in range(0, q.size(0), rows_per_chunk):
+        lens = context_lens[r0:r0 + rows_per_chunk]
+        width = -(-int(lens.max()) // bs)
+        rows = torch.arange(r0 + 1, r0 + 1 + lens.numel()).clamp(max=block_tables.size(0) - 1)
+        sub = A.context(context_lens=lens, block_tables=block_tables[rows, :width])
+        outs.append(math_.decode(q[r0:r0 + rows_per_chunk], k_cache, v_cache, sub))
+    return torch.cat(outs)
+
+
+@pytest.mark.parametrize("rows_per_chunk", [1, 3, 7, 10])
+def test_decode_in_row_chunks_equals_decode_of_the_whole_batch(gen, rows_per_chunk):
+    """``decode_in_row_chunks`` (the CPU baseline's decode) against ``TorchMath.decode`` of the whole batch and the
+    dense oracle: seven rows whose lengths end mid-page, on a page boundary and in the table's last page, sliced
+    into chunks of 1, 3, 7 and 10 rows. Each slice's table is narrowed to its own longest row, so slices whose
+    longest row ends mid-page (3 BS + 5 in the first chunk of three) and slices that end on a page boundary are both
+    exercised; two planted mistakes (a floor for the slice's page count, table rows shifted by one) are rejected."""
+    lens = [3 * BS + 5, 2, BS, 6 * BS, BS + 1, 4 * BS - 1, 5]
+    width = 6
+    pages = torch.randperm(len(lens) * width, generator=gen).tolist()
+    tables = [pages[r * width:r * width + -(-n // BS)] + [-1] * (width - -(-n // BS)) for r, n in enumerate(lens)]
+    qs, ks, vs, kc, vc, _ = paged_step(gen, [n - 1 for n in lens], [1] * len(lens), tables, len(lens) * width)
+    q = torch.cat(qs)
+    cl, bt = torch.tensor(lens, dtype=torch.int32), torch.tensor(tables, dtype=torch.int32)
+    m = A.TorchMath(H, D, SCALE, HKV)
+    whole = m.decode(q, kc, vc, A.context(context_lens=cl, block_tables=bt))
+    torch.testing.assert_close(whole, expected(qs, ks, vs), atol=TOL, rtol=TOL)
+    got = A.decode_in_row_chunks(m, q, kc, vc, cl, bt, rows_per_chunk)
+    torch.testing.assert_close(got, whole, atol=1e-5, rtol=1e-5)
+    if rows_per_chunk < len(lens):  # slices narrower than the batch: the mistakes change what a slice reads
+        for mutant in (_chunked_width_floor, _chunked_tables_shifted):
+            bad = mutant(m, q, kc, vc, cl, bt, rows_per_chunk)
+            assert not torch.allclose(bad, whole, atol=5 * TOL), mutant.__name__

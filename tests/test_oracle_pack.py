@@ -131,3 +131,29 @@ def test_a_planted_off_by_one_is_caught():
     bad = P.pack_numpy(cached, new, shifted, 8)
     assert got["slot_mapping"].tolist() == want["slot_mapping"]
     assert bad["slot_mapping"].tolist() != want["slot_mapping"]
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_rejected_drafts_move_rows_back_as_the_device_correction_does(seed):
+    """Rows whose previous drafts were rejected: the host-side correction (``starts[moved] -= num_rejected``,
+    model_runner.py:379-385) that ``pack_numpy(num_back=...)`` applies equals the device-side ``_move_back``
+    (:527-551) applied to the uncorrected packing; host lengths stay the uncorrected upper bounds."""
+    rng = random.Random(seed)
+    bs = 8
+    cached, new, lists = P.random_rows(rng, bs)
+    k = 3
+    new = [n if n > 1 else 1 + k for n in new]  # decode rows verify k drafts
+    lists = [[*lst, *range(50_000 + 10 * i, 50_000 + 10 * i + 2)] for i, lst in enumerate(lists)]
+    back = [rng.randint(0, min(k, c)) if n == 1 + k else 0 for c, n in zip(cached, new)]
+    raw = P.pack_numpy(cached, new, lists, bs, num_speculative_tokens=k)
+    got = P.pack_numpy(cached, new, lists, bs, num_speculative_tokens=k, num_back=back)
+    want = P.move_back(raw, back, bs)
+    for key in ("positions", "slot_mapping", "context_lens", "cu_seqlens_k", "cu_seqlens_q", "order"):
+        assert got[key].tolist() == want[key].tolist(), key
+    assert got["cu_seqlens_k_host"] == raw["cu_seqlens_k_host"] and got["max_seqlen_k"] == raw["max_seqlen_k"]
+    host_fix = P.pack_numpy([c - b for c, b in zip(cached, back)], new, lists, bs, num_speculative_tokens=k)
+    assert got["positions"].tolist() == host_fix["positions"].tolist()
+    if any(back):  # a planted mistake (the counts taken in batch order instead of scheduler order) is told apart
+        wrong = P.move_back(raw, [back[i] for i in raw["order"]], bs)
+        assert wrong["positions"].tolist() != want["positions"].tolist() or raw["order"].tolist() == sorted(
+            raw["order"].tolist())
