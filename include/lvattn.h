@@ -129,6 +129,26 @@ int lv_paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h, co
                        void* workspace, size_t workspace_bytes, int32_t schedule, int32_t prompt_workgroups,
                        int32_t dtype, void* stream);
 
+/* The same step with no workspace argument and no allocation of any kind. No counterpart in the reference: for
+ * callers that cannot call hipMalloc -- code under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation. The work list, its counters and the split-K partials live in a static device array of
+ * LV_STATIC_WORKSPACE_BYTES that each GPU the library runs on holds until the process ends; a step needing more
+ * (lv_paged_attention_workspace_bytes larger than that; the split-K sizing keeps steps of up to 4096 rows at any
+ * context length under 9 MiB) is refused with LV_EINVAL. The kernels clear what must start at zero themselves
+ * (the plan kernel zeroes the persistent grid's ticket), so no memset is recorded into a captured graph. Every call
+ * on one GPU shares that GPU's array, which keeps the last call's contents: calls that overlap on one GPU (two
+ * streams, two host threads, or a graph replay beside an eager call) race. Results equal lv_paged_attention's for
+ * the same arguments. */
+#define LV_STATIC_WORKSPACE_BYTES (16u << 20)
+int lv_paged_attention_static(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_cache,
+                              const void* v_cache, int64_t cache_stride_block, int64_t cache_stride_token,
+                              int64_t cache_stride_head, int32_t block_size, const int32_t* block_tables,
+                              int64_t table_stride, const int32_t* cu_seqlens_q, const int32_t* seqlens_k,
+                              const int32_t* cu_seqlens_k, int32_t num_rows, int32_t num_tokens, int32_t num_heads,
+                              int32_t num_kv_heads, int32_t head_dim, float scale, int32_t max_seqlen_q,
+                              int32_t max_seqlen_k, void* out, int64_t out_stride_t, int64_t out_stride_h,
+                              int32_t schedule, int32_t prompt_workgroups, int32_t dtype, void* stream);
+
 /* ---------------------------------------------------------------------------------------------------------
  * Attention over packed keys (no pages). Replaces AttentionBackend.prefill without block tables and
  * AttentionBackend.varlen_with_lse (lean_vllm/attention/abstract.py:148-164,187-204; math of TorchAttention.prefill

@@ -694,7 +694,42 @@ static int launch_d(const AttnParams& p, int d, int gs, bool listed, bool mixed,
   }
 }
 
-// One step, with the caller's workspace.
+// ---------------------------------------------------------------------------------------------------------
+// The workspace of lv_paged_attention_static: a file-scope device array (each GPU that loads the library holds its
+// own copy until the process ends). Host code must not pass the array's name to a kernel -- in host code it is a
+// stand-in, not a device address; its address on the current device comes from hipGetSymbolAddress, resolved once
+// per device and kept.
+static __device__ __align__(256) char scratch[LV_STATIC_WORKSPACE_BYTES];
+
+static void* scratch_on_current_device() {
+  static void* addr[64];
+  static std::mutex lock;
+  int dev = 0;
+  const hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error("paged_attention_static: hipGetDevice failed: %s", hipGetErrorString(e));
+    return nullptr;
+  }
+  if (dev < 0 || dev >= 64) {
+    set_error("paged_attention_static: device %d is past the 64 devices served", dev);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> g(lock);
+  if (!addr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t r = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (r != hipSuccess || !ptr) {
+      set_error("paged_attention_static: hipGetSymbolAddress of the static workspace failed on device %d: %s", dev,
+                hipGetErrorString(r));
+      return nullptr;
+    }
+    addr[dev] = ptr;
+  }
+  return addr[dev];
+}
+
+// One step, with the workspace given (workspace != nullptr or an empty shape) or, for static_ws, the device's
+// static workspace.
 static int paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_cache,
                            const void* v_cache, int64_t cache_stride_block, int64_t cache_stride_token,
                            int64_t cache_stride_head, int32_t block_size, const int32_t* block_tables,
@@ -702,7 +737,7 @@ static int paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h
                            const int32_t* cu_seqlens_k, int32_t num_rows, int32_t num_tokens, int32_t num_heads,
                            int32_t num_kv_heads, int32_t head_dim, float scale, int32_t max_seqlen_q,
                            int32_t max_seqlen_k, void* out, int64_t out_stride_t, int64_t out_stride_h,
-                           void* workspace, size_t workspace_bytes, int32_t schedule,
+                           void* workspace, size_t workspace_bytes, bool static_ws, int32_t schedule,
                            int32_t prompt_workgroups, int32_t dtype, void* stream) {
   LV_REQUIRE(dtype == LV_DTYPE_BF16 || dtype == LV_DTYPE_F16, "paged_attention: dtype %d is not bf16 or fp16",
              dtype);
@@ -738,6 +773,15 @@ static int paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h
              kPlanMaxRows, num_rows);
   const bool listed = num_rows <= kPlanMaxRows;
   const Shape s = plan_shape(num_rows, num_tokens, num_heads, num_kv_heads, head_dim, max_seqlen_k, listed);
+  if (static_ws) {
+    LV_REQUIRE(s.bytes <= (size_t)LV_STATIC_WORKSPACE_BYTES,
+               "paged_attention_static: this step needs %zu bytes of workspace; the static workspace holds %zu "
+               "(LV_STATIC_WORKSPACE_BYTES): call lv_paged_attention with a workspace instead",
+               s.bytes, (size_t)LV_STATIC_WORKSPACE_BYTES);
+    workspace = scratch_on_current_device();
+    if (!workspace) return LV_EHIP;
+    workspace_bytes = LV_STATIC_WORKSPACE_BYTES;
+  }
   LV_REQUIRE(workspace_bytes >= s.bytes && (s.bytes == 0 || workspace),
              "paged_attention: workspace of %zu bytes given, %zu needed", workspace_bytes, s.bytes);
   LV_REQUIRE(aligned(workspace, 256), "paged_attention: workspace must be 256-byte aligned");
@@ -821,6 +865,22 @@ extern "C" int lv_paged_attention(const void* q, int64_t q_stride_t, int64_t q_s
   return paged_attention(q, q_stride_t, q_stride_h, k_cache, v_cache, cache_stride_block, cache_stride_token,
                          cache_stride_head, block_size, block_tables, table_stride, cu_seqlens_q, seqlens_k,
                          cu_seqlens_k, num_rows, num_tokens, num_heads, num_kv_heads, head_dim, scale, max_seqlen_q,
-                         max_seqlen_k, out, out_stride_t, out_stride_h, workspace, workspace_bytes, schedule,
+                         max_seqlen_k, out, out_stride_t, out_stride_h, workspace, workspace_bytes, false, schedule,
                          prompt_workgroups, dtype, stream);
+}
+
+extern "C" int lv_paged_attention_static(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_cache,
+                                         const void* v_cache, int64_t cache_stride_block, int64_t cache_stride_token,
+                                         int64_t cache_stride_head, int32_t block_size, const int32_t* block_tables,
+                                         int64_t table_stride, const int32_t* cu_seqlens_q, const int32_t* seqlens_k,
+                                         const int32_t* cu_seqlens_k, int32_t num_rows, int32_t num_tokens,
+                                         int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float scale,
+                                         int32_t max_seqlen_q, int32_t max_seqlen_k, void* out, int64_t out_stride_t,
+                                         int64_t out_stride_h, int32_t schedule, int32_t prompt_workgroups,
+                                         int32_t dtype, void* stream) {
+  return paged_attention(q, q_stride_t, q_stride_h, k_cache, v_cache, cache_stride_block, cache_stride_token,
+                         cache_stride_head, block_size, block_tables, table_stride, cu_seqlens_q, seqlens_k,
+                         cu_seqlens_k, num_rows, num_tokens, num_heads, num_kv_heads, head_dim, scale, max_seqlen_q,
+                         max_seqlen_k, out, out_stride_t, out_stride_h, nullptr, 0, true, schedule, prompt_workgroups,
+                         dtype, stream);
 }

@@ -31,6 +31,10 @@ _PROTOTYPES = {
                                           c_int64, _P, _P, _P, c_int32, c_int32, c_int32, c_int32, c_int32,
                                           c_float, c_int32, c_int32, _P, c_int64, c_int64, _P, c_size_t,
                                           c_int32, c_int32, c_int32, _P]),
+    "lv_paged_attention_static": (ctypes.c_int, [_P, c_int64, c_int64, _P, _P, c_int64, c_int64, c_int64, c_int32,
+                                                 _P, c_int64, _P, _P, _P, c_int32, c_int32, c_int32, c_int32,
+                                                 c_int32, c_float, c_int32, c_int32, _P, c_int64, c_int64, c_int32,
+                                                 c_int32, c_int32, _P]),
     "lv_merge_attn_states": (ctypes.c_int, [_P, c_int64, c_int64, _P, c_int64, c_int64, _P, c_int64, c_int64,
                                             _P, c_int64, c_int64, _P, c_int64, c_int64, c_int32, c_int32,
                                             c_int32, c_int32, _P]),

@@ -59,3 +59,17 @@ def test_workspace_query_sizes():
     assert small <= 512 and big > 1 << 20
     assert _capi.query("lv_paged_attention_workspace_bytes", 0, 0, 8, 2, 64, 64, 1) == 0
 
+
+def test_the_static_workspace_refuses_a_step_that_needs_more():
+    """lv_paged_attention_static sizes the step before it touches the GPU; a step whose work list and split-K
+    partials exceed LV_STATIC_WORKSPACE_BYTES is refused with a message naming both sizes. (Arguments are fake
+    non-null pointers: the call returns before using them.)"""
+    # Split-K keeps a step's partials under 9 MiB at any context length; a step of 2^27 prompt tokens needs a work
+    # list of 4M items (32 MiB).
+    assert _capi.query("lv_paged_attention_workspace_bytes", 4096, 4096, 32, 8, 128, (1 << 31) - 1, 1) < 9 << 20
+    tokens = 1 << 27
+    need = _capi.query("lv_paged_attention_workspace_bytes", 4096, tokens, 32, 8, 128, 1 << 20, 0)
+    assert need > 16 << 20
+    with pytest.raises(_capi.LvError, match=rf"needs {need} bytes of workspace; the static workspace holds 16777216"):
+        _capi.call("lv_paged_attention_static", 16, 0, 0, 16, 16, 0, 0, 0, 256, 16, 0, 16, None, 16, 4096,
+                   tokens, 32, 8, 128, 1.0, 64, 1 << 20, 16, 0, 0, 0, 0, 0, None)
