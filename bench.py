@@ -1,21 +1,27 @@
 """Benchmark of the continuous-batching attention path on one MI355X.
 
-A step is one pass of the path over one synthetic batch, all on the GPU with inputs resident in HBM:
+A step is one pass of the path over one synthetic batch, all on the GPU with inputs resident in HBM, as a model
+runs it per step:
 - the pack kernel turns the rows' (num_cached, num_new, block list), staged on the device before timing, into the
-  step's metadata (cu_seqlens, positions, slot_mapping, context_lens, padded block_tables);
-- the store kernel scatters the step's new K/V (or MLA latents) into the paged cache;
-- the attention op attends the whole batch (one varlen launch for decode and prompt rows; MLA latent decode for
-  the DeepSeek workload).
+  step's metadata (cu_seqlens, positions, slot_mapping, context_lens, padded block_tables) -- once per step;
+- then, for each of the model's attention layers (Qwen3-8B 36, Qwen3-0.6B 28, DeepSeek-V2-Lite 27; ``--layers``
+  overrides), the store kernel scatters that layer's new K/V (or MLA latents) into its paged cache and the
+  attention op attends the whole batch (one varlen launch for decode and prompt rows; MLA latent decode for the
+  DeepSeek workload). Every layer reads the one Context the pack produced, so the attention work list is planned
+  in the first layer and reused by the rest, as the reference's backends cache per-step plans. The layers rotate
+  through enough copies of the cache that each one starts cold (none is still in the 256 MB Infinity Cache).
 
-The JSON line's ``value`` is the primary workload's algorithmic HBM bytes per step / step time (GB/s). Default
-primary: Qwen3-8B-shaped chunked-prefill mixed batch at token budget 8192 (4 chunks of 1536 new tokens on a
-cached prefix U[0, 6144], plus 2048 decode rows with context U[256, 4096]; 32/8 heads, d128, bf16, 256-token
-pages). The line also carries per-kernel times from HIP events on the launch stream, a ``roofline`` object for
-the attention op, a ``cpu_baseline`` (the oracle's restatement of the reference PyTorch backend timed on a bounded
-sample on the host cores) and, under ``workloads``, the same figures for the other shapes this path is measured on
-(Qwen3-8B pure decode at batch 256, long-context split-K decode, DeepSeek-V2-Lite MLA decode, Qwen3-0.6B mixed,
-and two steps of prompts -- the Qwen3-8B mixed step's four chunks alone and DeepSeek-V2-Lite MLA prefill chunks --
-which are MFMA work and report TFLOP/s against the bf16 peak).
+The JSON line's ``value`` is the primary workload's algorithmic HBM bytes per step / step time (GB/s), and
+``tokens_per_s_per_layer`` its tokens / (step time / layers). Default primary: Qwen3-8B-shaped chunked-prefill
+mixed batch at token budget 8192 (4 chunks of 1536 new tokens on a cached prefix U[0, 6144], plus 2048 decode rows
+with context U[256, 4096]; 32/8 heads, d128, bf16, 256-token pages). The line also carries per-kernel times from
+HIP events on the launch stream (per layer: store and attention, the attention of the first layer -- which plans
+-- and of the later ones), a ``roofline`` object for the attention op (mean over layers), a ``cpu_baseline`` (the
+oracle's restatement of the reference PyTorch backend timed on a bounded sample on the host cores) and, under
+``workloads``, the same figures for the other shapes this path is measured on (Qwen3-8B pure decode at batch 256,
+long-context split-K decode, DeepSeek-V2-Lite MLA decode, Qwen3-0.6B mixed, both decode steps again on
+lean-vLLM's default 16-token pages, and two steps of prompts -- the Qwen3-8B mixed step's four chunks alone and
+DeepSeek-V2-Lite MLA prefill chunks -- which are MFMA work and report TFLOP/s against the bf16 peak).
 """
 
 from __future__ import annotations
@@ -38,8 +44,6 @@ METRIC = "paged-attn HBM GB/s (% of peak) + tokens/s per layer, Qwen3-8B mixed b
 EXTRA = ("qwen3_8b_decode,qwen3_8b_long,deepseek_v2_lite_mla,qwen3_0_6b_mixed,qwen3_8b_prefill,"
          "deepseek_v2_lite_mla_prefill,qwen3_8b_decode_bs16,deepseek_v2_lite_mla_bs16")
 RIDGE_FLOP_PER_BYTE = PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)  # above it a step is MFMA-bound
-# Workloads whose whole working set fits the 256 MB Infinity Cache: each timed step starts from a flushed cache.
-FLUSHED = {"qwen3_0_6b_mixed"}
 
 
 def parse():
@@ -51,6 +55,8 @@ def parse():
     ap.add_argument("--extra", default=EXTRA, help="comma-separated workloads also measured ('none' for none)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--layers", type=int, default=None,
+                    help="attention layers per step (default: the model's own count; 1 times a single layer)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB, 5 times (the reference kernel for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
@@ -70,8 +76,21 @@ def calibrate_copy(mib: int):
     print(json.dumps({"copy_calibration_bytes_per_launch": mib << 20, "launches": 5}), flush=True)
 
 
-def measure(name: str, steps: int, warmup: int, seed: int, dev):
-    """Time ``steps`` steps of one workload; returns (figures, workload, tensors)."""
+def cache_sets(wl, touched_bytes: int, layers: int) -> int:
+    """Copies of the layer state (caches, or MLA prefill's expanded keys) the layers of a step rotate through, so
+    that no layer finds the one it attends still in the 256 MB Infinity Cache from an earlier layer."""
+    if layers <= 1:
+        return 1
+    return max(2, min(8, 1 + -(-2 * 256 * 2**20 // max(touched_bytes, 1))))
+
+
+def measure(name: str, steps: int, warmup: int, seed: int, dev, layers: int | None = None):
+    """Time ``steps`` steps of one workload; returns (figures, workload, tensors of the first layer).
+
+    A step is what the model runs per step on this path: the pack kernel once, then for each of the model's
+    attention layers the store of that layer's new K/V and its attention, every layer reading the one Context the
+    pack produced (so the work list is planned in the first layer and reused by the rest, as the reference caches
+    per-step plans). The layers rotate through a few copies of the cache so that each starts cold."""
     import torch
 
     import numpy as np
@@ -80,7 +99,11 @@ def measure(name: str, steps: int, warmup: int, seed: int, dev):
     from lvattn import workloads as W
 
     wl = W.WORKLOADS[name](seed)
-    t = W.materialize(wl, dev, torch.bfloat16, seed=seed)
+    layers = wl.num_layers if layers is None else layers
+    nbytes = W.algorithmic_bytes(wl)
+    sets = cache_sets(wl, nbytes["attention"] + nbytes["store"], layers)
+    ts = [W.materialize(wl, dev, torch.bfloat16, seed=seed + r) for r in range(sets)]
+    t = ts[0]
     heads_kv = wl.num_heads if wl.is_mla else wl.num_kv_heads
     head_dim = wl.expanded[0] if wl.is_mla_prefill else wl.latent_dim if wl.is_mla else wl.head_dim
     backend = MI355XAttention(wl.num_heads, head_dim, wl.scale, heads_kv)
@@ -99,40 +122,44 @@ def measure(name: str, steps: int, warmup: int, seed: int, dev):
     out_dim = wl.expanded[1] if wl.is_mla_prefill else wl.v_dim if wl.is_mla else wl.head_dim
     out = torch.empty(wl.tokens, wl.num_heads, out_dim, dtype=torch.bfloat16, device=dev)
     if wl.is_mla_prefill:  # the cached prefix as one unmasked chunk (layers/attention.py:288-315)
-        ex = t.expanded
         cu_ctx = torch.tensor([0, *np.cumsum(wl.num_cached).tolist()], dtype=torch.int32, device=dev)
         max_ctx = max(max(wl.num_cached), 1)
-    flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev) if name in FLUSHED else None
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
-    ev = {k: [torch.cuda.Event(enable_timing=True) for _ in range(steps)] for k in ("a", "b", "c", "d")}
+    ev_pack = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    ev_layer = [[tuple(torch.cuda.Event(enable_timing=True) for _ in range(3)) for _ in range(layers)]
+                for _ in range(steps)]
 
     def step(i=None):
-        if flush is not None:
-            flush.fill_(i or 0)  # evicts the previous step's lines; outside the event brackets
         if i is not None:
-            ev["a"][i].record(stream)
+            ev_pack[i][0].record(stream)
         _, ctx = packer.run(plan)
         if i is not None:
-            ev["b"][i].record(stream)
-        if wl.is_mla:
-            backend.store_latents(t.k_new, t.k_cache, ctx["slot_mapping"])
-        else:
-            backend.store_kvcache(t.k_new, t.v_new, t.k_cache, t.v_cache, ctx["slot_mapping"])
-        if i is not None:
-            ev["c"][i].record(stream)
-        fields = {k: v for k, v in ctx.items() if k in Context.__slots__}
-        if wl.is_mla_prefill:
-            cu_q, max_q = ctx["cu_seqlens_q"], ctx["max_seqlen_q"]
-            o, lse = backend.varlen_with_lse(ex["q"], ex["k"], ex["v"], cu_q, cu_q, max_q, max_q, True)
-            co, clse = backend.varlen_with_lse(ex["q"], ex["k_ctx"], ex["v_ctx"], cu_q, cu_ctx, max_q, max_ctx, False)
-            merge_attention_(co, clse, o, lse, out)
-        elif wl.is_mla:
-            backend.mla_decode(t.q, t.k_cache, wl.v_dim, Context(**fields), out=out)
-        else:
-            backend.forward(t.q, t.k_new, t.v_new, t.k_cache, t.v_cache, Context(**fields), out=out)
-        if i is not None:
-            ev["d"][i].record(stream)
+            ev_pack[i][1].record(stream)
+        context = Context(**{k: v for k, v in ctx.items() if k in Context.__slots__})
+        for layer in range(layers):
+            x = ts[layer % sets]
+            if i is not None:
+                ev_layer[i][layer][0].record(stream)
+            if wl.is_mla:
+                backend.store_latents(x.k_new, x.k_cache, ctx["slot_mapping"])
+            else:
+                backend.store_kvcache(x.k_new, x.v_new, x.k_cache, x.v_cache, ctx["slot_mapping"])
+            if i is not None:
+                ev_layer[i][layer][1].record(stream)
+            if wl.is_mla_prefill:
+                ex = x.expanded
+                cu_q, max_q = ctx["cu_seqlens_q"], ctx["max_seqlen_q"]
+                o, lse = backend.varlen_with_lse(ex["q"], ex["k"], ex["v"], cu_q, cu_q, max_q, max_q, True)
+                co, clse = backend.varlen_with_lse(ex["q"], ex["k_ctx"], ex["v_ctx"], cu_q, cu_ctx, max_q, max_ctx,
+                                                   False)
+                merge_attention_(co, clse, o, lse, out)
+            elif wl.is_mla:
+                backend.mla_decode(x.q, x.k_cache, wl.v_dim, context, out=out)
+            else:
+                backend.forward(x.q, x.k_new, x.v_new, x.k_cache, x.v_cache, context, out=out)
+            if i is not None:
+                ev_layer[i][layer][2].record(stream)
 
     for _ in range(warmup):
         step()
@@ -143,23 +170,32 @@ def measure(name: str, steps: int, warmup: int, seed: int, dev):
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
 
-    def avg_ms(x, y):
-        return sum(ev[x][i].elapsed_time(ev[y][i]) for i in range(steps)) / steps
+    def mean(xs):
+        return sum(xs) / len(xs)
 
-    pack_ms, store_ms, attn_ms = avg_ms("a", "b"), avg_ms("b", "c"), avg_ms("c", "d")
-    step_ms = avg_ms("a", "d") if flush is not None else wall_ms
-    nbytes = W.algorithmic_bytes(wl)
+    pack_ms = mean([a.elapsed_time(b) for a, b in ev_pack])
+    store_ms = mean([e[0].elapsed_time(e[1]) for st in ev_layer for e in st])
+    attn_ms = mean([e[1].elapsed_time(e[2]) for st in ev_layer for e in st])
+    attn_first = mean([st[0][1].elapsed_time(st[0][2]) for st in ev_layer])
+    attn_later = mean([e[1].elapsed_time(e[2]) for st in ev_layer for e in st[1:]]) if layers > 1 else attn_first
+    step_ms = wall_ms
+    layer_ms = step_ms / layers
     flops = W.algorithmic_flops(wl)
+    step_bytes = layers * (nbytes["attention"] + nbytes["store"]) + nbytes["pack"]
     attn_gbs = nbytes["attention"] / (attn_ms * 1e-3) / 1e9
     figures = {
         "workload": name,
         "rows": wl.rows,
         "tokens": wl.tokens,
+        "layers": layers,
+        "cache_sets": sets,
         "ms_per_step": round(step_ms, 4),
-        "GBs": round(nbytes["total"] / (step_ms * 1e-3) / 1e9, 1),
-        "pct_of_peak_hbm": round(100 * nbytes["total"] / (step_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 2),
-        "tokens_per_s_per_layer": round(wl.tokens / (step_ms * 1e-3), 1),
-        "kernel_ms": {"pack": round(pack_ms, 4), "store": round(store_ms, 4), "attention": round(attn_ms, 4)},
+        "ms_per_layer": round(layer_ms, 4),
+        "GBs": round(step_bytes / (step_ms * 1e-3) / 1e9, 1),
+        "pct_of_peak_hbm": round(100 * step_bytes / (step_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 2),
+        "tokens_per_s_per_layer": round(wl.tokens / (layer_ms * 1e-3), 1),
+        "kernel_ms": {"pack": round(pack_ms, 4), "store": round(store_ms, 4), "attention": round(attn_ms, 4),
+                      "attention_first_layer": round(attn_first, 4), "attention_later_layers": round(attn_later, 4)},
         "host_stage_ms": round(host_stage_ms, 4),
         "attention_GBs": round(attn_gbs, 1),
         "attention_frac_of_peak": round(attn_gbs / PEAK_HBM_GBS, 4),
@@ -168,8 +204,8 @@ def measure(name: str, steps: int, warmup: int, seed: int, dev):
         "bound": "mfma" if flops / nbytes["attention"] > RIDGE_FLOP_PER_BYTE else "hbm",
         "bytes": nbytes,
         "flops": flops,
-        "cache_flushed_each_step": flush is not None,
     }
+    del ts[1:]
     return figures, wl, t
 
 
@@ -315,13 +351,13 @@ def main():
     import torch
 
     dev = torch.device("cuda:0")
-    primary, wl, t = measure(args.workload, args.steps, args.warmup, args.seed, dev)
+    primary, wl, t = measure(args.workload, args.steps, args.warmup, args.seed, dev, args.layers)
     cpu = None if args.no_cpu_baseline or wl.is_mla else cpu_baseline(wl, t)
     del t
     torch.cuda.empty_cache()
     extras = []
     for name in [n for n in args.extra.split(",") if n and n != "none" and n != args.workload]:
-        fig, _, t = measure(name, args.steps, args.warmup, args.seed, dev)
+        fig, _, t = measure(name, args.steps, args.warmup, args.seed, dev, args.layers)
         extras.append(fig)
         del t
         torch.cuda.empty_cache()
@@ -334,6 +370,8 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": primary["ms_per_step"],
+        "ms_per_layer": primary["ms_per_layer"],
+        "layers_per_step": primary["layers"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -346,6 +384,7 @@ def main():
             "heads": f"{wl.num_heads}/{wl.num_heads if wl.is_mla else wl.num_kv_heads}",
             "head_dim": wl.latent_dim if wl.is_mla else wl.head_dim,
             "block_size": wl.block_size,
+            "layers": primary["layers"],
             "parallelism": "single GPU",
         },
         "pct_of_peak_hbm": primary["pct_of_peak_hbm"],

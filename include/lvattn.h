@@ -29,7 +29,7 @@ extern "C" {
 #define LV_SCHEDULE_SERIAL 1
 #define LV_SCHEDULE_OVERLAP 2
 
-#define LV_ABI_VERSION 6
+#define LV_ABI_VERSION 7
 
 /* The last error message of the calling thread ("" if none). */
 const char* lv_last_error(void);
@@ -115,7 +115,14 @@ int lv_store_latents(const void* latent, int64_t latent_stride_t, int32_t num_to
  * the same either way.
  * prompt_workgroups (overlap only): how many CUs run a prompt workgroup beside the decode rows; 0 picks half of
  * them. Other values are clamped to [half, three quarters] of the CUs and rounded down to a multiple of 8 (each
- * kv head's prompt items then stay on one XCD). A step heavy in prompt tiles ends sooner with more. */
+ * kv head's prompt items then stay on one XCD). A step heavy in prompt tiles ends sooner with more.
+ * flags: 0, or LV_ATTN_REUSE_PLAN for the later layers of a step: the workspace already holds the work list a previous
+ * call planned for this step (the same rows, lengths, shape and max_seqlen_k, through the same cu_seqlens_q /
+ * seqlens_k / cu_seqlens_k pointers, whose contents have not changed since), so the plan launch is skipped -- the
+ * per-step plan the reference's backends cache in context.attn_metadata (lean_vllm/attention/flash_backend.py:16-20,
+ * 157-160). The library honours the flag only if the last plan it made in this workspace was for the same shape and
+ * pointers, and plans again otherwise; unchanged contents are the caller's promise. */
+#define LV_ATTN_REUSE_PLAN 1
 size_t lv_paged_attention_workspace_bytes(int32_t num_rows, int32_t num_tokens, int32_t num_heads,
                                           int32_t num_kv_heads, int32_t head_dim, int32_t max_seqlen_k,
                                           int32_t decode_only);
@@ -127,7 +134,7 @@ int lv_paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h, co
                        int32_t num_kv_heads, int32_t head_dim, float scale, int32_t max_seqlen_q,
                        int32_t max_seqlen_k, void* out, int64_t out_stride_t, int64_t out_stride_h,
                        void* workspace, size_t workspace_bytes, int32_t schedule, int32_t prompt_workgroups,
-                       int32_t dtype, void* stream);
+                       int32_t flags, int32_t dtype, void* stream);
 
 /* The same step with no workspace argument and no allocation of any kind. No counterpart in the reference: for
  * callers that cannot call hipMalloc -- code under HIP graph capture, tight serving loops, harnesses that forbid
@@ -147,7 +154,8 @@ int lv_paged_attention_static(const void* q, int64_t q_stride_t, int64_t q_strid
                               const int32_t* cu_seqlens_k, int32_t num_rows, int32_t num_tokens, int32_t num_heads,
                               int32_t num_kv_heads, int32_t head_dim, float scale, int32_t max_seqlen_q,
                               int32_t max_seqlen_k, void* out, int64_t out_stride_t, int64_t out_stride_h,
-                              int32_t schedule, int32_t prompt_workgroups, int32_t dtype, void* stream);
+                              int32_t schedule, int32_t prompt_workgroups, int32_t flags, int32_t dtype,
+                              void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------
  * Attention over packed keys (no pages). Replaces AttentionBackend.prefill without block tables and

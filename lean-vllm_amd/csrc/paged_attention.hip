@@ -30,6 +30,7 @@ constexpr int kDecodeWgs = 2;         // persistent decode workgroups per CU out
 constexpr int kOverlapDecodeWgs = 2;  // persistent decode workgroups per CU beside a mixed step's prompt workgroups
 constexpr int kSplitTarget = 4096;    // decode items (x kv heads x query-head groups) a split-K grid aims for
 constexpr int kMinSplit = 256;        // keys per decode item at least
+constexpr int kSmallStepRounds = 8;   // a mixed step of at most this many GPU-fulls of workgroups is one launch
 
 // ---------------------------------------------------------------------------------------------------------
 // Decode item.
@@ -313,6 +314,9 @@ __global__ __launch_bounds__(256) void decode_list_kernel(AttnParams p) {
 // published at its merge barrier; the merge alternates between two LDS buffers, so one barrier per item suffices.
 // Alone on the GPU the grid holds two workgroups per CU, so their waves may take 256 registers (no spills; 1-2%
 // faster than under the 128 that room for four would leave); BESIDE a mixed step's prompt workgroups, 128.
+// The last workgroup to finish puts the ticket and the exit count back to zero, so the next layer of the step can
+// run on the same plan without a plan launch: every workgroup's ticket draws have returned (their values were
+// read) before it counts itself out, so no draw can follow the reset.
 template <typename T, int D, int GS, bool BESIDE = false>
 __global__ __launch_bounds__(256, BESIDE ? 4 : 2) void decode_persistent_kernel(AttnParams p) {
   __shared__ __attribute__((aligned(16))) char smem[2][SmemBytes<D, GS>::kDecode];
@@ -331,6 +335,10 @@ __global__ __launch_bounds__(256, BESIDE ? 4 : 2) void decode_persistent_kernel(
     const int2 it = p.items[first + bx];
     decode_item<T, D, GS>(p, it.x, it.y, kvh, qg, smem[k & 1], &s_ticket[(k + 1) & 1], next);
     f = __builtin_amdgcn_readfirstlane(s_ticket[(k + 1) & 1]);
+  }
+  if (threadIdx.x == 0 && atomicAdd(p.ticket + 1, 1) == (int)gridDim.x - 1) {
+    atomicExch(p.ticket, 0);
+    atomicExch(p.ticket + 1, 0);
   }
 }
 
@@ -361,6 +369,32 @@ __global__ __launch_bounds__(256, 2) void prompt_overlap_kernel(AttnParams p) {
     const int2 it = p.items[bx];
     prefill_item<T, D, D, true, true, RING>(p, it.x, -1 - it.y, kvh, smem);
     __syncthreads();  // the next item restages the LDS tiles
+  }
+}
+
+// A small mixed step in one launch: workgroups [0, prompt_wgs) take the prompt items (one per item and kv head, the
+// longest first), the rest the decode items in list order. Dispatched in that order, the prompt workgroups start
+// first and the decode workgroups stream through the slots they leave, as in the overlapped schedule but without a
+// second stream, its events and one launch: for steps of a few hundred rows, whose launch sequence is a large share
+// of their time.
+template <typename T, int D, int GS, int RING>
+__global__ __launch_bounds__(256, 2) void mixed_small_kernel(AttnParams p, int32_t prompt_wgs) {
+  static_assert(SmemBytes<D, GS>::kDecode <= (RING > 0 ? RING : 1) * PromptSmem<D, D>::kBytes, "LDS for both");
+  __shared__ __attribute__((aligned(16))) char smem[(RING > 0 ? RING : 1) * PromptSmem<D, D>::kBytes];
+  const int b = blockIdx.x;
+  if (b < prompt_wgs) {
+    const int bx = b / p.hkv, kvh = b - bx * p.hkv;
+    if (bx >= p.n_items[1]) return;
+    const int2 it = p.items[bx];
+    prefill_item<T, D, D, true, false, RING>(p, it.x, -1 - it.y, kvh, smem);
+  } else {
+    const int ny = p.hkv * p.qgroups;
+    const int f = b - prompt_wgs, bx = f / ny, by = f - bx * ny;
+    const int kvh = by / p.qgroups, qg = by - kvh * p.qgroups;
+    const int i = bx + p.n_items[1];
+    if (i >= p.n_items[0]) return;
+    const int2 it = p.items[i];
+    decode_item<T, D, GS>(p, it.x, it.y, kvh, qg, smem);
   }
 }
 
@@ -434,6 +468,7 @@ __global__ __launch_bounds__(kScanThreads) void plan_kernel(const int32_t* __res
     n_items[0] = min(npre + nfull + npart, max_items);
     n_items[1] = min(npre, max_items);
     n_items[2] = 0;  // the persistent decode launch's ticket counter
+    n_items[3] = 0;  // and its count of workgroups done
   }
 }
 
@@ -636,6 +671,24 @@ static int launch(const AttnParams& p, bool listed, bool mixed, bool overlap, in
                   hipStream_t stream) {
   const int ny = p.hkv * p.qgroups;
   const bool ring = p.bs.d % kPrefillKeys == 0;  // every 64-key tile in one page
+  if (overlap && listed && mixed) {
+    // A step whose workgroups (bounds: most prompt bounds exit at once) fill the GPU at most kSmallStepRounds times
+    // runs as one launch.
+    const int64_t pw = (int64_t)s.max_prompt_items * p.hkv, dw = (int64_t)s.max_decode_items * ny;
+    const int resident = ring ? resident_per_cu<mixed_small_kernel<T, D, GS, kPromptRing>>()
+                              : resident_per_cu<mixed_small_kernel<T, D, GS, 0>>();
+    if (pw + dw <= (int64_t)kSmallStepRounds * resident * device_cus()) {
+      if (ring)
+        hipLaunchKernelGGL((mixed_small_kernel<T, D, GS, kPromptRing>), dim3(pw + dw), dim3(256), 0, stream, p,
+                           (int32_t)pw);
+      else
+        hipLaunchKernelGGL((mixed_small_kernel<T, D, GS, 0>), dim3(pw + dw), dim3(256), 0, stream, p, (int32_t)pw);
+      LV_LAUNCH_CHECK("mixed_small_kernel");
+      if (p.max_splits > 1)
+        hipLaunchKernelGGL((splitk_merge_kernel<T, D>), dim3(p.rows, p.hq), dim3(64), 0, stream, p);
+      return LV_OK;
+    }
+  }
   SideStream* side = overlap && listed && mixed ? side_stream() : nullptr;
   bool forked = false;
   if (side) {
@@ -728,6 +781,43 @@ static void* scratch_on_current_device() {
   return addr[dev];
 }
 
+// What a work list was planned for, per workspace: a caller's request to reuse the plan already in a workspace
+// (LV_ATTN_REUSE_PLAN, for the later layers of a step) is honoured only if the workspace's last plan was made for the
+// same rows, shape and row-length arrays; otherwise the call plans again.
+struct PlanSig {
+  const void* ws = nullptr;
+  const int32_t *cu_q = nullptr, *lens = nullptr, *cu_k = nullptr;
+  int64_t rows = 0, tokens = 0, max_k = 0, split = 0, qp = 0, max_items = 0, bytes = 0;
+  bool mixed = false;
+  bool operator==(const PlanSig& o) const {
+    return ws == o.ws && cu_q == o.cu_q && lens == o.lens && cu_k == o.cu_k && rows == o.rows &&
+           tokens == o.tokens && max_k == o.max_k && split == o.split && qp == o.qp && max_items == o.max_items &&
+           bytes == o.bytes && mixed == o.mixed;
+  }
+};
+constexpr int kPlanRecords = 32;
+static std::mutex g_plan_lock;
+static PlanSig g_plans[kPlanRecords];
+
+// True if `sig`'s workspace holds the plan `sig` describes; otherwise records that it is about to.
+static bool plan_is_current(const PlanSig& sig, bool reuse) {
+  std::lock_guard<std::mutex> g(g_plan_lock);
+  int slot = -1;
+  for (int i = 0; i < kPlanRecords; ++i)
+    if (g_plans[i].ws == sig.ws) slot = i;
+  if (reuse && slot >= 0 && g_plans[slot] == sig) return true;
+  if (slot < 0) {  // a new workspace: take a free record, else the first
+    slot = 0;
+    for (int i = 0; i < kPlanRecords; ++i)
+      if (!g_plans[i].ws) {
+        slot = i;
+        break;
+      }
+  }
+  g_plans[slot] = sig;
+  return false;
+}
+
 // One step, with the workspace given (workspace != nullptr or an empty shape) or, for static_ws, the device's
 // static workspace.
 static int paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_cache,
@@ -738,13 +828,14 @@ static int paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h
                            int32_t num_kv_heads, int32_t head_dim, float scale, int32_t max_seqlen_q,
                            int32_t max_seqlen_k, void* out, int64_t out_stride_t, int64_t out_stride_h,
                            void* workspace, size_t workspace_bytes, bool static_ws, int32_t schedule,
-                           int32_t prompt_workgroups, int32_t dtype, void* stream) {
+                           int32_t prompt_workgroups, int32_t flags, int32_t dtype, void* stream) {
   LV_REQUIRE(dtype == LV_DTYPE_BF16 || dtype == LV_DTYPE_F16, "paged_attention: dtype %d is not bf16 or fp16",
              dtype);
   LV_REQUIRE(num_rows >= 0 && num_tokens >= 0, "paged_attention: negative row or token count");
   LV_REQUIRE(schedule == LV_SCHEDULE_AUTO || schedule == LV_SCHEDULE_SERIAL || schedule == LV_SCHEDULE_OVERLAP,
              "paged_attention: unknown schedule %d", schedule);
   LV_REQUIRE(prompt_workgroups >= 0, "paged_attention: negative prompt_workgroups %d", prompt_workgroups);
+  LV_REQUIRE((flags & ~LV_ATTN_REUSE_PLAN) == 0, "paged_attention: unknown flags 0x%x", flags);
   if (num_rows == 0 || num_tokens == 0) return LV_OK;
   LV_REQUIRE(num_heads > 0 && num_kv_heads > 0 && num_heads % num_kv_heads == 0,
              "paged_attention: %d query heads do not group over %d key heads", num_heads, num_kv_heads);
@@ -824,8 +915,21 @@ static int paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h
   p.ticket = listed ? reinterpret_cast<int32_t*>(ws + s.count_off) + 2 : nullptr;
 
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (listed) {
-    const int qp = kPrefillRows / p.group;
+  const int qp = kPrefillRows / p.group;
+  PlanSig sig;
+  sig.ws = workspace;
+  sig.cu_q = mixed ? cu_seqlens_q : nullptr;
+  sig.lens = seqlens_k;
+  sig.cu_k = cu_seqlens_k;
+  sig.rows = num_rows;
+  sig.tokens = num_tokens;
+  sig.max_k = max_seqlen_k;
+  sig.split = s.split;
+  sig.qp = qp;
+  sig.max_items = s.max_items;
+  sig.bytes = (int64_t)s.bytes;
+  sig.mixed = mixed;
+  if (listed && !plan_is_current(sig, (flags & LV_ATTN_REUSE_PLAN) != 0)) {
     hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kScanThreads), 0, st, mixed ? cu_seqlens_q : nullptr, seqlens_k,
                        cu_seqlens_k, num_rows, s.split, qp, s.max_items, reinterpret_cast<int2*>(ws + s.items_off),
                        reinterpret_cast<int32_t*>(ws + s.count_off));
@@ -861,12 +965,12 @@ extern "C" int lv_paged_attention(const void* q, int64_t q_stride_t, int64_t q_s
                                   int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float scale,
                                   int32_t max_seqlen_q, int32_t max_seqlen_k, void* out, int64_t out_stride_t,
                                   int64_t out_stride_h, void* workspace, size_t workspace_bytes, int32_t schedule,
-                                  int32_t prompt_workgroups, int32_t dtype, void* stream) {
+                                  int32_t prompt_workgroups, int32_t flags, int32_t dtype, void* stream) {
   return paged_attention(q, q_stride_t, q_stride_h, k_cache, v_cache, cache_stride_block, cache_stride_token,
                          cache_stride_head, block_size, block_tables, table_stride, cu_seqlens_q, seqlens_k,
                          cu_seqlens_k, num_rows, num_tokens, num_heads, num_kv_heads, head_dim, scale, max_seqlen_q,
                          max_seqlen_k, out, out_stride_t, out_stride_h, workspace, workspace_bytes, false, schedule,
-                         prompt_workgroups, dtype, stream);
+                         prompt_workgroups, flags, dtype, stream);
 }
 
 extern "C" int lv_paged_attention_static(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_cache,
@@ -877,10 +981,10 @@ extern "C" int lv_paged_attention_static(const void* q, int64_t q_stride_t, int6
                                          int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float scale,
                                          int32_t max_seqlen_q, int32_t max_seqlen_k, void* out, int64_t out_stride_t,
                                          int64_t out_stride_h, int32_t schedule, int32_t prompt_workgroups,
-                                         int32_t dtype, void* stream) {
+                                         int32_t flags, int32_t dtype, void* stream) {
   return paged_attention(q, q_stride_t, q_stride_h, k_cache, v_cache, cache_stride_block, cache_stride_token,
                          cache_stride_head, block_size, block_tables, table_stride, cu_seqlens_q, seqlens_k,
                          cu_seqlens_k, num_rows, num_tokens, num_heads, num_kv_heads, head_dim, scale, max_seqlen_q,
                          max_seqlen_k, out, out_stride_t, out_stride_h, nullptr, 0, true, schedule, prompt_workgroups,
-                         dtype, stream);
+                         flags, dtype, stream);
 }

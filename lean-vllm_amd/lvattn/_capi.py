@@ -30,11 +30,11 @@ _PROTOTYPES = {
     "lv_paged_attention": (ctypes.c_int, [_P, c_int64, c_int64, _P, _P, c_int64, c_int64, c_int64, c_int32, _P,
                                           c_int64, _P, _P, _P, c_int32, c_int32, c_int32, c_int32, c_int32,
                                           c_float, c_int32, c_int32, _P, c_int64, c_int64, _P, c_size_t,
-                                          c_int32, c_int32, c_int32, _P]),
+                                          c_int32, c_int32, c_int32, c_int32, _P]),
     "lv_paged_attention_static": (ctypes.c_int, [_P, c_int64, c_int64, _P, _P, c_int64, c_int64, c_int64, c_int32,
                                                  _P, c_int64, _P, _P, _P, c_int32, c_int32, c_int32, c_int32,
                                                  c_int32, c_float, c_int32, c_int32, _P, c_int64, c_int64, c_int32,
-                                                 c_int32, c_int32, _P]),
+                                                 c_int32, c_int32, c_int32, _P]),
     "lv_merge_attn_states": (ctypes.c_int, [_P, c_int64, c_int64, _P, c_int64, c_int64, _P, c_int64, c_int64,
                                             _P, c_int64, c_int64, _P, c_int64, c_int64, c_int32, c_int32,
                                             c_int32, c_int32, _P]),
@@ -83,9 +83,14 @@ def exported_symbols() -> dict[str, bool]:
     return {name: hasattr(lib, name) for name in _PROTOTYPES}
 
 
+_fns: dict = {}
+
+
 def call(name: str, *args):
     """Call ``name`` and raise ``LvError`` with the library's message on a non-zero status."""
-    fn = getattr(load(), name)
+    fn = _fns.get(name)
+    if fn is None:
+        fn = _fns[name] = getattr(load(), name)
     rc = fn(*args)
     if rc != LV_OK:
         msg = load().lv_last_error().decode(errors="replace")
@@ -95,7 +100,10 @@ def call(name: str, *args):
 
 def query(name: str, *args):
     """Call a function returning a value (no status)."""
-    return getattr(load(), name)(*args)
+    fn = _fns.get(name)
+    if fn is None:
+        fn = _fns[name] = getattr(load(), name)
+    return fn(*args)
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

@@ -56,6 +56,7 @@ _WORKSPACE = _Workspace()
 
 # Launch schedules of a step with prompt rows (LV_SCHEDULE_* of lvattn.h).
 SCHEDULE_AUTO, SCHEDULE_SERIAL, SCHEDULE_OVERLAP = 0, 1, 2
+LV_ATTN_REUSE_PLAN = 1
 # Measured MI355X rates the schedule choice compares (bf16, head_dim 128). Overlapped, the prompt tiles run at
 # about 0.18 PFLOP/s (one workgroup on half the CUs, beside the decode rows) against 0.84 PFLOP/s alone on the whole
 # GPU, and the decode rows stream about 6.6 TB/s. Overlap wins while the prompt tiles' extra time beside the decode
@@ -122,50 +123,67 @@ class MI355XAttention(AttentionBackend):
     # -- cache writes --------------------------------------------------------------------------------------
     def store_kvcache(self, key, value, k_cache, v_cache, slot_mapping) -> None:
         num_tokens, heads, dim = key.shape
-        assert key.stride(-1) == 1 and value.stride(-1) == 1, "unit dim stride"
-        assert key.stride(1) == dim and value.stride(1) == dim, "head stride must equal head_dim"
-        assert k_cache.stride() == v_cache.stride() and k_cache.stride(-1) == 1
+        ks, vs, cs = key.stride(), value.stride(), k_cache.stride()
+        assert ks[2] == 1 and vs[2] == 1, "unit dim stride"
+        assert ks[1] == dim and vs[1] == dim, "head stride must equal head_dim"
+        assert cs == v_cache.stride() and cs[3] == 1
         assert slot_mapping.numel() == num_tokens
         assert key.dtype == value.dtype == k_cache.dtype == v_cache.dtype
-        if checks.enabled():
+        if checks.ENABLED:
             checks.check_slots(slot_mapping, k_cache.size(0), k_cache.size(1))
-        slot_mapping = slot_mapping if slot_mapping.dtype == torch.int32 else slot_mapping.to(torch.int32)
-        sb, st, sh, _ = k_cache.stride()
-        _capi.call("lv_store_kvcache", key.data_ptr(), value.data_ptr(), key.stride(0), value.stride(0), num_tokens,
-                   heads, dim, k_cache.data_ptr(), v_cache.data_ptr(), sb, st, sh, k_cache.size(1),
+        if slot_mapping.dtype != torch.int32:
+            slot_mapping = slot_mapping.to(torch.int32)
+        _capi.call("lv_store_kvcache", key.data_ptr(), value.data_ptr(), ks[0], vs[0], num_tokens, heads, dim,
+                   k_cache.data_ptr(), v_cache.data_ptr(), cs[0], cs[1], cs[2], k_cache.size(1),
                    slot_mapping.data_ptr(), key.element_size(), _capi.stream_of(key.device))
 
     def store_latents(self, latent, latent_cache, slot_mapping) -> None:
         num_tokens, dim = latent.shape
         assert latent.stride(-1) == 1 and latent_cache.stride(-2) == dim and latent_cache.stride(-1) == 1
         assert slot_mapping.numel() == num_tokens and latent.dtype == latent_cache.dtype
-        if checks.enabled():
+        if checks.ENABLED:
             checks.check_slots(slot_mapping, latent_cache.numel() // dim, 1)
         slot_mapping = slot_mapping if slot_mapping.dtype == torch.int32 else slot_mapping.to(torch.int32)
         _capi.call("lv_store_latents", latent.data_ptr(), latent.stride(0), num_tokens, dim, latent_cache.data_ptr(),
                    slot_mapping.data_ptr(), latent.element_size(), _capi.stream_of(latent.device))
 
     # -- attention -----------------------------------------------------------------------------------------
-    def _attend(self, q, k_cache, v_cache, out, *, block_tables, cu_seqlens_q, seqlens_k, cu_seqlens_k, rows,
-                max_seqlen_q, max_seqlen_k, schedule=SCHEDULE_AUTO, prompt_workgroups=0):
+    def _attend(self, q, k_cache, v_cache, out, *, context, block_tables, cu_seqlens_q, seqlens_k, cu_seqlens_k,
+                rows, max_seqlen_q, max_seqlen_k, schedule=SCHEDULE_AUTO, prompt_workgroups=0):
+        qs, cs = q.stride(), k_cache.stride()
         assert q.dtype in _capi.DTYPES and k_cache.dtype == q.dtype == v_cache.dtype
-        assert q.stride(-1) == 1 and k_cache.stride() == v_cache.stride() and k_cache.stride(-1) == 1
-        assert block_tables is not None and block_tables.dtype == torch.int32 and block_tables.stride(-1) == 1
+        assert qs[2] == 1 and cs == v_cache.stride() and cs[3] == 1
+        assert block_tables is not None and block_tables.dtype == torch.int32
         if out is None:
             out = torch.empty_like(q)
-        assert out.shape == q.shape and out.stride(-1) == 1 and out.dtype == q.dtype
+        os_ = out.stride()
+        assert out.shape == q.shape and os_[2] == 1 and out.dtype == q.dtype
         tokens, heads, dim = q.shape
-        decode_only = cu_seqlens_q is None or max_seqlen_q == 1
-        nbytes = _capi.query("lv_paged_attention_workspace_bytes", rows, tokens, heads, self.num_kv_heads, dim,
-                             max_seqlen_k, int(decode_only))
-        ws = _WORKSPACE.get(q.device, nbytes)
-        sb, st, sh, _ = k_cache.stride()
-        _capi.call("lv_paged_attention", q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(),
-                   v_cache.data_ptr(), sb, st, sh, k_cache.size(1), block_tables.data_ptr(), block_tables.stride(0),
-                   _capi.ptr(cu_seqlens_q), _capi.ptr(seqlens_k), _capi.ptr(cu_seqlens_k), rows, tokens, heads,
-                   self.num_kv_heads, dim, float(self.scale), max_seqlen_q, max_seqlen_k, out.data_ptr(),
-                   out.stride(0), out.stride(1), _capi.ptr(ws), 0 if ws is None else ws.numel(), schedule,
-                   prompt_workgroups, _capi.DTYPES[q.dtype], _capi.stream_of(q.device))
+        # The work list is planned once per step and every later layer reuses it, as the reference's backends cache
+        # per-step plans in context.attn_metadata (flash_backend.py:16-20,157-160). The plan depends on the rows'
+        # lengths (read through these tensors, which the step's context holds), the shape and the bound on key
+        # lengths; the step's workspace size is kept with it.
+        meta = context.attn_metadata
+        if meta is None:
+            meta = context.attn_metadata = {}
+        key = ("plan", heads, self.num_kv_heads, dim, rows, tokens, max_seqlen_q, max_seqlen_k,
+               id(cu_seqlens_q), id(seqlens_k), id(cu_seqlens_k))
+        planned = meta.get(key)
+        if planned is None:
+            decode_only = cu_seqlens_q is None or max_seqlen_q == 1
+            nbytes = _capi.query("lv_paged_attention_workspace_bytes", rows, tokens, heads, self.num_kv_heads, dim,
+                                 max_seqlen_k, int(decode_only))
+            planned = meta[key] = [nbytes, None, (cu_seqlens_q, seqlens_k, cu_seqlens_k)]  # holds the tensors
+        ws = _WORKSPACE.get(q.device, planned[0])
+        flags = LV_ATTN_REUSE_PLAN if ws is not None and planned[1] is ws else 0
+        planned[1] = ws
+        bt = block_tables
+        _capi.call("lv_paged_attention", q.data_ptr(), qs[0], qs[1], k_cache.data_ptr(), v_cache.data_ptr(), cs[0],
+                   cs[1], cs[2], k_cache.size(1), bt.data_ptr(), bt.stride(0), _capi.ptr(cu_seqlens_q),
+                   _capi.ptr(seqlens_k), _capi.ptr(cu_seqlens_k), rows, tokens, heads, self.num_kv_heads, dim,
+                   float(self.scale), max_seqlen_q, max_seqlen_k, out.data_ptr(), os_[0], os_[1], _capi.ptr(ws),
+                   0 if ws is None else ws.numel(), schedule, prompt_workgroups, flags, _capi.DTYPES[q.dtype],
+                   _capi.stream_of(q.device))
         return out
 
     def _schedule(self, context: Context, elem_bytes: int) -> int:
@@ -218,14 +236,14 @@ class MI355XAttention(AttentionBackend):
         assert lens.numel() == q.size(0) == bt.size(0), (
             f"decode takes one query per row: {q.size(0)} queries, {lens.numel()} context lengths, {bt.size(0)} table "
             "rows (a step whose rows carry drafts is is_prefill and goes to prefill)")
-        if checks.enabled():
+        if checks.ENABLED:
             checks.check_tables(bt, k_cache.size(0))
             checks.check_key_lengths(lens, bt, k_cache.size(1))
         lens = lens if lens.dtype == torch.int32 else lens.to(torch.int32)
         # The table's width bounds every length, so nothing is read back (torch_backend.py:98).
         max_k = bt.size(1) * k_cache.size(1)
-        return self._attend(q, k_cache, v_cache, out, block_tables=bt, cu_seqlens_q=None, seqlens_k=lens,
-                            cu_seqlens_k=None, rows=q.size(0), max_seqlen_q=1, max_seqlen_k=max_k)
+        return self._attend(q, k_cache, v_cache, out, context=context, block_tables=bt, cu_seqlens_q=None,
+                            seqlens_k=lens, cu_seqlens_k=None, rows=q.size(0), max_seqlen_q=1, max_seqlen_k=max_k)
 
     def prefill(self, q, k, v, k_cache, v_cache, context: Context, out=None):
         """Varlen causal attention over the step's rows, bottom-right aligned, every key read from the pages;
@@ -237,14 +255,15 @@ class MI355XAttention(AttentionBackend):
             o, _ = self._varlen(q, k, v, cu_q, cu_k, max_q, causal=True, want_lse=False, out=out)
             return o
         bt = context.block_tables
-        if checks.enabled():
+        if checks.ENABLED:
             checks.check_query_rows(cu_q, cu_k, q.size(0))
             checks.check_tables(bt, k_cache.size(0))
             checks.check_key_lengths(cu_k[1:] - cu_k[:-1], bt, k_cache.size(1), what="cu_seqlens_k row length")
         max_k = context.max_seqlen_k or bt.size(1) * k_cache.size(1)
         max_q = context.max_seqlen_q or q.size(0)
-        return self._attend(q, k_cache, v_cache, out, block_tables=bt, cu_seqlens_q=cu_q.to(torch.int32),
-                            seqlens_k=None, cu_seqlens_k=cu_k.to(torch.int32), rows=cu_q.numel() - 1,
+        return self._attend(q, k_cache, v_cache, out, context=context, block_tables=bt,
+                            cu_seqlens_q=cu_q if cu_q.dtype == torch.int32 else cu_q.to(torch.int32), seqlens_k=None,
+                            cu_seqlens_k=cu_k if cu_k.dtype == torch.int32 else cu_k.to(torch.int32), rows=cu_q.numel() - 1,
                             max_seqlen_q=max_q, max_seqlen_k=max_k,
                             schedule=self._schedule(context, q.element_size()),
                             prompt_workgroups=self._prompt_workgroups(context, q.element_size()))
@@ -264,7 +283,7 @@ class MI355XAttention(AttentionBackend):
         rows = lens.numel()
         tokens, heads, dim = q.shape
         assert tokens % rows == 0, "every row has the same number of queries"
-        if checks.enabled():
+        if checks.ENABLED:
             checks.check_tables(bt, latent_cache.size(0))
             checks.check_key_lengths(lens, bt, latent_cache.size(1))
         lq = tokens // rows

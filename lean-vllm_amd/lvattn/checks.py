@@ -3,9 +3,9 @@
 The kernels trust their index inputs -- slots, block tables, key lengths -- as the reference's kernels do. A
 scheduler bug that hands over a slot past the pool, a table entry past the pool, or a key length that its table
 does not cover would make a kernel read or write outside the caches. With ``LVATTN_CHECK`` set to anything but
-``""`` or ``"0"``, the backend and the packer first copy those inputs to the host (a synchronising copy: this is a
-debug mode) and raise ``ValueError`` naming the first bad entry. Off by default: the checks read back device
-memory, which a captured graph cannot do.
+``""`` or ``"0"`` when this module is imported (or when ``refresh()`` reads it again), the backend first copies those
+inputs to the host (a synchronising copy: this is a debug mode) and raises ``ValueError`` naming the first bad entry.
+Off by default: the checks read back device memory, which a captured graph cannot do.
 """
 
 from __future__ import annotations
@@ -16,7 +16,18 @@ import torch
 
 
 def enabled() -> bool:
+    """``LVATTN_CHECK`` as the environment holds it now."""
     return os.environ.get("LVATTN_CHECK", "") not in ("", "0")
+
+
+ENABLED = enabled()  # read once: the backend tests this flag on every call
+
+
+def refresh() -> bool:
+    """Read ``LVATTN_CHECK`` again (after the environment changed)."""
+    global ENABLED
+    ENABLED = enabled()
+    return ENABLED
 
 
 def _host(t: torch.Tensor) -> torch.Tensor:

@@ -1,7 +1,8 @@
 """Synthetic continuous-batching steps of the shapes this path is measured on.
 
 Each workload is a step's per-row scheduler state -- ``num_cached``, ``num_new`` and a block list per row, in
-scheduler order -- plus the layer shape. Lengths and block lists come from ``numpy.random.default_rng(seed)``
+scheduler order -- plus the layer shape and the model's number of attention layers (Qwen3-0.6B 28, Qwen3-8B 36,
+DeepSeek-V2-Lite 27), every one of which attends the same step. Lengths and block lists come from ``numpy.random.default_rng(seed)``
 (identical on every machine); block lists are consecutive slices of a seeded permutation of the block pool, so
 pages are scattered. Tensor values are drawn by ``materialize`` with a seeded torch generator on the target
 device. Key lengths include the token(s) stored this step (``context_lens = num_cached + num_new``).
@@ -48,6 +49,7 @@ class Workload:
     latent_dim: int = 0  # MLA: cached latent width
     v_dim: int = 0  # MLA: value width (leading entries of a latent)
     expanded: tuple = (0, 0)  # MLA prefill: (q.k width, value width) of the expanded heads
+    num_layers: int = 1  # attention layers of the model the step belongs to (each attends the same step)
     notes: dict = field(default_factory=dict)
 
     @property
@@ -96,7 +98,7 @@ def qwen3_0_6b_mixed(seed: int = 0) -> Workload:
     num_new = [512, 384] + [1] * 30
     ends = [c + n for c, n in zip(num_cached, num_new)]
     return Workload("qwen3_0_6b_mixed", 16, 8, 128, 256, 512, num_cached, num_new, _tables(rng, 512, ends, 256),
-                    1 / math.sqrt(128))
+                    1 / math.sqrt(128), num_layers=28)
 
 
 def qwen3_8b_decode(seed: int = 0, batch: int = 256, block_size: int = 256) -> Workload:
@@ -107,7 +109,7 @@ def qwen3_8b_decode(seed: int = 0, batch: int = 256, block_size: int = 256) -> W
     pool = 12_000 * 256 // block_size
     name = "qwen3_8b_decode" if block_size == 256 else f"qwen3_8b_decode_bs{block_size}"
     return Workload(name, 32, 8, 128, block_size, pool, num_cached, num_new, _tables(rng, pool, ctx, block_size),
-                    1 / math.sqrt(128))
+                    1 / math.sqrt(128), num_layers=36)
 
 
 def qwen3_8b_mixed(seed: int = 0) -> Workload:
@@ -119,7 +121,7 @@ def qwen3_8b_mixed(seed: int = 0) -> Workload:
     num_new = [1536] * 4 + [1] * 2048
     ends = [c + n for c, n in zip(num_cached, num_new)]
     return Workload("qwen3_8b_mixed", 32, 8, 128, 256, 24_000, num_cached, num_new,
-                    _tables(rng, 24_000, ends, 256), 1 / math.sqrt(128))
+                    _tables(rng, 24_000, ends, 256), 1 / math.sqrt(128), num_layers=36)
 
 
 def qwen3_8b_prefill(seed: int = 0) -> Workload:
@@ -127,7 +129,8 @@ def qwen3_8b_prefill(seed: int = 0) -> Workload:
     mixed = qwen3_8b_mixed(seed)
     rows = [i for i, n in enumerate(mixed.num_new) if n > 1]
     return Workload("qwen3_8b_prefill", 32, 8, 128, 256, 24_000, [mixed.num_cached[i] for i in rows],
-                    [mixed.num_new[i] for i in rows], [mixed.block_lists[i] for i in rows], 1 / math.sqrt(128))
+                    [mixed.num_new[i] for i in rows], [mixed.block_lists[i] for i in rows], 1 / math.sqrt(128),
+                    num_layers=36)
 
 
 def qwen3_8b_long(seed: int = 0) -> Workload:
@@ -135,7 +138,7 @@ def qwen3_8b_long(seed: int = 0) -> Workload:
     ctx = rng.integers(32768, 131072 + 1, size=16)
     num_cached = [int(c) - 1 for c in ctx]
     return Workload("qwen3_8b_long", 32, 8, 128, 256, 10_000, num_cached, [1] * 16,
-                    _tables(rng, 10_000, ctx, 256), 1 / math.sqrt(128))
+                    _tables(rng, 10_000, ctx, 256), 1 / math.sqrt(128), num_layers=36)
 
 
 def deepseek_v2_lite_mla(seed: int = 0, block_size: int = 64) -> Workload:
@@ -145,7 +148,7 @@ def deepseek_v2_lite_mla(seed: int = 0, block_size: int = 64) -> Workload:
     pool = 34_000 * 64 // block_size
     name = "deepseek_v2_lite_mla" if block_size == 64 else f"deepseek_v2_lite_mla_bs{block_size}"
     return Workload(name, 16, 1, 576, block_size, pool, num_cached, [1] * 128, _tables(rng, pool, ctx, block_size),
-                    1 / math.sqrt(192), value_std=0.5, latent_dim=576, v_dim=512)
+                    1 / math.sqrt(192), value_std=0.5, latent_dim=576, v_dim=512, num_layers=27)
 
 
 def deepseek_v2_lite_mla_prefill(seed: int = 0) -> Workload:
@@ -156,7 +159,7 @@ def deepseek_v2_lite_mla_prefill(seed: int = 0) -> Workload:
     ends = [c + n for c, n in zip(num_cached, num_new)]
     return Workload("deepseek_v2_lite_mla_prefill", 16, 1, 576, 64, 1024, num_cached, num_new,
                     _tables(rng, 1024, ends, 64), 1 / math.sqrt(192), value_std=0.5, latent_dim=576, v_dim=512,
-                    expanded=(192, 128))
+                    expanded=(192, 128), num_layers=27)
 
 
 WORKLOADS = {

@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
     lib = _capi.load()
     missing = [n for n in declared() if not hasattr(lib, n)]
     assert not missing, f"declared in lvattn.h but not exported: {missing}"
-    assert lib.lv_abi_version() == 6
+    assert lib.lv_abi_version() == 7
     assert all(n in _capi._PROTOTYPES for n in declared()), "every declared function has a ctypes prototype"
 
 
@@ -40,16 +40,16 @@ def test_bad_arguments_raise_with_the_library_message():
         _capi.call("lv_store_kvcache", None, None, 0, 0, 1, 1, 8, None, None, 0, 0, 0, 0, None, 2, None)
     with pytest.raises(_capi.LvError, match="head_dim 96"):
         _capi.call("lv_paged_attention", 1, 0, 0, 1, 1, 0, 0, 0, 16, 1, 0, None, 1, None, 1, 1, 8, 2, 96, 1.0, 1, 16,
-                   1, 0, 0, None, 0, 0, 0, 0, None)
+                   1, 0, 0, None, 0, 0, 0, 0, 0, None)
     with pytest.raises(_capi.LvError, match="not bf16 or fp16"):
         _capi.call("lv_paged_attention", 1, 0, 0, 1, 1, 0, 0, 0, 16, 1, 0, None, 1, None, 1, 1, 8, 2, 64, 1.0, 1, 16,
-                   1, 0, 0, None, 0, 0, 0, 7, None)
+                   1, 0, 0, None, 0, 0, 0, 0, 7, None)
     with pytest.raises(_capi.LvError, match="unknown schedule 5"):
         _capi.call("lv_paged_attention", 1, 0, 0, 1, 1, 0, 0, 0, 16, 1, 0, None, 1, None, 1, 1, 8, 2, 64, 1.0, 1, 16,
-                   1, 0, 0, None, 0, 5, 0, 0, None)
+                   1, 0, 0, None, 0, 5, 0, 0, 0, None)
     with pytest.raises(_capi.LvError, match="negative prompt_workgroups"):
         _capi.call("lv_paged_attention", 1, 0, 0, 1, 1, 0, 0, 0, 16, 1, 0, None, 1, None, 1, 1, 8, 2, 64, 1.0, 1, 16,
-                   1, 0, 0, None, 0, 2, -1, 0, None)
+                   1, 0, 0, None, 0, 2, -1, 0, 0, None)
 
 
 def test_workspace_query_sizes():
@@ -72,4 +72,4 @@ def test_the_static_workspace_refuses_a_step_that_needs_more():
     assert need > 16 << 20
     with pytest.raises(_capi.LvError, match=rf"needs {need} bytes of workspace; the static workspace holds 16777216"):
         _capi.call("lv_paged_attention_static", 16, 0, 0, 16, 16, 0, 0, 0, 256, 16, 0, 16, None, 16, 4096,
-                   tokens, 32, 8, 128, 1.0, 64, 1 << 20, 16, 0, 0, 0, 0, 0, None)
+                   tokens, 32, 8, 128, 1.0, 64, 1 << 20, 16, 0, 0, 0, 0, 0, 0, None)

@@ -280,9 +280,10 @@ def test_decode_replays_in_a_graph(cuda):
 @pytest.mark.parametrize("schedule", ["serial", "overlap"])
 def test_mixed_step_replays_in_a_graph(cuda, schedule, monkeypatch):
     """A captured mixed step (work-list plan, prompt kernel, decode kernel, split-K merge) replays with new queries
-    and cache contents; each replay equals an eager call, with eager work between replays. Under the overlapped
-    schedule the decode items run on the library's second stream, forked from and joined back into the capturing
-    stream by events, so the capture holds both branches."""
+    and cache contents; each replay equals an eager call, with eager work between replays. This step is small, so
+    its overlapped schedule is the one-launch form; the two-stream form (decode items forked onto the library's
+    second stream and joined back by events inside the capture) is captured in
+    test_layers_of_one_step_share_one_plan's 600-row mixed step."""
     from lvattn import backend as B
 
     sched = B.SCHEDULE_OVERLAP if schedule == "overlap" else B.SCHEDULE_SERIAL
@@ -445,3 +446,68 @@ def test_a_mixed_step_of_many_decode_rows_under_both_schedules(cuda, monkeypatch
         torch.testing.assert_close(out.float().cpu(), want, atol=2e-2, rtol=1e-2)
         outs[sched] = out
     assert torch.equal(outs[B.SCHEDULE_SERIAL], outs[B.SCHEDULE_OVERLAP])
+
+
+@pytest.mark.parametrize("kind", ["decode", "mixed-overlap", "mixed-serial", "small"])
+def test_layers_of_one_step_share_one_plan(cuda, kind, monkeypatch):
+    """Three layers (each with its own cache) attend through one step's Context: the first plans the work list, the
+    next two reuse it (LV_ATTN_REUSE_PLAN), so the persistent decode grid must leave its ticket at zero for them.
+    Each layer equals the same call on a fresh Context (which plans again), bit for bit; then the three layers are
+    captured in one graph (one plan launch in it) and every replay equals the eager layers."""
+    from lvattn import backend as B
+
+    gen = torch.Generator().manual_seed(31)
+    b = MI355XAttention(32, 128, 1 / math.sqrt(128), 8)
+    if kind == "decode":  # 256 rows: the persistent grid
+        lens = torch.randint(16, 601, (256,), generator=gen).tolist()
+        num_cached, num_new = [n - 1 for n in lens], [1] * 256
+    elif kind == "small":  # a few rows: one workgroup per item
+        num_cached, num_new = [300, 5000, 20], [1, 1, 1]
+    else:  # two chunks beside 600 decode rows (persistent grid beside the prompt tiles when overlapped)
+        dec = torch.randint(16, 601, (600,), generator=gen).tolist()
+        num_cached, num_new = [100, 0] + [n - 1 for n in dec], [40, 70] + [1] * 600
+        sched = B.SCHEDULE_OVERLAP if kind == "mixed-overlap" else B.SCHEDULE_SERIAL
+        monkeypatch.setattr(b, "_schedule", lambda context, elem_bytes: sched)
+    tables, step0 = _wide_step(cuda, num_cached, num_new, seed=2)
+    q = torch.cat(step0[0])
+    caches = [(step0[5], step0[6])]
+    for layer in range(2):  # two more layers: other keys and values in caches of the same shape
+        kc = torch.randn(step0[5].shape, generator=gen).to(torch.bfloat16).to(cuda)
+        vc = torch.randn(step0[6].shape, generator=gen).to(torch.bfloat16).to(cuda)
+        caches.append((kc, vc))
+    b.store_kvcache(step0[3], step0[4], *caches[0], step0[7])
+
+    template = (Context(context_lens=torch.tensor([c + n for c, n in zip(num_cached, num_new)], dtype=torch.int32,
+                                                  device=cuda),
+                        block_tables=torch.tensor(tables, dtype=torch.int32, device=cuda))
+                if kind in ("decode", "small") else context_for(num_cached, num_new, tables, cuda))
+
+    def context():
+        """A new step's Context over the same device tensors (no copies: it is also built inside the capture)."""
+        skip = ("attn_metadata", "decode_splits")  # per-step caches
+        return Context(**{k: getattr(template, k) for k in Context.__slots__ if k not in skip})
+
+    step = context()
+    shared = [b.forward(q, None, None, kc, vc, step) for kc, vc in caches]
+    torch.cuda.synchronize()
+    assert sum(1 for k in step.attn_metadata if k[0] == "plan") == 1
+    fresh = [b.forward(q, None, None, kc, vc, context()) for kc, vc in caches]
+    torch.cuda.synchronize()
+    for i, (x, y) in enumerate(zip(shared, fresh)):
+        assert torch.equal(x, y), f"layer {i}"
+    torch.testing.assert_close(shared[0].float().cpu(), dense_expected(step0[0], step0[1], step0[2],
+                                                                       1 / math.sqrt(128)), atol=2e-2, rtol=1e-2)
+    outs = [torch.empty_like(q) for _ in caches]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        g_step = context()
+        for (kc, vc), out in zip(caches, outs):
+            b.forward(q, None, None, kc, vc, g_step, out=out)
+    for rep in range(3):
+        q.copy_(torch.randn(q.shape, generator=gen).to(q.dtype))
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = [b.forward(q, None, None, kc, vc, context()) for kc, vc in caches]
+        torch.cuda.synchronize()
+        for i, (x, y) in enumerate(zip(outs, eager)):
+            assert torch.equal(x, y), f"replay {rep} layer {i}"

@@ -274,6 +274,7 @@ def test_the_opt_in_index_checks(monkeypatch):
         checks.check_query_rows(torch.tensor([0, 1, 4], **i32), torch.tensor([0, 9, 13], **i32), 5)
 
     monkeypatch.setenv("LVATTN_CHECK", "1")
+    monkeypatch.setattr(checks, "ENABLED", True)
     b = MI355XAttention(8, 64, 0.1, 2)
     k_cache = torch.zeros(4, 16, 2, 64, dtype=torch.bfloat16)
     key = torch.zeros(2, 2, 64, dtype=torch.bfloat16)
@@ -313,3 +314,43 @@ def test_the_merge_keeps_the_reference_signature():
     assert list(sig.parameters) == ["o_a", "lse_a", "o_b", "lse_b", "out"]
     assert sig.parameters["out"].default is None
     assert list(inspect.signature(merge_attention).parameters) == ["o_a", "lse_a", "o_b", "lse_b"]
+
+
+def test_layers_of_one_step_plan_once(monkeypatch):
+    """The work list is planned once per step: the first layer's call plans, every later layer with the same
+    Context passes LV_ATTN_REUSE_PLAN (the reference caches per-step plans in context.attn_metadata,
+    flash_backend.py:16-20,157-160). A new step's Context plans again, and so does a layer of another shape."""
+    from lvattn import _capi
+    from lvattn import backend as B
+
+    calls = []
+    monkeypatch.setattr(_capi, "call", lambda name, *args: calls.append((name, args)))
+    monkeypatch.setattr(_capi, "stream_of", lambda device: 0)
+    i32 = dict(dtype=torch.int32)
+
+    def flags_of(call):
+        name, args = call
+        assert name == "lv_paged_attention"
+        return args[-3]
+
+    cache = torch.zeros(8, 16, 2, 64, dtype=torch.bfloat16)
+    step = Context(context_lens=torch.tensor([40, 7], **i32), block_tables=torch.tensor([[0, 1, 2], [3, -1, -1]], **i32))
+    layer = MI355XAttention(8, 64, 0.1, 2)
+    q = torch.zeros(2, 8, 64, dtype=torch.bfloat16)
+    for _ in range(3):  # three layers of one step
+        layer.decode(q, cache, cache, step)
+    assert [flags_of(c) for c in calls] == [0, B.LV_ATTN_REUSE_PLAN, B.LV_ATTN_REUSE_PLAN]
+    calls.clear()
+    other = MI355XAttention(16, 64, 0.1, 2)  # another layer shape: its own plan
+    other.decode(torch.zeros(2, 16, 64, dtype=torch.bfloat16), cache, cache, step)
+    layer.decode(q, cache, cache, step)
+    assert [flags_of(c) for c in calls] == [0, B.LV_ATTN_REUSE_PLAN]
+    calls.clear()
+    nxt = Context(context_lens=step.context_lens.clone(), block_tables=step.block_tables.clone())
+    layer.decode(q, cache, cache, nxt)  # the next step
+    assert [flags_of(c) for c in calls] == [0]
+    calls.clear()
+    mixed = host_context([20, 0], [1, 9], [[0, 1], [2, -1]])  # a step with prompts: the same rule
+    for _ in range(2):
+        layer.prefill(torch.zeros(10, 8, 64, dtype=torch.bfloat16), None, None, cache, cache, mixed)
+    assert [flags_of(c) for c in calls] == [0, B.LV_ATTN_REUSE_PLAN]

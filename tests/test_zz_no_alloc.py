@@ -39,7 +39,7 @@ def call(name, b, q, kc, vc, ctx, out, *, decode, schedule):
         args += [ws.data_ptr(), ws.numel()]
     else:
         ws = None
-    _capi.call(name, *args, schedule, 0, _capi.DTYPES[q.dtype], _capi.stream_of(q.device))
+    _capi.call(name, *args, schedule, 0, 0, _capi.DTYPES[q.dtype], _capi.stream_of(q.device))
     torch.cuda.synchronize()
     return ws
 
