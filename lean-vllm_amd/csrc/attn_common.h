@@ -43,7 +43,7 @@ __device__ inline int key_len(const AttnParams& p, int row) {
 }
 
 // ---------------------------------------------------------------------------------------------------------
-// Prompt item: (row, tile of query positions, kv head). The 128 (position, head) query rows of one GQA group (32
+// Prompt item: (row, tile of query positions, kv head). The 32 WAVES (position, head) query rows of one GQA group (32
 // per wave, as two 16-row MFMA blocks that share every K and V operand read) run against 64-key tiles staged
 // row-major in LDS, the next tile's K/V loads in flight in registers meanwhile. S^T = K Q^T and O^T += V^T P^T on
 // MFMA 16x16x32 with fp32 accumulation; the V^T operands come from the row-major value tile by the transposing
@@ -66,7 +66,9 @@ struct PromptSmem {
 // RING > 0: tiles go straight from memory into a ring of RING LDS stages (smem holds RING * PromptSmem::kBytes),
 // RING - 1 in flight while one is consumed, one barrier per tile; for keys whose 64-key tiles each lie in one page
 // (unpaged, or pages a multiple of 64). The caller picks it; the register path serves every other page size.
-template <typename T, int DQK, int DV, bool PREFETCH = true, bool OPAQUE_TID = false, int RING = 0>
+// WAVES: waves of the workgroup (blockDim.x == 64 WAVES), each taking 32 query rows; an item is 32 WAVES rows, so
+// with 8 waves every staged K/V tile serves twice the rows of a 4-wave item.
+template <typename T, int DQK, int DV, bool PREFETCH = true, bool OPAQUE_TID = false, int RING = 0, int WAVES = 4>
 __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, char* smem) {
   using E = Elem<T>;
   constexpr int KS = DQK / 32;  // MFMA k-steps over the q.k width
@@ -75,9 +77,13 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
   constexpr int VROW = PromptSmem<DQK, DV>::kVRow;
   constexpr int KCH = DQK / 8, VCH = DV / 8;  // 16-byte chunks per key / value row
   constexpr int KCHUNKS = kPrefillKeys * KCH;
-  constexpr int KPER = KCHUNKS / 256;                   // key chunks each thread stages per tile
-  constexpr int PER = kPrefillKeys * (KCH + VCH) / 256;  // all chunks each thread stages per tile
-  static_assert(KCHUNKS % 256 == 0 && kPrefillKeys * (KCH + VCH) % 256 == 0, "tile chunks split over 256 threads");
+  constexpr int NT = 64 * WAVES;                        // threads
+  constexpr int ROWS = 32 * WAVES;                      // (position, head) query rows per item
+  constexpr int KPER = KCHUNKS / NT;                    // key chunks each thread stages per tile
+  constexpr int PER = kPrefillKeys * (KCH + VCH) / NT;  // all chunks each thread stages per tile
+  static_assert(WAVES == 4 || WAVES == 8, "4 or 8 waves");
+  static_assert(RING > 0 || (KCHUNKS % NT == 0 && kPrefillKeys * (KCH + VCH) % NT == 0),
+                "tile chunks split over the threads");
   static_assert(DQK % 32 == 0 && DV % 16 == 0, "MFMA tile widths");
   int tid = threadIdx.x;
   if (OPAQUE_TID) asm volatile("" : "+v"(tid));
@@ -85,7 +91,7 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, j4 = lane >> 4;
   const int G = p.group;
-  const int qp = kPrefillRows / G;  // positions per item
+  const int qp = ROWS / G;  // positions per item
   const int q0 = p.cu_q[row], lq = p.cu_q[row + 1] - q0;
   const int lk = key_len(p, row);
   const int p0 = qtile * qp;
@@ -119,9 +125,9 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
     for (int b = 0; b < DB; ++b) o[nb][b] = f32x4{0, 0, 0, 0};
 
   // Staging: chunk i of this thread is key key_of(i) (a tile row), 16-byte part part_of(i).
-  auto key_of = [&](int i) { return i < KPER ? (tid + 256 * i) / KCH : (tid + 256 * i - KCHUNKS) / VCH; };
+  auto key_of = [&](int i) { return i < KPER ? (tid + NT * i) / KCH : (tid + NT * i - KCHUNKS) / VCH; };
   auto part_of = [&](int i) {
-    return i < KPER ? (tid + 256 * i) % KCH : (tid + 256 * i - KCHUNKS) % VCH;
+    return i < KPER ? (tid + NT * i) % KCH : (tid + NT * i - KCHUNKS) % VCH;
   };
   const int32_t* table = p.tables + (int64_t)row * p.t_stride;
   const int kbase = p.paged ? 0 : p.cu_k[row];
@@ -251,15 +257,16 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
   if constexpr (RING > 0) {
     // Stage layout: key rows of KCH data slots + 1 pad slot, then value rows of VCH + 2 (the tile pitches); the
     // pad slots hold a copy of the row's last chunk. 64-lane load j covers slots 64 j .. 64 j + 63; wave w issues
-    // j = w, w + 4, ... Keys at or past lk load key lk - 1 instead (finite values; their weight is 0).
+    // j = w, w + WAVES, ... Keys at or past lk load key lk - 1 instead (finite values; their weight is 0).
     constexpr int KJ = KCH + 1, VJ = VCH + 2;  // loads per stage for the key / value rows (64 keys each)
     constexpr int NJ = KJ + VJ;
-    constexpr int CNT_HI = (NJ + 3) / 4, CNT_LO = NJ / 4;  // this wave's loads per stage: waves < NJ % 4 take HI
+    // this wave's loads per stage: waves < NJ % WAVES take HI
+    constexpr int CNT_HI = (NJ + WAVES - 1) / WAVES, CNT_LO = NJ / WAVES;
     constexpr int kStageElems = PromptSmem<DQK, DV>::kBytes / 2;
     static_assert(PromptSmem<DQK, DV>::kKRow == KJ * 8 && PromptSmem<DQK, DV>::kVRow == VJ * 8, "pitches");
     static_assert(RING >= 2 && RING <= 3, "one or two tiles in flight");
     uint16_t* ring = reinterpret_cast<uint16_t*>(smem);
-    const bool hi = wave < NJ % 4 || NJ % 4 == 0;
+    const bool hi = wave < NJ % WAVES || NJ % WAVES == 0;
     // Stages fill in key order, so the page of the last fill is kept: one page-table lookup per page, shared by
     // the key and value sources (a page of 256 keys holds four tiles).
     int cached_pg = -1;
@@ -283,8 +290,8 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
       const char* kb = p.k_cache + koff;
       const char* vb = p.v_cache + voff;
 #pragma unroll
-      for (int i = 0; i < (NJ + 3) / 4; ++i) {
-        const int j = wave + 4 * i;
+      for (int i = 0; i < (NJ + WAVES - 1) / WAVES; ++i) {
+        const int j = wave + WAVES * i;
         if (j < NJ) {
           uint32_t off;
           const char* b;

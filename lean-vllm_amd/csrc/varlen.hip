@@ -10,42 +10,74 @@
 
 namespace lv {
 
-// Keys are packed, so every 64-key tile is contiguous: tiles stream through an LDS ring. Two workgroups fit a CU
-// up to 128-wide q.k; wider tiles take one (and its registers).
+// Keys are packed, so every 64-key tile is contiguous: tiles stream through an LDS ring. Up to 128-wide q.k two
+// 4-wave workgroups fit a CU; a 192-wide stage pair (88 KB of LDS) leaves room for one workgroup, which then takes 8
+// waves (256 query rows per item, two waves per SIMD, each staged tile serving twice the rows).
 template <int DQK, int DV>
 struct VarlenCfg {
-  static constexpr int kRing = 2;
-  static constexpr int kSmem = (kRing > 0 ? kRing : 1) * PromptSmem<DQK, DV>::kBytes;
-  static constexpr int kWaves = kSmem <= 80 * 1024 && DQK <= 128 ? 2 : 1;
+  static constexpr int kPerCu = 2 * PromptSmem<DQK, DV>::kBytes <= 80 * 1024 ? 2 : 1;  // workgroups per CU
+  static constexpr int kRing = 2;  // a third stage for the one-per-CU tiles measured 6% slower
+  static constexpr int kSmem = kRing * PromptSmem<DQK, DV>::kBytes;
+  static constexpr int kWaves = kPerCu == 2 ? 4 : 8;        // waves per workgroup
+  static constexpr int kRows = 32 * kWaves;                  // (position, head) query rows per item
 };
 
 constexpr int kXcds = 8;  // workgroups are dealt round-robin over the XCDs by their linear index
 
-// Item w = (kv head, row, query tile), query tiles innermost. Workgroup b (on XCD b % 8) takes item
-// start(b % 8) + b / 8, so each XCD runs a contiguous range of items: the query tiles of one (row, kv head),
-// which read the same key and value tiles, share an L2 instead of fetching them once per XCD.
+// Items (kv head, row, query tile) are dealt to the XCDs in contiguous ranges of (kv head, row) groups: the query
+// tiles of one (row, kv head), which read the same key and value tiles, share an L2 instead of fetching them once
+// per XCD. Workgroup b runs on XCD b % 8 and is that XCD's (b / 8)-th workgroup. Unmasked, every query tile of a row
+// walks all its keys: an XCD's items go out group by group, so a group's tiles run together and read each key tile
+// once from memory (query tiles outermost cost 1.5x the time on DeepSeek-V2-Lite's prefix chunks). Causal, query
+// tile t walks t + 1 tiles' worth of keys: the items go out by descending query tile, then group, so the long ones
+// start first and the short ones fill the tail (0.67x the time of group order on its 1536-token chunks).
 template <typename T, int DQK, int DV>
-__global__ __launch_bounds__(256, (VarlenCfg<DQK, DV>::kWaves)) void varlen_kernel(AttnParams p, int32_t qtiles) {
-  __shared__ __attribute__((aligned(16))) char smem[VarlenCfg<DQK, DV>::kSmem];
-  const int n = gridDim.x, b = blockIdx.x, x = b % kXcds;
-  const int w = x * (n / kXcds) + min(x, n % kXcds) + b / kXcds;
-  const int per_head = p.rows * qtiles;
-  const int kvh = w / per_head, rest = w - kvh * per_head;
-  const int row = rest / qtiles, qt = rest - row * qtiles;
-  prefill_item<T, DQK, DV, true, false, VarlenCfg<DQK, DV>::kRing>(p, row, qt, kvh, smem);
+__global__ __launch_bounds__((64 * VarlenCfg<DQK, DV>::kWaves), (VarlenCfg<DQK, DV>::kPerCu)) void varlen_kernel(
+    AttnParams p, int32_t qtiles) {
+  using Cfg = VarlenCfg<DQK, DV>;
+  __shared__ __attribute__((aligned(16))) char smem[Cfg::kSmem];
+  const int groups = p.rows * p.hkv;  // (kv head, row) groups
+  const int x = blockIdx.x % kXcds, k = blockIdx.x / kXcds;
+  const int g0 = x * (groups / kXcds) + min(x, groups % kXcds);   // this XCD's first group
+  const int ng = groups / kXcds + (x < groups % kXcds ? 1 : 0);    // and its number of groups
+  if (k >= ng * qtiles) return;  // the grid is rounded up to whole XCD rounds
+  const int qt = p.causal ? qtiles - 1 - k / ng : k % qtiles;
+  const int g = g0 + (p.causal ? k % ng : k / qtiles);
+  const int kvh = g / p.rows, row = g - kvh * p.rows;
+  prefill_item<T, DQK, DV, true, false, Cfg::kRing, Cfg::kWaves>(p, row, qt, kvh, smem);
+}
+
+// Query tiles per row of at most max_seqlen_q queries, for a (q.k, v) width pair; 0 for unsupported widths.
+static int64_t varlen_qtiles(int dqk, int dv, int group, int max_seqlen_q) {
+  int rows = 0;
+  if (dqk == 64 && dv == 64) rows = VarlenCfg<64, 64>::kRows;
+  else if (dqk == 128 && dv == 128) rows = VarlenCfg<128, 128>::kRows;
+  else if (dqk == 192 && dv == 128) rows = VarlenCfg<192, 128>::kRows;
+  else if (dqk == 192 && dv == 192) rows = VarlenCfg<192, 192>::kRows;
+  if (rows == 0 || group > rows) return 0;
+  const int qp = rows / group;
+  return (max_seqlen_q + qp - 1) / qp;
+}
+
+template <typename T, int DQK, int DV>
+static void launch_one(const AttnParams& p, int qtiles, hipStream_t st) {
+  // Each XCD gets a whole number of (kv head, row) groups: ceil(groups / 8) groups' items per XCD.
+  const int64_t groups = (int64_t)p.rows * p.hkv;
+  const int64_t per_xcd = (groups + kXcds - 1) / kXcds * qtiles;
+  hipLaunchKernelGGL((varlen_kernel<T, DQK, DV>), dim3(per_xcd * kXcds), dim3(64 * VarlenCfg<DQK, DV>::kWaves), 0, st,
+                     p, qtiles);
 }
 
 template <typename T>
 static int launch_varlen(const AttnParams& p, int dqk, int dv, int qtiles, hipStream_t st) {
-  const dim3 grid(p.rows * qtiles * p.hkv);
   if (dqk == 64 && dv == 64)
-    hipLaunchKernelGGL((varlen_kernel<T, 64, 64>), grid, dim3(256), 0, st, p, qtiles);
+    launch_one<T, 64, 64>(p, qtiles, st);
   else if (dqk == 128 && dv == 128)
-    hipLaunchKernelGGL((varlen_kernel<T, 128, 128>), grid, dim3(256), 0, st, p, qtiles);
+    launch_one<T, 128, 128>(p, qtiles, st);
   else if (dqk == 192 && dv == 128)
-    hipLaunchKernelGGL((varlen_kernel<T, 192, 128>), grid, dim3(256), 0, st, p, qtiles);
+    launch_one<T, 192, 128>(p, qtiles, st);
   else if (dqk == 192 && dv == 192)
-    hipLaunchKernelGGL((varlen_kernel<T, 192, 192>), grid, dim3(256), 0, st, p, qtiles);
+    launch_one<T, 192, 192>(p, qtiles, st);
   else {
     set_error("varlen_attention: head dims (q.k %d, v %d) are not (64, 64), (128, 128), (192, 128) or (192, 192)",
               dqk, dv);
@@ -108,9 +140,11 @@ extern "C" int lv_varlen_attention(const void* q, int64_t q_stride_t, int64_t q_
   p.lse = lse;
   p.lse_st = lse_stride_t;
   p.lse_sh = lse_stride_h;
-  const int qp = kPrefillRows / p.group;
-  const int64_t qtiles = (max_seqlen_q + qp - 1) / qp;
-  LV_REQUIRE(qtiles * num_rows * num_kv_heads < ((int64_t)1 << 31), "varlen_attention: grid too large");
+  const int64_t qtiles = varlen_qtiles(head_dim_qk, head_dim_v, p.group, max_seqlen_q);
+  LV_REQUIRE(qtiles > 0, "varlen_attention: head dims (q.k %d, v %d) are not (64, 64), (128, 128), (192, 128) or "
+             "(192, 192)", head_dim_qk, head_dim_v);
+  LV_REQUIRE((((int64_t)num_rows * num_kv_heads + kXcds - 1) / kXcds) * qtiles * kXcds < ((int64_t)1 << 31),
+             "varlen_attention: grid too large");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   return dtype == LV_DTYPE_BF16 ? launch_varlen<BF16>(p, head_dim_qk, head_dim_v, (int)qtiles, st)
                                 : launch_varlen<F16>(p, head_dim_qk, head_dim_v, (int)qtiles, st);
