@@ -123,6 +123,9 @@ int lv_store_latents(const void* latent, int64_t latent_stride_t, int32_t num_to
  * 157-160). The library honours the flag only if the last plan it made in this workspace was for the same shape and
  * pointers, and plans again otherwise; unchanged contents are the caller's promise. */
 #define LV_ATTN_REUSE_PLAN 1
+/* flags, also: LV_ATTN_PROMPTS_ONLY -- every row of the step has more than one query (the caller's host lengths say
+ * so), so no decode launch and no split-K merge are made. Needs cu_seqlens_q and max_seqlen_q > 1. */
+#define LV_ATTN_PROMPTS_ONLY 2
 size_t lv_paged_attention_workspace_bytes(int32_t num_rows, int32_t num_tokens, int32_t num_heads,
                                           int32_t num_kv_heads, int32_t head_dim, int32_t max_seqlen_k,
                                           int32_t decode_only);

@@ -668,9 +668,13 @@ static void launch_prompt_list(const AttnParams& p, const Shape& s, bool ring, h
 // launch leaves the two streams unordered and is returned as LV_EHIP.
 template <typename T, int D, int GS>
 static int launch(const AttnParams& p, bool listed, bool mixed, bool overlap, int prompt_wgs, const Shape& s,
-                  hipStream_t stream) {
+                  hipStream_t stream, bool prompts_only) {
   const int ny = p.hkv * p.qgroups;
   const bool ring = p.bs.d % kPrefillKeys == 0;  // every 64-key tile in one page
+  if (prompts_only) {  // a step of prompts: the prompt tiles on the whole GPU, nothing else
+    launch_prompt_list<T, D>(p, s, ring, stream);
+    return LV_OK;
+  }
   if (overlap && listed && mixed) {
     // A step whose workgroups (bounds: most prompt bounds exit at once) fill the GPU at most kSmallStepRounds times
     // runs as one launch.
@@ -731,18 +735,18 @@ static int launch(const AttnParams& p, bool listed, bool mixed, bool overlap, in
 
 template <typename T, int D>
 static int launch_gs(const AttnParams& p, int gs, bool listed, bool mixed, bool overlap, int prompt_wgs,
-                     const Shape& s, hipStream_t stream) {
-  if (gs == 4) return launch<T, D, 4>(p, listed, mixed, overlap, prompt_wgs, s, stream);
-  if (gs == 2) return launch<T, D, 2>(p, listed, mixed, overlap, prompt_wgs, s, stream);
-  return launch<T, D, 1>(p, listed, mixed, overlap, prompt_wgs, s, stream);
+                     const Shape& s, hipStream_t stream, bool prompts_only) {
+  if (gs == 4) return launch<T, D, 4>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
+  if (gs == 2) return launch<T, D, 2>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
+  return launch<T, D, 1>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
 }
 
 template <typename T>
 static int launch_d(const AttnParams& p, int d, int gs, bool listed, bool mixed, bool overlap, int prompt_wgs,
-                    const Shape& s, hipStream_t stream) {
+                    const Shape& s, hipStream_t stream, bool prompts_only) {
   switch (d) {
-    case 64: return launch_gs<T, 64>(p, gs, listed, mixed, overlap, prompt_wgs, s, stream);
-    case 128: return launch_gs<T, 128>(p, gs, listed, mixed, overlap, prompt_wgs, s, stream);
+    case 64: return launch_gs<T, 64>(p, gs, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
+    case 128: return launch_gs<T, 128>(p, gs, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
     default: set_error("paged_attention: head_dim %d is not 64 or 128", d); return LV_EINVAL;
   }
 }
@@ -835,7 +839,10 @@ static int paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h
   LV_REQUIRE(schedule == LV_SCHEDULE_AUTO || schedule == LV_SCHEDULE_SERIAL || schedule == LV_SCHEDULE_OVERLAP,
              "paged_attention: unknown schedule %d", schedule);
   LV_REQUIRE(prompt_workgroups >= 0, "paged_attention: negative prompt_workgroups %d", prompt_workgroups);
-  LV_REQUIRE((flags & ~LV_ATTN_REUSE_PLAN) == 0, "paged_attention: unknown flags 0x%x", flags);
+  LV_REQUIRE((flags & ~(LV_ATTN_REUSE_PLAN | LV_ATTN_PROMPTS_ONLY)) == 0, "paged_attention: unknown flags 0x%x",
+             flags);
+  LV_REQUIRE(!(flags & LV_ATTN_PROMPTS_ONLY) || (cu_seqlens_q && max_seqlen_q > 1),
+             "paged_attention: LV_ATTN_PROMPTS_ONLY needs cu_seqlens_q and max_seqlen_q > 1");
   if (num_rows == 0 || num_tokens == 0) return LV_OK;
   LV_REQUIRE(num_heads > 0 && num_kv_heads > 0 && num_heads % num_kv_heads == 0,
              "paged_attention: %d query heads do not group over %d key heads", num_heads, num_kv_heads);
@@ -936,9 +943,11 @@ static int paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h
     LV_LAUNCH_CHECK("plan_kernel");
   }
   const bool overlap = schedule != LV_SCHEDULE_SERIAL;
+  const bool prompts_only = (flags & LV_ATTN_PROMPTS_ONLY) != 0;
   const int rc =
-      dtype == LV_DTYPE_BF16 ? launch_d<BF16>(p, head_dim, s.gs, listed, mixed, overlap, prompt_workgroups, s, st)
-                             : launch_d<F16>(p, head_dim, s.gs, listed, mixed, overlap, prompt_workgroups, s, st);
+      dtype == LV_DTYPE_BF16
+          ? launch_d<BF16>(p, head_dim, s.gs, listed, mixed, overlap, prompt_workgroups, s, st, prompts_only)
+          : launch_d<F16>(p, head_dim, s.gs, listed, mixed, overlap, prompt_workgroups, s, st, prompts_only);
   if (rc != LV_OK) return rc;
   LV_LAUNCH_CHECK("paged_attention_kernel");
   return LV_OK;

@@ -56,7 +56,7 @@ _WORKSPACE = _Workspace()
 
 # Launch schedules of a step with prompt rows (LV_SCHEDULE_* of lvattn.h).
 SCHEDULE_AUTO, SCHEDULE_SERIAL, SCHEDULE_OVERLAP = 0, 1, 2
-LV_ATTN_REUSE_PLAN = 1
+LV_ATTN_REUSE_PLAN, LV_ATTN_PROMPTS_ONLY = 1, 2  # flags of lv_paged_attention
 # Measured MI355X rates the schedule choice compares (bf16, head_dim 128). Overlapped, the prompt tiles run at
 # about 0.18 PFLOP/s (one workgroup on half the CUs, beside the decode rows) against 0.84 PFLOP/s alone on the whole
 # GPU, and the decode rows stream about 6.6 TB/s. Overlap wins while the prompt tiles' extra time beside the decode
@@ -149,7 +149,7 @@ class MI355XAttention(AttentionBackend):
 
     # -- attention -----------------------------------------------------------------------------------------
     def _attend(self, q, k_cache, v_cache, out, *, context, block_tables, cu_seqlens_q, seqlens_k, cu_seqlens_k,
-                rows, max_seqlen_q, max_seqlen_k, schedule=SCHEDULE_AUTO, prompt_workgroups=0):
+                rows, max_seqlen_q, max_seqlen_k, schedule=SCHEDULE_AUTO, prompt_workgroups=0, prompts_only=False):
         qs, cs = q.stride(), k_cache.stride()
         assert q.dtype in _capi.DTYPES and k_cache.dtype == q.dtype == v_cache.dtype
         assert qs[2] == 1 and cs == v_cache.stride() and cs[3] == 1
@@ -176,6 +176,8 @@ class MI355XAttention(AttentionBackend):
             planned = meta[key] = [nbytes, None, (cu_seqlens_q, seqlens_k, cu_seqlens_k)]  # holds the tensors
         ws = _WORKSPACE.get(q.device, planned[0])
         flags = LV_ATTN_REUSE_PLAN if ws is not None and planned[1] is ws else 0
+        if prompts_only:
+            flags |= LV_ATTN_PROMPTS_ONLY
         planned[1] = ws
         bt = block_tables
         _capi.call("lv_paged_attention", q.data_ptr(), qs[0], qs[1], k_cache.data_ptr(), v_cache.data_ptr(), cs[0],
@@ -221,7 +223,14 @@ class MI355XAttention(AttentionBackend):
             cache[key] = SCHEDULE_OVERLAP if overlap else SCHEDULE_SERIAL
             decode_s = decode_bytes / DECODE_BYTES_PER_S
             cache[key + ("workgroups",)] = int(prompt_flops / PROMPT_WORKGROUP_FLOPS_PER_S / decode_s) if overlap else 0
+            cache[key + ("prompts_only",)] = lo == 0 and all(cu_q[r + 1] - cu_q[r] > 1 for r in range(rows))
         return cache[key]
+
+    def _prompts_only(self, context: Context, elem_bytes: int) -> bool:
+        """Whether every row of the step has more than one query, as ``_schedule`` found from the host lengths."""
+        cache = context.attn_metadata or {}
+        return cache.get(("schedule", self.num_heads, self.num_kv_heads, self.head_dim, elem_bytes, "prompts_only"),
+                         False)
 
     def _prompt_workgroups(self, context: Context, elem_bytes: int) -> int:
         """CUs that hold a prompt workgroup in this step's overlap, as ``_schedule`` sized them (0: the library's
@@ -266,7 +275,8 @@ class MI355XAttention(AttentionBackend):
                             cu_seqlens_k=cu_k if cu_k.dtype == torch.int32 else cu_k.to(torch.int32), rows=cu_q.numel() - 1,
                             max_seqlen_q=max_q, max_seqlen_k=max_k,
                             schedule=self._schedule(context, q.element_size()),
-                            prompt_workgroups=self._prompt_workgroups(context, q.element_size()))
+                            prompt_workgroups=self._prompt_workgroups(context, q.element_size()),
+                            prompts_only=self._prompts_only(context, q.element_size()))
 
     def mla_decode(self, q, latent_cache, v_dim, context: Context, out=None):
         """Each row's last ``Lq`` queries against its paged latents, read as one key head shared by every query

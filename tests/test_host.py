@@ -354,3 +354,21 @@ def test_layers_of_one_step_plan_once(monkeypatch):
     for _ in range(2):
         layer.prefill(torch.zeros(10, 8, 64, dtype=torch.bfloat16), None, None, cache, cache, mixed)
     assert [flags_of(c) for c in calls] == [0, B.LV_ATTN_REUSE_PLAN]
+
+
+def test_a_step_of_prompts_says_so(monkeypatch):
+    """A step whose rows all have several queries passes LV_ATTN_PROMPTS_ONLY (no decode launch, no merge); a step
+    with one decode row among its chunks does not."""
+    from lvattn import _capi
+    from lvattn import backend as B
+
+    calls = []
+    monkeypatch.setattr(_capi, "call", lambda name, *args: calls.append(args[-3]))
+    monkeypatch.setattr(_capi, "stream_of", lambda device: 0)
+    layer = MI355XAttention(8, 64, 0.1, 2)
+    cache = torch.zeros(8, 16, 2, 64, dtype=torch.bfloat16)
+    prompts = host_context([20, 0], [3, 9], [[0, 1], [2, -1]])
+    layer.prefill(torch.zeros(12, 8, 64, dtype=torch.bfloat16), None, None, cache, cache, prompts)
+    mixed = host_context([20, 0], [1, 9], [[0, 1], [2, -1]])
+    layer.prefill(torch.zeros(10, 8, 64, dtype=torch.bfloat16), None, None, cache, cache, mixed)
+    assert [bool(f & B.LV_ATTN_PROMPTS_ONLY) for f in calls] == [True, False]
