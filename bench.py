@@ -42,7 +42,8 @@ PEAK_HBM_GBS = 8000.0
 PEAK_BF16_TFLOPS = 2500.0
 METRIC = "paged-attn HBM GB/s (% of peak) + tokens/s per layer, Qwen3-8B mixed batch"
 EXTRA = ("qwen3_8b_decode,qwen3_8b_long,deepseek_v2_lite_mla,qwen3_0_6b_mixed,qwen3_8b_prefill,"
-         "deepseek_v2_lite_mla_prefill,qwen3_8b_decode_bs16,deepseek_v2_lite_mla_bs16")
+         "deepseek_v2_lite_mla_prefill,deepseek_v2_lite_mla_prefill_two_pass,qwen3_8b_decode_bs16,"
+         "deepseek_v2_lite_mla_bs16")
 RIDGE_FLOP_PER_BYTE = PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)  # above it a step is MFMA-bound
 
 
@@ -150,10 +151,14 @@ def measure(name: str, steps: int, warmup: int, seed: int, dev, layers: int | No
             if wl.is_mla_prefill:
                 ex = x.expanded
                 cu_q, max_q = ctx["cu_seqlens_q"], ctx["max_seqlen_q"]
-                o, lse = backend.varlen_with_lse(ex["q"], ex["k"], ex["v"], cu_q, cu_q, max_q, max_q, True)
-                co, clse = backend.varlen_with_lse(ex["q"], ex["k_ctx"], ex["v_ctx"], cu_q, cu_ctx, max_q, max_ctx,
-                                                   False)
-                merge_attention_(co, clse, o, lse, out)
+                if wl.two_pass:  # the reference layer's calls
+                    o, lse = backend.varlen_with_lse(ex["q"], ex["k"], ex["v"], cu_q, cu_q, max_q, max_q, True)
+                    co, clse = backend.varlen_with_lse(ex["q"], ex["k_ctx"], ex["v_ctx"], cu_q, cu_ctx, max_q,
+                                                       max_ctx, False)
+                    merge_attention_(co, clse, o, lse, out)
+                else:  # one call over context and new keys
+                    backend.prefill_with_context(ex["q"], ex["k"], ex["v"], ex["k_ctx"], ex["v_ctx"], cu_q, cu_ctx,
+                                                 max_q, out=out)
             elif wl.is_mla:
                 backend.mla_decode(x.q, x.k_cache, wl.v_dim, context, out=out)
             else:
@@ -319,8 +324,10 @@ def cpu_baseline(wl, t, dec_sample: int = 256, passes: int = 5):
 
 def attention_op(wl) -> str:
     """The kernels of one attention op on this workload (the roofline's subject)."""
-    if wl.is_mla_prefill:
+    if wl.is_mla_prefill and wl.two_pass:
         return "lv_varlen_attention x2 (causal new tokens, unmasked prefix; varlen_kernel) + lv_merge_attn_states"
+    if wl.is_mla_prefill:
+        return "lv_varlen_context_attention (varlen_kernel over prefix then causal new keys, one softmax)"
     if wl.is_mla:
         return "lv_mla_decode (mla_run_kernel + mla_run_merge_kernel)"
     if all(n > 1 for n in wl.num_new):  # a step of prompts: the serial schedule, prompt tiles on the whole GPU

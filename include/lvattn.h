@@ -29,7 +29,7 @@ extern "C" {
 #define LV_SCHEDULE_SERIAL 1
 #define LV_SCHEDULE_OVERLAP 2
 
-#define LV_ABI_VERSION 7
+#define LV_ABI_VERSION 8
 
 /* The last error message of the calling thread ("" if none). */
 const char* lv_last_error(void);
@@ -177,6 +177,25 @@ int lv_varlen_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h, c
                         int32_t num_kv_heads, int32_t head_dim_qk, int32_t head_dim_v, float scale, int32_t causal,
                         int32_t max_seqlen_q, void* out, int64_t out_stride_t, int64_t out_stride_h, float* lse,
                         int64_t lse_stride_t, int64_t lse_stride_h, int32_t dtype, void* stream);
+
+/* MLA prefill over cached context in one call. Replaces the sequence MLAAttention._prefill runs for a step whose
+ * cached keys form one chunk (lean_vllm/layers/attention.py:280-316): varlen_with_lse over the new tokens (causal),
+ * varlen_with_lse over the expanded context keys (unmasked), then merge_attention_ of the two -- the same
+ * attention, computed as one softmax per query over [context keys; new keys] with no partial outputs.
+ *
+ * As lv_varlen_attention with causal = 1, plus each row's context keys ctx_k: [Tc, Hkv, head_dim_qk], ctx_v:
+ * [Tc, Hkv, head_dim_v] (token and head strides in elements, unit dim stride), rows given by cu_seqlens_ctx
+ * [num_rows + 1] (device; a row may have none). Every query of a row sees all of its context keys, then its own
+ * keys under the causal mask. lse (optional) is over both. No workspace. */
+int lv_varlen_context_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k,
+                                int64_t k_stride_t, int64_t k_stride_h, const void* v, int64_t v_stride_t,
+                                int64_t v_stride_h, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                const void* ctx_k, int64_t ctx_k_stride_t, int64_t ctx_k_stride_h, const void* ctx_v,
+                                int64_t ctx_v_stride_t, int64_t ctx_v_stride_h, const int32_t* cu_seqlens_ctx,
+                                int32_t num_rows, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim_qk,
+                                int32_t head_dim_v, float scale, int32_t max_seqlen_q, void* out,
+                                int64_t out_stride_t, int64_t out_stride_h, float* lse, int64_t lse_stride_t,
+                                int64_t lse_stride_h, int32_t dtype, void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------
  * MLA absorbed decode. Replaces AttentionBackend.mla_decode (lean_vllm/attention/abstract.py:206-219; math of

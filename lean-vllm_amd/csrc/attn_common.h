@@ -36,6 +36,11 @@ struct AttnParams {
   const int2* items;
   const int32_t* n_items;  // [0]: list length, [1]: prompt items at its head
   int32_t* ticket;         // next decode item of a persistent launch (zeroed by the plan kernel)
+  // Packed keys only: a row's context keys, seen unmasked before the row's own keys (prefill_item's CTX).
+  const char* ctx_k;  // [Tc, Hkv, DQK]
+  const char* ctx_v;  // [Tc, Hkv, DV]
+  int64_t cx_st, cx_sh, cv_st, cv_sh;  // bytes: context key / value row and head strides
+  const int32_t* cu_ctx;               // [rows + 1]
 };
 
 __device__ inline int key_len(const AttnParams& p, int row) {
@@ -68,7 +73,11 @@ struct PromptSmem {
 // (unpaged, or pages a multiple of 64). The caller picks it; the register path serves every other page size.
 // WAVES: waves of the workgroup (blockDim.x == 64 WAVES), each taking 32 query rows; an item is 32 WAVES rows, so
 // with 8 waves every staged K/V tile serves twice the rows of a 4-wave item.
-template <typename T, int DQK, int DV, bool PREFETCH = true, bool OPAQUE_TID = false, int RING = 0, int WAVES = 4>
+// CTX (packed keys, RING > 0): the row's context keys (p.ctx_k / p.ctx_v, rows p.cu_ctx) come first, every one
+// visible to every query, then the row's own keys under the mask above -- one softmax over both, as the attention
+// over [context; own keys] with the mask aligned to the end.
+template <typename T, int DQK, int DV, bool PREFETCH = true, bool OPAQUE_TID = false, int RING = 0, int WAVES = 4,
+          bool CTX = false>
 __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, char* smem) {
   using E = Elem<T>;
   constexpr int KS = DQK / 32;  // MFMA k-steps over the q.k width
@@ -85,6 +94,7 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
   static_assert(RING > 0 || (KCHUNKS % NT == 0 && kPrefillKeys * (KCH + VCH) % NT == 0),
                 "tile chunks split over the threads");
   static_assert(DQK % 32 == 0 && DV % 16 == 0, "MFMA tile widths");
+  static_assert(!CTX || RING > 0, "context keys stream through the LDS ring");
   int tid = threadIdx.x;
   if (OPAQUE_TID) asm volatile("" : "+v"(tid));
   const int lane = tid & 63;
@@ -116,6 +126,13 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
                              : u32x4{0, 0, 0, 0};
   }
   const int kmax = p.causal ? min(lk, lk - lq + min(p0 + qp, lq)) : lk;  // keys the item needs
+  int lc = 0, cbase = 0;  // the row's context keys
+  if constexpr (CTX) {
+    cbase = p.cu_ctx[row];
+    lc = p.cu_ctx[row + 1] - cbase;
+  }
+  const int nc = (lc + kPrefillKeys - 1) / kPrefillKeys;                  // context tiles
+  const int ntiles = nc + (kmax + kPrefillKeys - 1) / kPrefillKeys;       // all tiles of the item
 
   float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};  // raw-score running max and row sums
   f32x4 o[2][DB];
@@ -170,8 +187,9 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
     }
   };
 
-  // One 64-key tile from the K/V tile in LDS at ks / vs: scores, mask, online softmax, P.V.
-  auto consume = [&](int kt, const uint16_t* ks, const uint16_t* vs) {
+  // One 64-key tile (keys kt .. kt + 63 of its source) from the K/V tile in LDS at ks / vs: scores, mask (query row
+  // nb sees keys < l[nb]), online softmax, P.V.
+  auto consume = [&](int kt, const int (&lm)[2], const uint16_t* ks, const uint16_t* vs) {
     // S^T (keys x query rows): st[kb][nb] lane holds keys kt + 16 kb + 4 j4 + r of query row (nb, n).
     f32x4 st[4][2];
 #pragma unroll
@@ -187,14 +205,14 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
         for (int nb = 0; nb < 2; ++nb) st[kb][nb] = E::mfma16x16x32(a, qb[nb][k], st[kb][nb]);
       }
     // Mask only a tile that crosses some row's last key (wave-uniform test).
-    if (__any(kt + kPrefillKeys > lim[0] || kt + kPrefillKeys > lim[1])) {
+    if (__any(kt + kPrefillKeys > lm[0] || kt + kPrefillKeys > lm[1])) {
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int key = kt + kb * 16 + 4 * j4 + r;
 #pragma unroll
-          for (int nb = 0; nb < 2; ++nb) st[kb][nb][r] = key < lim[nb] ? st[kb][nb][r] : -INFINITY;
+          for (int nb = 0; nb < 2; ++nb) st[kb][nb][r] = key < lm[nb] ? st[kb][nb][r] : -INFINITY;
         }
     }
     float mx[2];
@@ -271,10 +289,17 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
     // the key and value sources (a page of 256 keys holds four tiles).
     int cached_pg = -1;
     int64_t page_off = 0;  // the cached page's byte offset in either cache
-    auto fill = [&](int kt, uint16_t* stage) {
-      const int last = lk - 1 - kt;
+    // Tile t of the item: context tile t (t < nc), else the row's keys from (t - nc) 64.
+    auto fill = [&](int t, uint16_t* stage) {
+      const bool in_ctx = CTX && t < nc;
+      const int kt = (in_ctx ? t : t - nc) * kPrefillKeys;
+      const int last = (in_ctx ? lc : lk) - 1 - kt;
+      const int64_t kst = in_ctx ? p.cx_st : p.c_st, vst = in_ctx ? p.cv_st : p.v_st;
       int64_t koff, voff;  // wave-uniform byte offsets of key kt of this kv head
-      if (p.paged) {
+      if (in_ctx) {
+        koff = (int64_t)(cbase + kt) * p.cx_st + kvh * p.cx_sh;
+        voff = (int64_t)(cbase + kt) * p.cv_st + kvh * p.cv_sh;
+      } else if (p.paged) {
         const int pg = (int)p.bs.div(kt);
         if (pg != cached_pg) {
           cached_pg = pg;
@@ -287,8 +312,8 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
         koff = (int64_t)(kbase + kt) * p.c_st + kvh * p.c_sh;
         voff = (int64_t)(kbase + kt) * p.v_st + kvh * p.v_sh;
       }
-      const char* kb = p.k_cache + koff;
-      const char* vb = p.v_cache + voff;
+      const char* kb = (in_ctx ? p.ctx_k : p.k_cache) + koff;
+      const char* vb = (in_ctx ? p.ctx_v : p.v_cache) + voff;
 #pragma unroll
       for (int i = 0; i < (NJ + WAVES - 1) / WAVES; ++i) {
         const int j = wave + WAVES * i;
@@ -297,11 +322,11 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
           const char* b;
           if (j < KJ) {
             const int slot = 64 * j + lane, key = slot / KJ;
-            off = (uint32_t)(min(key, last) * (int)p.c_st + min(slot - key * KJ, KCH - 1) * 16);
+            off = (uint32_t)(min(key, last) * (int)kst + min(slot - key * KJ, KCH - 1) * 16);
             b = kb;
           } else {
             const int slot = 64 * (j - KJ) + lane, key = slot / VJ;
-            off = (uint32_t)(min(key, last) * (int)p.v_st + min(slot - key * VJ, VCH - 1) * 16);
+            off = (uint32_t)(min(key, last) * (int)vst + min(slot - key * VJ, VCH - 1) * 16);
             b = vb;
           }
           lds_dma16<false>(b, off, lds_addr(stage + 64 * 8 * j));  // tiles other query tiles read again
@@ -316,21 +341,22 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
 #pragma unroll
       for (int k = 0; k < KS; ++k) asm volatile("" ::"v"(qb[nb][k]));
     int issued = 0;
-    for (; issued < RING - 1 && issued * kPrefillKeys < kmax; ++issued)
-      fill(issued * kPrefillKeys, ring + issued * kStageElems);
-    for (int it = 0, kt = 0; kt < kmax; ++it, kt += kPrefillKeys) {
+    for (; issued < RING - 1 && issued < ntiles; ++issued) fill(issued, ring + issued * kStageElems);
+    for (int it = 0; it < ntiles; ++it) {
       // This wave's loads of tile `it` have landed when only the later tiles' are outstanding; the barrier makes
       // every wave's visible and frees the slot read last iteration.
       const int ahead = issued - it - 1;
       if (ahead == 0) vm_wait_barrier<0>();
       else if (ahead == 1) { if (hi) vm_wait_barrier<CNT_HI>(); else vm_wait_barrier<CNT_LO>(); }
       else { if (hi) vm_wait_barrier<2 * CNT_HI>(); else vm_wait_barrier<2 * CNT_LO>(); }
-      if (issued * kPrefillKeys < kmax) {
-        fill(issued * kPrefillKeys, ring + (issued % RING) * kStageElems);
+      if (issued < ntiles) {
+        fill(issued, ring + (issued % RING) * kStageElems);
         ++issued;
       }
       const uint16_t* ks = ring + (it % RING) * kStageElems;
-      consume(kt, ks, ks + kPrefillKeys * KROW);
+      const bool in_ctx = CTX && it < nc;  // a context tile: every query sees its keys < lc
+      const int lcur[2] = {in_ctx ? lc : lim[0], in_ctx ? lc : lim[1]};
+      consume((in_ctx ? it : it - nc) * kPrefillKeys, lcur, ks, ks + kPrefillKeys * KROW);
     }
   } else {
     uint16_t* ks = reinterpret_cast<uint16_t*>(smem);  // [64 keys][KROW]
@@ -343,7 +369,7 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
       stash(ks, vs, stage);
       __syncthreads();
       if (PREFETCH && kt + kPrefillKeys < kmax) fetch(kt + kPrefillKeys, stage);
-      consume(kt, ks, vs);
+      consume(kt, lim, ks, vs);
     }
   }
 

@@ -312,13 +312,11 @@ __global__ __launch_bounds__(256) void decode_list_kernel(AttnParams p) {
 // plan kernel zeroes), in list order, so the longest still go first. A fixed number of workgroups per CU lets a
 // mixed step's prompt workgroups stay resident beside them. The next ticket is drawn at the start of an item and
 // published at its merge barrier; the merge alternates between two LDS buffers, so one barrier per item suffices.
-// Alone on the GPU the grid holds two workgroups per CU, so their waves may take 256 registers (no spills; 1-2%
-// faster than under the 128 that room for four would leave); BESIDE a mixed step's prompt workgroups, 128.
 // The last workgroup to finish puts the ticket and the exit count back to zero, so the next layer of the step can
 // run on the same plan without a plan launch: every workgroup's ticket draws have returned (their values were
 // read) before it counts itself out, so no draw can follow the reset.
-template <typename T, int D, int GS, bool BESIDE = false>
-__global__ __launch_bounds__(256, BESIDE ? 4 : 2) void decode_persistent_kernel(AttnParams p) {
+template <typename T, int D, int GS>
+__device__ __forceinline__ void decode_persistent(const AttnParams& p) {
   __shared__ __attribute__((aligned(16))) char smem[2][SmemBytes<D, GS>::kDecode];
   __shared__ int s_ticket[2];
   const int ny = p.hkv * p.qgroups;
@@ -340,6 +338,21 @@ __global__ __launch_bounds__(256, BESIDE ? 4 : 2) void decode_persistent_kernel(
     atomicExch(p.ticket, 0);
     atomicExch(p.ticket + 1, 0);
   }
+}
+
+// Alone on the GPU the grid holds two workgroups per CU, so their waves may take 256 registers (no spills; 1-2%
+// faster than under 128).
+template <typename T, int D, int GS>
+__global__ __launch_bounds__(256, 2) void decode_persistent_kernel(AttnParams p) {
+  decode_persistent<T, D, GS>(p);
+}
+
+// Beside a mixed step's prompt workgroups (one per CU, up to 192 registers per wave) two decode workgroups share
+// each SIMD's 512 registers per lane: at most 160 per wave. (The 128 that four workgroups per CU would leave spill
+// the D = 128 item.)
+template <typename T, int D, int GS>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_num_vgpr(160))) void decode_beside_kernel(AttnParams p) {
+  decode_persistent<T, D, GS>(p);
 }
 
 // RING > 0: pages are a multiple of 64 tokens, so prompt tiles stream through an LDS ring of RING stages.
@@ -634,10 +647,14 @@ static int resident_per_cu() {
 template <typename T, int D, int GS, bool BESIDE = false>
 static void launch_decode(const AttnParams& p, const Shape& s, int per_cu, hipStream_t stream) {
   const int items = s.max_decode_items * p.hkv * p.qgroups;  // a bound: the plan lists no more
-  const int grid =
-      per_cu > 0 ? std::min(per_cu, resident_per_cu<decode_persistent_kernel<T, D, GS, BESIDE>>()) * device_cus() : 0;
+  const int resident = BESIDE ? resident_per_cu<decode_beside_kernel<T, D, GS>>()
+                              : resident_per_cu<decode_persistent_kernel<T, D, GS>>();
+  const int grid = per_cu > 0 ? std::min(per_cu, resident) * device_cus() : 0;
   if (grid > 0 && items >= 8 * grid) {
-    hipLaunchKernelGGL((decode_persistent_kernel<T, D, GS, BESIDE>), dim3(grid), dim3(256), 0, stream, p);
+    if (BESIDE)
+      hipLaunchKernelGGL((decode_beside_kernel<T, D, GS>), dim3(grid), dim3(256), 0, stream, p);
+    else
+      hipLaunchKernelGGL((decode_persistent_kernel<T, D, GS>), dim3(grid), dim3(256), 0, stream, p);
   } else {
     hipLaunchKernelGGL((decode_list_kernel<T, D, GS>), dim3(items), dim3(256), 0, stream, p);
   }

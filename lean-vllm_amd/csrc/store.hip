@@ -8,6 +8,18 @@
 
 namespace lv {
 
+// An empty use of x in registers: whatever computes x must have happened here.
+template <typename X>
+__device__ __forceinline__ void keep_live(const X& x) {
+  if constexpr (sizeof(X) == 16) {
+    asm volatile("" ::"v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]));
+  } else if constexpr (sizeof(X) == 8) {
+    asm volatile("" ::"v"(x[0]), "v"(x[1]));
+  } else {
+    asm volatile("" ::"v"((uint32_t)x));
+  }
+}
+
 template <int VEC>
 struct Piece;
 template <> struct Piece<16> { typedef u32x4 type; };
@@ -16,8 +28,10 @@ template <> struct Piece<4> { typedef uint32_t type; };
 template <> struct Piece<2> { typedef uint16_t type; };
 template <> struct Piece<1> { typedef uint8_t type; };
 
-// kStoreTokens tokens per workgroup: their slots, then every piece of theirs that a thread copies, are loaded
-// before the first is used, so a workgroup waits for two round trips to memory, not two per token.
+// kStoreTokens tokens per workgroup; each thread copies one piece of their key or value rows (blockIdx.y picks
+// the thread's share of the pieces when a row pair has more than 256). The source rows do not depend on the slots,
+// so every load -- the pieces, and each wave's four slots, one per lane -- is issued before the first wait: one
+// round trip to memory before the stores, not two.
 constexpr int kStoreTokens = 4;
 template <int VEC>
 __global__ __launch_bounds__(256) void store_kv_kernel(const char* __restrict__ key, const char* __restrict__ value,
@@ -28,34 +42,47 @@ __global__ __launch_bounds__(256) void store_kv_kernel(const char* __restrict__ 
                                                        int32_t tokens) {
   typedef typename Piece<VEC>::type P;
   const int t0 = blockIdx.x * kStoreTokens;
-  int64_t base[kStoreTokens];  // cache byte offset of each token's (block, offset)
-  bool keep[kStoreTokens];     // slot -1, or past the last token: nothing stored
+  const int n = min(kStoreTokens, tokens - t0);  // tokens of this workgroup
+  // Every thread runs to the end, so lanes 0-3 of each wave load the slots; threads past the row pair copy piece 0
+  // without storing it.
+  const bool active = blockIdx.y * blockDim.x + threadIdx.x < 2 * pieces_per_row;
+  const int i = active ? blockIdx.y * blockDim.x + threadIdx.x : 0;
+  // Pieces [0, pieces_per_row) are the key row, the rest the value row.
+  const bool is_v = i >= pieces_per_row;
+  const int j = is_v ? i - pieces_per_row : i;
+  const int head = j / pieces_per_head;
+  const int within = j - head * pieces_per_head;
+  const int64_t dst = head * sh + (int64_t)within * VEC;
+  const int64_t row = is_v ? value_row : key_row;
+  const char* src = (is_v ? value : key) + (int64_t)j * VEC + (int64_t)t0 * row;
+  char* cache = is_v ? v_cache : k_cache;
+  // No branch between the loads: a last workgroup's missing tokens read its first token again (slot -1 below).
+  P piece[kStoreTokens];
+#pragma unroll
+  for (int k = 0; k < kStoreTokens; ++k) piece[k] = *reinterpret_cast<const P*>(src + (k < n ? k : 0) * row);
+  const int lane = threadIdx.x & 63;
+  const int mine = slots[t0 + (lane % kStoreTokens < n ? lane % kStoreTokens : 0)];  // lane k: token k's slot
+  // The pieces are needed here, before the branches on the slots: the compiler would otherwise sink a piece's load
+  // into its store's branch, after the wait for the slots.
+#pragma unroll
+  for (int k = 0; k < kStoreTokens; ++k) keep_live(piece[k]);
+  // Every slot is read out before the first store: a wait for the slot load after a store would wait for the
+  // store too (stores count in the same counter).
+  int slot[kStoreTokens];
 #pragma unroll
   for (int k = 0; k < kStoreTokens; ++k) {
-    const int slot = t0 + k < tokens ? slots[t0 + k] : -1;
-    keep[k] = slot >= 0;
-    base[k] = keep[k] ? (int64_t)(slot / block_size) * sb + (int64_t)(slot % block_size) * st : 0;
+    slot[k] = k < n ? __builtin_amdgcn_readlane(mine, k) : -1;  // tokens past the last: nothing stored
+    asm volatile("" ::"s"(slot[k]));
   }
-  // Pieces [0, pieces_per_row) are the key row, the rest the value row.
-  for (int i = threadIdx.x; i < 2 * pieces_per_row; i += blockDim.x) {
-    const bool is_v = i >= pieces_per_row;
-    const int j = is_v ? i - pieces_per_row : i;
-    const int head = j / pieces_per_head;
-    const int within = j - head * pieces_per_head;
-    const int64_t dst = head * sh + (int64_t)within * VEC;
-    const char* src = (is_v ? value : key) + (int64_t)j * VEC;
-    const int64_t row = is_v ? value_row : key_row;
-    char* cache = is_v ? v_cache : k_cache;
-    P piece[kStoreTokens];
 #pragma unroll
-    for (int k = 0; k < kStoreTokens; ++k)
-      if (keep[k]) piece[k] = *reinterpret_cast<const P*>(src + (int64_t)(t0 + k) * row);
-#pragma unroll
-    for (int k = 0; k < kStoreTokens; ++k)
-      if (keep[k]) *reinterpret_cast<P*>(cache + base[k] + dst) = piece[k];
-  }
+  for (int k = 0; k < kStoreTokens; ++k)
+    if (active && slot[k] >= 0)  // slot -1: nothing stored
+      *reinterpret_cast<P*>(cache + (int64_t)(slot[k] / block_size) * sb + (int64_t)(slot[k] % block_size) * st +
+                            dst) = piece[k];
 }
 
+// One latent per workgroup; each thread copies one piece (blockIdx.y picks the thread's share of the pieces when a
+// latent has more than 128). The piece and the slot are loaded together, as vector loads, before the first wait.
 template <int VEC>
 __global__ __launch_bounds__(128) void store_latent_kernel(const char* __restrict__ latent, int64_t latent_row,
                                                            int32_t pieces, int64_t cache_row,
@@ -63,12 +90,15 @@ __global__ __launch_bounds__(128) void store_latent_kernel(const char* __restric
                                                            const int32_t* __restrict__ slots) {
   typedef typename Piece<VEC>::type P;
   const int t = blockIdx.x;
-  const int slot = slots[t];
+  const int i = blockIdx.y * blockDim.x + threadIdx.x;
+  if (i >= pieces) return;
+  const P piece = *reinterpret_cast<const P*>(latent + (int64_t)t * latent_row + (int64_t)i * VEC);
+  int zero;  // 0, in a vector register: the slot load is then a vector load, counted in order with the piece load
+  asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+  const int slot = __builtin_amdgcn_readfirstlane(slots[t + zero]);
+  keep_live(piece);
   if (slot < 0) return;
-  const char* src = latent + (int64_t)t * latent_row;
-  char* dst = cache + (int64_t)slot * cache_row;
-  for (int i = threadIdx.x; i < pieces; i += blockDim.x)
-    *reinterpret_cast<P*>(dst + (int64_t)i * VEC) = *reinterpret_cast<const P*>(src + (int64_t)i * VEC);
+  *reinterpret_cast<P*>(cache + (int64_t)slot * cache_row + (int64_t)i * VEC) = piece;
 }
 
 // Widest piece (16, 8, 4, 2 or 1 bytes) that divides every byte offset and pointer involved.
@@ -107,9 +137,11 @@ extern "C" int lv_store_kvcache(const void* key, const void* value, int64_t key_
   const int32_t pph = (int32_t)(head_bytes / vec);
   const int32_t ppr = (int32_t)(row_bytes / vec);
   const int threads = ppr * 2 >= 256 ? 256 : ((ppr * 2 + 63) / 64) * 64;
+  const int shares = (ppr * 2 + threads - 1) / threads;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
 #define LV_STORE_LAUNCH(V)                                                                                     \
-  hipLaunchKernelGGL(store_kv_kernel<V>, dim3((num_tokens + kStoreTokens - 1) / kStoreTokens), dim3(threads), 0, \
+  hipLaunchKernelGGL(store_kv_kernel<V>, dim3((num_tokens + kStoreTokens - 1) / kStoreTokens, shares),       \
+                     dim3(threads), 0,                                                                         \
                      s, (const char*)key, (const char*)value, key_stride_t * eb, value_stride_t * eb, pph, ppr,  \
                      (char*)k_cache, (char*)v_cache, cache_stride_block * eb, cache_stride_token * eb,           \
                      cache_stride_head * eb, block_size, slot_mapping, num_tokens)
@@ -138,7 +170,8 @@ extern "C" int lv_store_latents(const void* latent, int64_t latent_stride_t, int
   const int32_t pieces = (int32_t)(row / vec);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
 #define LV_LATENT_LAUNCH(V)                                                                                    \
-  hipLaunchKernelGGL(store_latent_kernel<V>, dim3(num_tokens), dim3(128), 0, s, (const char*)latent,           \
+  hipLaunchKernelGGL(store_latent_kernel<V>, dim3(num_tokens, (pieces + 127) / 128), dim3(128), 0, s,          \
+                     (const char*)latent,                                                                      \
                      latent_stride_t * eb, pieces, row, (char*)cache, slot_mapping)
   switch (vec) {
     case 16: LV_LATENT_LAUNCH(16); break;

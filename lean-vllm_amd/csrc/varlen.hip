@@ -30,8 +30,10 @@ constexpr int kXcds = 8;  // workgroups are dealt round-robin over the XCDs by t
 // walks all its keys: an XCD's items go out group by group, so a group's tiles run together and read each key tile
 // once from memory (query tiles outermost cost 1.5x the time on DeepSeek-V2-Lite's prefix chunks). Causal, query
 // tile t walks t + 1 tiles' worth of keys: the items go out by descending query tile, then group, so the long ones
-// start first and the short ones fill the tail (0.67x the time of group order on its 1536-token chunks).
-template <typename T, int DQK, int DV>
+// start first and the short ones fill the tail (0.67x the time of group order on its 1536-token chunks). With
+// context keys (CTX) every query tile walks the whole context first: items go out group by group, as unmasked ones,
+// the longest query tile of each group first.
+template <typename T, int DQK, int DV, bool CTX>
 __global__ __launch_bounds__((64 * VarlenCfg<DQK, DV>::kWaves), (VarlenCfg<DQK, DV>::kPerCu)) void varlen_kernel(
     AttnParams p, int32_t qtiles) {
   using Cfg = VarlenCfg<DQK, DV>;
@@ -41,10 +43,10 @@ __global__ __launch_bounds__((64 * VarlenCfg<DQK, DV>::kWaves), (VarlenCfg<DQK, 
   const int g0 = x * (groups / kXcds) + min(x, groups % kXcds);   // this XCD's first group
   const int ng = groups / kXcds + (x < groups % kXcds ? 1 : 0);    // and its number of groups
   if (k >= ng * qtiles) return;  // the grid is rounded up to whole XCD rounds
-  const int qt = p.causal ? qtiles - 1 - k / ng : k % qtiles;
-  const int g = g0 + (p.causal ? k % ng : k / qtiles);
+  const int qt = CTX ? qtiles - 1 - k % qtiles : p.causal ? qtiles - 1 - k / ng : k % qtiles;
+  const int g = g0 + (CTX || !p.causal ? k / qtiles : k % ng);
   const int kvh = g / p.rows, row = g - kvh * p.rows;
-  prefill_item<T, DQK, DV, true, false, Cfg::kRing, Cfg::kWaves>(p, row, qt, kvh, smem);
+  prefill_item<T, DQK, DV, true, false, Cfg::kRing, Cfg::kWaves, CTX>(p, row, qt, kvh, smem);
 }
 
 // Query tiles per row of at most max_seqlen_q queries, for a (q.k, v) width pair; 0 for unsupported widths.
@@ -64,8 +66,11 @@ static void launch_one(const AttnParams& p, int qtiles, hipStream_t st) {
   // Each XCD gets a whole number of (kv head, row) groups: ceil(groups / 8) groups' items per XCD.
   const int64_t groups = (int64_t)p.rows * p.hkv;
   const int64_t per_xcd = (groups + kXcds - 1) / kXcds * qtiles;
-  hipLaunchKernelGGL((varlen_kernel<T, DQK, DV>), dim3(per_xcd * kXcds), dim3(64 * VarlenCfg<DQK, DV>::kWaves), 0, st,
-                     p, qtiles);
+  const dim3 grid(per_xcd * kXcds), block(64 * VarlenCfg<DQK, DV>::kWaves);
+  if (p.cu_ctx)
+    hipLaunchKernelGGL((varlen_kernel<T, DQK, DV, true>), grid, block, 0, st, p, qtiles);
+  else
+    hipLaunchKernelGGL((varlen_kernel<T, DQK, DV, false>), grid, block, 0, st, p, qtiles);
 }
 
 template <typename T>
@@ -91,13 +96,15 @@ static int launch_varlen(const AttnParams& p, int dqk, int dv, int qtiles, hipSt
 
 using namespace lv;
 
-extern "C" int lv_varlen_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k,
-                                   int64_t k_stride_t, int64_t k_stride_h, const void* v, int64_t v_stride_t,
-                                   int64_t v_stride_h, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
-                                   int32_t num_rows, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim_qk,
-                                   int32_t head_dim_v, float scale, int32_t causal, int32_t max_seqlen_q, void* out,
-                                   int64_t out_stride_t, int64_t out_stride_h, float* lse, int64_t lse_stride_t,
-                                   int64_t lse_stride_h, int32_t dtype, void* stream) {
+// Both entry points: without context keys (ctx_k null) or with them.
+static int varlen_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k, int64_t k_stride_t,
+                            int64_t k_stride_h, const void* v, int64_t v_stride_t, int64_t v_stride_h,
+                            const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, const void* ctx_k,
+                            int64_t ctx_k_stride_t, int64_t ctx_k_stride_h, const void* ctx_v, int64_t ctx_v_stride_t,
+                            int64_t ctx_v_stride_h, const int32_t* cu_seqlens_ctx, int32_t num_rows, int32_t num_heads,
+                            int32_t num_kv_heads, int32_t head_dim_qk, int32_t head_dim_v, float scale, int32_t causal,
+                            int32_t max_seqlen_q, void* out, int64_t out_stride_t, int64_t out_stride_h, float* lse,
+                            int64_t lse_stride_t, int64_t lse_stride_h, int32_t dtype, void* stream) {
   LV_REQUIRE(dtype == LV_DTYPE_BF16 || dtype == LV_DTYPE_F16, "varlen_attention: dtype %d is not bf16 or fp16",
              dtype);
   LV_REQUIRE(num_rows >= 0 && max_seqlen_q >= 0, "varlen_attention: negative row count or max_seqlen_q");
@@ -113,6 +120,13 @@ extern "C" int lv_varlen_attention(const void* q, int64_t q_stride_t, int64_t q_
                  (v_stride_t * 2) % 16 == 0 && (v_stride_h * 2) % 16 == 0 && (out_stride_t * 2) % 8 == 0 &&
                  (out_stride_h * 2) % 8 == 0,
              "varlen_attention: tensors and their strides must be 16-byte aligned");
+  if (cu_seqlens_ctx) {
+    LV_REQUIRE(ctx_k && ctx_v, "varlen_context_attention: null context key or value pointer");
+    LV_REQUIRE(aligned(ctx_k, 16) && aligned(ctx_v, 16) && (ctx_k_stride_t * 2) % 16 == 0 &&
+                   (ctx_k_stride_h * 2) % 16 == 0 && (ctx_v_stride_t * 2) % 16 == 0 &&
+                   (ctx_v_stride_h * 2) % 16 == 0,
+               "varlen_context_attention: context keys, values and their strides must be 16-byte aligned");
+  }
   AttnParams p{};
   p.q = (const char*)q;
   p.q_st = q_stride_t * 2;
@@ -140,6 +154,15 @@ extern "C" int lv_varlen_attention(const void* q, int64_t q_stride_t, int64_t q_
   p.lse = lse;
   p.lse_st = lse_stride_t;
   p.lse_sh = lse_stride_h;
+  if (cu_seqlens_ctx) {
+    p.ctx_k = (const char*)ctx_k;
+    p.ctx_v = (const char*)ctx_v;
+    p.cx_st = ctx_k_stride_t * 2;
+    p.cx_sh = ctx_k_stride_h * 2;
+    p.cv_st = ctx_v_stride_t * 2;
+    p.cv_sh = ctx_v_stride_h * 2;
+    p.cu_ctx = cu_seqlens_ctx;
+  }
   const int64_t qtiles = varlen_qtiles(head_dim_qk, head_dim_v, p.group, max_seqlen_q);
   LV_REQUIRE(qtiles > 0, "varlen_attention: head dims (q.k %d, v %d) are not (64, 64), (128, 128), (192, 128) or "
              "(192, 192)", head_dim_qk, head_dim_v);
@@ -148,4 +171,32 @@ extern "C" int lv_varlen_attention(const void* q, int64_t q_stride_t, int64_t q_
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   return dtype == LV_DTYPE_BF16 ? launch_varlen<BF16>(p, head_dim_qk, head_dim_v, (int)qtiles, st)
                                 : launch_varlen<F16>(p, head_dim_qk, head_dim_v, (int)qtiles, st);
+}
+
+extern "C" int lv_varlen_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k,
+                                   int64_t k_stride_t, int64_t k_stride_h, const void* v, int64_t v_stride_t,
+                                   int64_t v_stride_h, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                   int32_t num_rows, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim_qk,
+                                   int32_t head_dim_v, float scale, int32_t causal, int32_t max_seqlen_q, void* out,
+                                   int64_t out_stride_t, int64_t out_stride_h, float* lse, int64_t lse_stride_t,
+                                   int64_t lse_stride_h, int32_t dtype, void* stream) {
+  return varlen_attention(q, q_stride_t, q_stride_h, k, k_stride_t, k_stride_h, v, v_stride_t, v_stride_h,
+                          cu_seqlens_q, cu_seqlens_k, nullptr, 0, 0, nullptr, 0, 0, nullptr, num_rows, num_heads,
+                          num_kv_heads, head_dim_qk, head_dim_v, scale, causal, max_seqlen_q, out, out_stride_t,
+                          out_stride_h, lse, lse_stride_t, lse_stride_h, dtype, stream);
+}
+
+extern "C" int lv_varlen_context_attention(
+    const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k, int64_t k_stride_t, int64_t k_stride_h,
+    const void* v, int64_t v_stride_t, int64_t v_stride_h, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+    const void* ctx_k, int64_t ctx_k_stride_t, int64_t ctx_k_stride_h, const void* ctx_v, int64_t ctx_v_stride_t,
+    int64_t ctx_v_stride_h, const int32_t* cu_seqlens_ctx, int32_t num_rows, int32_t num_heads, int32_t num_kv_heads,
+    int32_t head_dim_qk, int32_t head_dim_v, float scale, int32_t max_seqlen_q, void* out, int64_t out_stride_t,
+    int64_t out_stride_h, float* lse, int64_t lse_stride_t, int64_t lse_stride_h, int32_t dtype, void* stream) {
+  LV_REQUIRE(cu_seqlens_ctx, "varlen_context_attention: cu_seqlens_ctx is null");
+  return varlen_attention(q, q_stride_t, q_stride_h, k, k_stride_t, k_stride_h, v, v_stride_t, v_stride_h,
+                          cu_seqlens_q, cu_seqlens_k, ctx_k, ctx_k_stride_t, ctx_k_stride_h, ctx_v, ctx_v_stride_t,
+                          ctx_v_stride_h, cu_seqlens_ctx, num_rows, num_heads, num_kv_heads, head_dim_qk, head_dim_v,
+                          scale, 1, max_seqlen_q, out, out_stride_t, out_stride_h, lse, lse_stride_t, lse_stride_h,
+                          dtype, stream);
 }

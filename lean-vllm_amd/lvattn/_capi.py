@@ -41,6 +41,10 @@ _PROTOTYPES = {
     "lv_varlen_attention": (ctypes.c_int, [_P, c_int64, c_int64, _P, c_int64, c_int64, _P, c_int64, c_int64, _P, _P,
                                            c_int32, c_int32, c_int32, c_int32, c_int32, c_float, c_int32, c_int32,
                                            _P, c_int64, c_int64, _P, c_int64, c_int64, c_int32, _P]),
+    "lv_varlen_context_attention": (ctypes.c_int, [_P, c_int64, c_int64, _P, c_int64, c_int64, _P, c_int64, c_int64,
+                                                   _P, _P, _P, c_int64, c_int64, _P, c_int64, c_int64, _P, c_int32,
+                                                   c_int32, c_int32, c_int32, c_int32, c_float, c_int32, _P, c_int64,
+                                                   c_int64, _P, c_int64, c_int64, c_int32, _P]),
     "lv_mla_decode_workspace_bytes": (c_size_t, [c_int32, c_int32, c_int32, c_int32]),
     "lv_mla_decode": (ctypes.c_int, [_P, c_int64, c_int64, _P, c_int64, c_int64, c_int32, _P, c_int64, _P, c_int32,
                                      c_int32, c_int32, c_int32, c_int32, c_float, c_int32, _P, c_int64, c_int64,

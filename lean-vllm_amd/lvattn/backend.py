@@ -335,3 +335,32 @@ class MI355XAttention(AttentionBackend):
         every query row for merging (``abstract.py:187-204``); -inf for a row with no keys. ``host_cu_seqlens``
         is not needed: the grid is sized from ``max_seqlen_q``."""
         return self._varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, causal=causal, want_lse=True)
+
+    def prefill_with_context(self, q, k, v, k_ctx, v_ctx, cu_seqlens_q, cu_seqlens_ctx, max_seqlen_q, out=None,
+                             want_lse=False):
+        """MLA prefill over cached context in one call: each row's new queries attend all of the row's context
+        keys ``k_ctx``/``v_ctx`` (rows by ``cu_seqlens_ctx``) and, causally, its new keys ``k``/``v`` (rows by
+        ``cu_seqlens_q``), as one softmax. The same result as ``MLAAttention._prefill``'s causal
+        ``varlen_with_lse``, unmasked ``varlen_with_lse`` over the context and ``merge_attention_``
+        (``lean_vllm/layers/attention.py:280-316``), without their partial outputs. Returns ``out`` (and the
+        natural log-sum-exp ``[T, H]`` with ``want_lse``)."""
+        assert q.dtype in _capi.DTYPES and k.dtype == q.dtype == v.dtype == k_ctx.dtype == v_ctx.dtype
+        for t in (q, k, v, k_ctx, v_ctx):
+            assert t.stride(-1) == 1
+        tokens, heads, dqk = q.shape
+        dv = v.size(-1)
+        assert k.size(0) == tokens and k_ctx.size(1) == k.size(1) and v_ctx.size(-1) == dv
+        cu_q = cu_seqlens_q if cu_seqlens_q.dtype == torch.int32 else cu_seqlens_q.to(torch.int32)
+        cu_c = cu_seqlens_ctx if cu_seqlens_ctx.dtype == torch.int32 else cu_seqlens_ctx.to(torch.int32)
+        assert cu_c.numel() == cu_q.numel()
+        if out is None:
+            out = torch.empty(tokens, heads, dv, dtype=q.dtype, device=q.device)
+        assert out.shape == (tokens, heads, dv) and out.stride(-1) == 1 and out.dtype == q.dtype
+        lse = torch.empty(tokens, heads, dtype=torch.float32, device=q.device) if want_lse else None
+        _capi.call("lv_varlen_context_attention", q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0),
+                   k.stride(1), v.data_ptr(), v.stride(0), v.stride(1), cu_q.data_ptr(), cu_q.data_ptr(),
+                   k_ctx.data_ptr(), k_ctx.stride(0), k_ctx.stride(1), v_ctx.data_ptr(), v_ctx.stride(0),
+                   v_ctx.stride(1), cu_c.data_ptr(), cu_q.numel() - 1, heads, k.size(1), dqk, dv, float(self.scale),
+                   int(max_seqlen_q), out.data_ptr(), out.stride(0), out.stride(1), _capi.ptr(lse),
+                   heads if want_lse else 0, 1 if want_lse else 0, _capi.DTYPES[q.dtype], _capi.stream_of(q.device))
+        return (out, lse) if want_lse else out

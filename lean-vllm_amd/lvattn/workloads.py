@@ -21,11 +21,14 @@ device. Key lengths include the token(s) stored this step (``context_lens = num_
   names no page size, ``:85-89``), over pools of the same bytes (192,000 and 136,000 pages).
 - ``deepseek_v2_lite_mla_prefill``: the same layer's prompt chunks as ``MLAAttention._prefill`` runs them
   (``lean_vllm/layers/attention.py:265-317``) on expanded heads (q.k 192, values 128): 4 chunks of 1536 new tokens
-  on a cached prefix U[0, 6144]; the new tokens attend each other causally, the prefix unmasked, merged by lse.
+  on a cached prefix U[0, 6144]; the new tokens attend the prefix unmasked and each other causally, in one
+  ``prefill_with_context`` call. ``deepseek_v2_lite_mla_prefill_two_pass`` is the same step as the reference layer's
+  calls: causal ``varlen_with_lse`` over the new tokens, unmasked over the prefix, merged by lse.
 """
 
 from __future__ import annotations
 
+import dataclasses
 import math
 from dataclasses import dataclass, field
 
@@ -50,6 +53,7 @@ class Workload:
     v_dim: int = 0  # MLA: value width (leading entries of a latent)
     expanded: tuple = (0, 0)  # MLA prefill: (q.k width, value width) of the expanded heads
     num_layers: int = 1  # attention layers of the model the step belongs to (each attends the same step)
+    two_pass: bool = False  # MLA prefill: the reference layer's calls (two varlen passes and a merge), not one call
     notes: dict = field(default_factory=dict)
 
     @property
@@ -170,6 +174,8 @@ WORKLOADS = {
     "qwen3_8b_long": qwen3_8b_long,
     "deepseek_v2_lite_mla": deepseek_v2_lite_mla,
     "deepseek_v2_lite_mla_prefill": deepseek_v2_lite_mla_prefill,
+    "deepseek_v2_lite_mla_prefill_two_pass": lambda seed=0: dataclasses.replace(
+        deepseek_v2_lite_mla_prefill(seed), name="deepseek_v2_lite_mla_prefill_two_pass", two_pass=True),
     "qwen3_8b_decode_bs16": lambda seed=0: qwen3_8b_decode(seed, block_size=16),
     "deepseek_v2_lite_mla_bs16": lambda seed=0: deepseek_v2_lite_mla(seed, block_size=16),
 }

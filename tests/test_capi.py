@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
     lib = _capi.load()
     missing = [n for n in declared() if not hasattr(lib, n)]
     assert not missing, f"declared in lvattn.h but not exported: {missing}"
-    assert lib.lv_abi_version() == 7
+    assert lib.lv_abi_version() == 8
     assert all(n in _capi._PROTOTYPES for n in declared()), "every declared function has a ctypes prototype"
 
 
@@ -47,6 +47,12 @@ def test_bad_arguments_raise_with_the_library_message():
     with pytest.raises(_capi.LvError, match="unknown schedule 5"):
         _capi.call("lv_paged_attention", 1, 0, 0, 1, 1, 0, 0, 0, 16, 1, 0, None, 1, None, 1, 1, 8, 2, 64, 1.0, 1, 16,
                    1, 0, 0, None, 0, 5, 0, 0, 0, None)
+    with pytest.raises(_capi.LvError, match="cu_seqlens_ctx is null"):
+        _capi.call("lv_varlen_context_attention", 1, 0, 0, 1, 0, 0, 1, 0, 0, 1, 1, 1, 0, 0, 1, 0, 0, None, 1, 16, 16,
+                   192, 128, 1.0, 16, 1, 0, 0, None, 0, 0, 0, None)
+    with pytest.raises(_capi.LvError, match="context keys, values and their strides must be 16-byte aligned"):
+        _capi.call("lv_varlen_context_attention", 16, 0, 0, 16, 0, 0, 16, 0, 0, 16, 16, 17, 0, 0, 16, 0, 0, 16, 1, 16,
+                   16, 192, 128, 1.0, 16, 16, 0, 0, None, 0, 0, 0, None)
     with pytest.raises(_capi.LvError, match="negative prompt_workgroups"):
         _capi.call("lv_paged_attention", 1, 0, 0, 1, 1, 0, 0, 0, 16, 1, 0, None, 1, None, 1, 1, 8, 2, 64, 1.0, 1, 16,
                    1, 0, 0, None, 0, 2, -1, 0, 0, None)

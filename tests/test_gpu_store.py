@@ -36,6 +36,44 @@ def test_store_matches_the_oracle_bit_for_bit(cuda, dtype, layout):
     assert torch.equal(dk.cpu(), want_k) and torch.equal(dv.cpu(), want_v)
 
 
+@pytest.mark.parametrize("heads,dim,dtype", [(1, 2, torch.float16), (1, 4, torch.float16), (3, 64, torch.bfloat16),
+                                             (16, 128, torch.bfloat16), (5, 24, torch.float32)])
+@pytest.mark.parametrize("tokens", [1, 2, 3, 5, 7, 41])
+def test_store_row_widths_and_token_tails(cuda, heads, dim, dtype, tokens):
+    """Rows of one or two pieces (fewer copying threads than a workgroup's four tokens), rows spread over two thread
+    shares (16 x 128 bf16 = 4 KB per token), and token counts that leave a last workgroup short: bit-exact."""
+    bs, blocks = 16, 4
+    gen = torch.Generator().manual_seed(tokens * 100 + dim)
+    key = (torch.randn(tokens, heads, dim, generator=gen) * 3).to(dtype)
+    value = (torch.randn(tokens, heads, dim, generator=gen) * 3).to(dtype)
+    slots = torch.randperm(blocks * bs, generator=gen)[:tokens].to(torch.int32)
+    if tokens > 2:
+        slots[tokens // 2] = -1
+    kc = torch.full((blocks, bs, heads, dim), 7.0, dtype=dtype)
+    vc = torch.full((blocks, bs, heads, dim), -7.0, dtype=dtype)
+    want_k, want_v = kc.clone(), vc.clone()
+    S.store_kvcache(key, value, want_k, want_v, slots)
+    dk, dv = kc.to(cuda), vc.to(cuda)
+    MI355XAttention(heads, dim, 1.0, heads).store_kvcache(key.to(cuda), value.to(cuda), dk, dv, slots.to(cuda))
+    torch.cuda.synchronize()
+    assert torch.equal(dk.cpu(), want_k) and torch.equal(dv.cpu(), want_v)
+
+
+@pytest.mark.parametrize("dim,dtype", [(576, torch.bfloat16), (4, torch.float16), (1152, torch.bfloat16)])
+def test_store_latent_widths(cuda, dim, dtype):
+    """Latents of 576 (one thread share), 4 (one piece) and 1152 elements (two shares of 128 threads)."""
+    gen = torch.Generator().manual_seed(dim)
+    latent = torch.randn(9, dim, generator=gen).to(dtype)
+    slots = torch.tensor([5, -1, 0, 63, 17, -1, 40, 2, 33], dtype=torch.int32)
+    cache = torch.full((2, 32, dim), 7.0, dtype=dtype)
+    want = cache.clone()
+    S.store_latents(latent, want, slots.tolist())
+    got = cache.to(cuda)
+    MI355XAttention(16, 128, 1.0, 16).store_latents(latent.to(cuda), got, slots.to(cuda))
+    torch.cuda.synchronize()
+    assert torch.equal(got.cpu(), want)
+
+
 def test_store_latents_skips_negative_slots(cuda):
     """tests/test_attention_backends.py:439-455."""
     b = MI355XAttention(16, 128, 1.0, 16)

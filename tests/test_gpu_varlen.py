@@ -170,11 +170,13 @@ def test_merge_matches_the_oracle(cuda, dtype, into, dim):
         assert torch.equal(o_a, before)
 
 
-def test_full_size_mla_prefill_step(cuda):
+@pytest.mark.parametrize("path", ["two_pass_and_merge", "one_call"])
+def test_full_size_mla_prefill_step(cuda, path):
     """The measured DeepSeek-V2-Lite prefill step at full size (4 chunks of 1536 new tokens on prefixes up to 6144,
-    192-wide q.k and 128-wide values): causal attention over each chunk, unmasked attention over its prefix, and
-    the LSE merge, as the bench runs them. Every 64th query of every chunk and its last query are checked against
-    the fp32 oracle over the prefix keys followed by the chunk's keys up to the query."""
+    192-wide q.k and 128-wide values), either as the reference's layer runs it (causal attention over each chunk,
+    unmasked attention over its prefix, the LSE merge) or in one ``prefill_with_context`` call, as the bench runs
+    it. Every 64th query of every chunk and its last query are checked against the fp32 oracle over the prefix keys
+    followed by the chunk's keys up to the query."""
     import numpy as np
 
     from lvattn import workloads as W
@@ -187,10 +189,13 @@ def test_full_size_mla_prefill_step(cuda):
     cu_q = torch.tensor(cu_q_host, dtype=torch.int32, device=cuda)
     cu_c = torch.tensor(cu_c_host, dtype=torch.int32, device=cuda)
     max_q, max_c = max(wl.num_new), max(max(wl.num_cached), 1)
-    o, lse = b.varlen_with_lse(ex["q"], ex["k"], ex["v"], cu_q, cu_q, max_q, max_q, True)
-    co, clse = b.varlen_with_lse(ex["q"], ex["k_ctx"], ex["v_ctx"], cu_q, cu_c, max_q, max_c, False)
-    out = torch.empty_like(o)
-    merge_attention_(co, clse, o, lse, out)
+    if path == "one_call":
+        out = b.prefill_with_context(ex["q"], ex["k"], ex["v"], ex["k_ctx"], ex["v_ctx"], cu_q, cu_c, max_q)
+    else:
+        o, lse = b.varlen_with_lse(ex["q"], ex["k"], ex["v"], cu_q, cu_q, max_q, max_q, True)
+        co, clse = b.varlen_with_lse(ex["q"], ex["k_ctx"], ex["v_ctx"], cu_q, cu_c, max_q, max_c, False)
+        out = torch.empty_like(o)
+        merge_attention_(co, clse, o, lse, out)
     torch.cuda.synchronize()
     assert torch.isfinite(out).all()
     for r in range(len(wl.num_new)):
@@ -204,3 +209,62 @@ def test_full_size_mla_prefill_step(cuda):
             want = A.dense_attention(ex["q"][t:t + 1].cpu().float(), k, v, wl.scale, causal=False)
             torch.testing.assert_close(out[t:t + 1].float().cpu(), want, **TOL[torch.bfloat16],
                                        msg=lambda m: f"chunk {r} query {j}: {m}")
+
+
+CTX_CASES = [(torch.bfloat16, 16, 16, 192, 128), (torch.bfloat16, 8, 2, 128, 128), (torch.float16, 8, 2, 64, 64),
+             (torch.bfloat16, 4, 4, 192, 192)]
+
+
+@pytest.mark.parametrize("dtype, heads, kv_heads, qk, vd", CTX_CASES, ids=["mla-192-128", "gqa-128", "fp16-64",
+                                                                            "192-192"])
+def test_prefill_with_context(cuda, dtype, heads, kv_heads, qk, vd):
+    """One call over context keys then causal new keys equals the dense oracle over each row's [context; new] keys
+    with the causal mask aligned to the end: rows with no context, with context a multiple of the 64-key tile and
+    not, with one query, and with more queries than one item holds; lse included. The two-pass path (causal and
+    unmasked varlen_with_lse, then the merge) agrees within the same tolerance."""
+    gen = torch.Generator().manual_seed(5)
+    lens_q = [5, 1, 12, 300, 70, 64]
+    lens_c = [0, 7, 64, 333, 1, 128]
+    q = rnd(sum(lens_q), heads, qk, gen=gen, dtype=dtype, device=cuda)
+    k = rnd(sum(lens_q), kv_heads, qk, gen=gen, dtype=dtype, device=cuda)
+    v = rnd(sum(lens_q), kv_heads, vd, gen=gen, dtype=dtype, device=cuda)
+    kc = rnd(sum(lens_c), kv_heads, qk, gen=gen, dtype=dtype, device=cuda)
+    vc = rnd(sum(lens_c), kv_heads, vd, gen=gen, dtype=dtype, device=cuda)
+    cu_q, cu_c = cumulative(lens_q, cuda), cumulative(lens_c, cuda)
+    b = MI355XAttention(heads, qk, SCALE, kv_heads)
+    out, lse = b.prefill_with_context(q, k, v, kc, vc, cu_q, cu_c, max(lens_q), want_lse=True)
+    torch.cuda.synchronize()
+    qs, ks, vs = [], [], []
+    oq = oc = 0
+    for nq, nc in zip(lens_q, lens_c):
+        qs.append(q[oq:oq + nq])
+        ks.append(torch.cat([kc[oc:oc + nc], k[oq:oq + nq]]))
+        vs.append(torch.cat([vc[oc:oc + nc], v[oq:oq + nq]]))
+        oq, oc = oq + nq, oc + nc
+    want, want_lse = dense_rows(qs, ks, vs, True)
+    torch.testing.assert_close(out.float().cpu(), want, **TOL[dtype])
+    torch.testing.assert_close(lse.cpu(), want_lse, **TOL[dtype])
+    o1, l1 = b.varlen_with_lse(q, k, v, cu_q, cu_q, max(lens_q), max(lens_q), True)
+    o2, l2 = b.varlen_with_lse(q, kc, vc, cu_q, cu_c, max(lens_q), max(lens_c), False)
+    two = torch.empty_like(o1)
+    merge_attention_(o2, l2, o1, l1, two)
+    torch.testing.assert_close(out.float().cpu(), two.float().cpu(), **TOL[dtype])
+
+
+def test_prefill_with_context_writes_into_a_strided_out(cuda):
+    """``out`` as a view of a wider buffer (the layer's output slice): only its columns change."""
+    dtype, heads, qk, vd = torch.bfloat16, 16, 192, 128
+    gen = torch.Generator().manual_seed(6)
+    lens_q, lens_c = [9, 130], [65, 0]
+    q = rnd(sum(lens_q), heads, qk, gen=gen, dtype=dtype, device=cuda)
+    k = rnd(sum(lens_q), heads, qk, gen=gen, dtype=dtype, device=cuda)
+    v = rnd(sum(lens_q), heads, vd, gen=gen, dtype=dtype, device=cuda)
+    kc = rnd(sum(lens_c), heads, qk, gen=gen, dtype=dtype, device=cuda)
+    vc = rnd(sum(lens_c), heads, vd, gen=gen, dtype=dtype, device=cuda)
+    cu_q, cu_c = cumulative(lens_q, cuda), cumulative(lens_c, cuda)
+    b = MI355XAttention(heads, qk, SCALE, heads)
+    wide = torch.full((sum(lens_q), heads, vd + 64), 3.0, dtype=dtype, device=cuda)
+    b.prefill_with_context(q, k, v, kc, vc, cu_q, cu_c, max(lens_q), out=wide[..., :vd])
+    want = b.prefill_with_context(q, k, v, kc, vc, cu_q, cu_c, max(lens_q))
+    torch.cuda.synchronize()
+    assert torch.equal(wide[..., :vd], want) and (wide[..., vd:] == 3.0).all()

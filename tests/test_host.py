@@ -372,3 +372,23 @@ def test_a_step_of_prompts_says_so(monkeypatch):
     mixed = host_context([20, 0], [1, 9], [[0, 1], [2, -1]])
     layer.prefill(torch.zeros(10, 8, 64, dtype=torch.bfloat16), None, None, cache, cache, mixed)
     assert [bool(f & B.LV_ATTN_PROMPTS_ONLY) for f in calls] == [True, False]
+
+
+def test_whole_context_slots_and_offsets():
+    """``whole_context``: every row's cached keys in position order (rows with none included), their cache slots
+    through the row's table, and the per-step cache in ``attn_metadata``."""
+    from lvattn import Context, whole_context
+
+    bs = 4
+    cu_q = [0, 3, 4, 4, 9]          # new tokens per row: 3, 1, 0, 5
+    cu_k = [0, 10, 11, 17, 30]      # keys per row: 10, 1, 6, 13 -> cached 7, 0, 6, 8
+    tables = torch.tensor([[5, 2, 9, -1], [4, -1, -1, -1], [1, 0, -1, -1], [3, 8, 6, 7]], dtype=torch.int32)
+    ctx = Context(is_prefill=True, cu_seqlens_q_host=cu_q, cu_seqlens_k_host=cu_k, block_tables=tables)
+    slots, cu_ctx, max_ctx = whole_context(ctx, bs)
+    want = []
+    for r in range(4):
+        cached = (cu_k[r + 1] - cu_k[r]) - (cu_q[r + 1] - cu_q[r])
+        want += [int(tables[r, p // bs]) * bs + p % bs for p in range(cached)]
+    assert slots.tolist() == want and slots.dtype == torch.int64
+    assert cu_ctx.tolist() == [0, 7, 7, 13, 21] and cu_ctx.dtype == torch.int32 and max_ctx == 8
+    assert whole_context(ctx, bs)[0] is slots  # planned once per step
