@@ -60,8 +60,11 @@ __device__ inline int key_len(const AttnParams& p, int row) {
 
 template <int DQK, int DV>
 struct PromptSmem {
-  static constexpr int kKRow = DQK + 8;   // key tile row pitch, elements: conflict-free operand reads
-  static constexpr int kVRow = DV + 16;   // value tile row pitch, elements: conflict-free transposing reads
+  // Row pitches in elements. gfx950 serves the 16-byte operand reads (row = lane % 16) and the transposing 8-byte
+  // reads without bank conflicts when the pitch in dwords is 8 mod 16 (measured: 72 and 104 dwords free, 68, 76, 80,
+  // 100 and 108 two-way): 32 bytes of padding on both tiles, since every width here is a multiple of 64 elements.
+  static constexpr int kKRow = DQK + 16;  // key tile row pitch
+  static constexpr int kVRow = DV + 16;   // value tile row pitch
   static constexpr int kBytes = kPrefillKeys * (kKRow + kVRow) * 2;
 };
 
@@ -273,10 +276,10 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
   };
 
   if constexpr (RING > 0) {
-    // Stage layout: key rows of KCH data slots + 1 pad slot, then value rows of VCH + 2 (the tile pitches); the
+    // Stage layout: key rows of KCH data slots + 2 pad slots, then value rows of VCH + 2 (the tile pitches); the
     // pad slots hold a copy of the row's last chunk. 64-lane load j covers slots 64 j .. 64 j + 63; wave w issues
     // j = w, w + WAVES, ... Keys at or past lk load key lk - 1 instead (finite values; their weight is 0).
-    constexpr int KJ = KCH + 1, VJ = VCH + 2;  // loads per stage for the key / value rows (64 keys each)
+    constexpr int KJ = KCH + 2, VJ = VCH + 2;  // loads per stage for the key / value rows (64 keys each)
     constexpr int NJ = KJ + VJ;
     // this wave's loads per stage: waves < NJ % WAVES take HI
     constexpr int CNT_HI = (NJ + WAVES - 1) / WAVES, CNT_LO = NJ / WAVES;
