@@ -317,22 +317,19 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
       }
       const char* kb = (in_ctx ? p.ctx_k : p.k_cache) + koff;
       const char* vb = (in_ctx ? p.ctx_v : p.v_cache) + voff;
+      // Branch-free where it can be: every wave issues NJ / WAVES loads (when WAVES does not divide NJ, the first
+      // NJ % WAVES waves one more), each picking its source by selects rather than branches.
 #pragma unroll
       for (int i = 0; i < (NJ + WAVES - 1) / WAVES; ++i) {
         const int j = wave + WAVES * i;
-        if (j < NJ) {
-          uint32_t off;
-          const char* b;
-          if (j < KJ) {
-            const int slot = 64 * j + lane, key = slot / KJ;
-            off = (uint32_t)(min(key, last) * (int)kst + min(slot - key * KJ, KCH - 1) * 16);
-            b = kb;
-          } else {
-            const int slot = 64 * (j - KJ) + lane, key = slot / VJ;
-            off = (uint32_t)(min(key, last) * (int)vst + min(slot - key * VJ, VCH - 1) * 16);
-            b = vb;
-          }
-          lds_dma16<false>(b, off, lds_addr(stage + 64 * 8 * j));  // tiles other query tiles read again
+        if (NJ % WAVES == 0 || i < NJ / WAVES || j < NJ) {
+          const bool isk = j < KJ;  // wave-uniform: a load of key rows, else of value rows
+          const int slot = 64 * (isk ? j : j - KJ) + lane;
+          const int kkey = slot / KJ, vkey = slot / VJ;
+          const int key = isk ? kkey : vkey;
+          const int chunk = isk ? min(slot - kkey * KJ, KCH - 1) : min(slot - vkey * VJ, VCH - 1);
+          const uint32_t off = (uint32_t)(min(key, last) * (int)(isk ? kst : vst) + chunk * 16);
+          lds_dma16<false>(isk ? kb : vb, off, lds_addr(stage + 64 * 8 * j));  // tiles other query tiles read again
         }
       }
     };
