@@ -79,8 +79,11 @@ struct PromptSmem {
 // CTX (packed keys, RING > 0): the row's context keys (p.ctx_k / p.ctx_v, rows p.cu_ctx) come first, every one
 // visible to every query, then the row's own keys under the mask above -- one softmax over both, as the attention
 // over [context; own keys] with the mask aligned to the end.
+// TP (paged keys, RING > 0): pages per 64-key tile -- 1 for pages of a multiple of 64 keys (one lookup per page,
+// kept across the page's tiles), 2 or 4 for pages of 32 or 16 keys (the tile's pages looked up at every fill, each
+// lane loading from its key's page).
 template <typename T, int DQK, int DV, bool PREFETCH = true, bool OPAQUE_TID = false, int RING = 0, int WAVES = 4,
-          bool CTX = false>
+          bool CTX = false, int TP = 1>
 __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, char* smem) {
   using E = Elem<T>;
   constexpr int KS = DQK / 32;  // MFMA k-steps over the q.k width
@@ -98,6 +101,7 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
                 "tile chunks split over the threads");
   static_assert(DQK % 32 == 0 && DV % 16 == 0, "MFMA tile widths");
   static_assert(!CTX || RING > 0, "context keys stream through the LDS ring");
+  static_assert((TP == 1 || TP == 2 || TP == 4) && (TP == 1 || (RING > 0 && !CTX)), "pages per 64-key tile");
   int tid = threadIdx.x;
   if (OPAQUE_TID) asm volatile("" : "+v"(tid));
   const int lane = tid & 63;
@@ -302,7 +306,7 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
       if (in_ctx) {
         koff = (int64_t)(cbase + kt) * p.cx_st + kvh * p.cx_sh;
         voff = (int64_t)(cbase + kt) * p.cv_st + kvh * p.cv_sh;
-      } else if (p.paged) {
+      } else if (p.paged && TP == 1) {
         const int pg = (int)p.bs.div(kt);
         if (pg != cached_pg) {
           cached_pg = pg;
@@ -314,6 +318,33 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
       } else {
         koff = (int64_t)(kbase + kt) * p.c_st + kvh * p.c_sh;
         voff = (int64_t)(kbase + kt) * p.v_st + kvh * p.v_sh;
+      }
+      if constexpr (TP > 1) {
+        // Pages of BS = 64 / TP keys: the tile's TP pages (clamped to the row's last one), then per lane its key's.
+        constexpr int BS = kPrefillKeys / TP;
+        const int pg0 = kt / BS, pg_last = (lk - 1) / BS;
+        int64_t pb[TP];
+#pragma unroll
+        for (int q = 0; q < TP; ++q) pb[q] = (int64_t)sload(table + min(pg0 + q, pg_last)) * p.c_sb;
+#pragma unroll
+        for (int i = 0; i < (NJ + WAVES - 1) / WAVES; ++i) {
+          const int j = wave + WAVES * i;
+          if (NJ % WAVES == 0 || i < NJ / WAVES || j < NJ) {
+            const bool isk = j < KJ;  // wave-uniform: a load of key rows, else of value rows
+            const int slot = 64 * (isk ? j : j - KJ) + lane;
+            const int kkey = slot / KJ, vkey = slot / VJ;
+            const int key = min(isk ? kkey : vkey, last);
+            const int chunk = isk ? min(slot - kkey * KJ, KCH - 1) : min(slot - vkey * VJ, VCH - 1);
+            int64_t b = pb[0];
+#pragma unroll
+            for (int q = 1; q < TP; ++q) b = key / BS == q ? pb[q] : b;
+            const char* src = (isk ? p.k_cache : p.v_cache) + b +
+                              (int64_t)(key % BS) * (isk ? p.c_st : p.v_st) + kvh * (isk ? p.c_sh : p.v_sh) +
+                              chunk * 16;
+            lds_dma16<false>(src, lds_addr(stage + 64 * 8 * j));  // tiles other query tiles read again
+          }
+        }
+        return;
       }
       const char* kb = (in_ctx ? p.ctx_k : p.k_cache) + koff;
       const char* vb = (in_ctx ? p.ctx_v : p.v_cache) + voff;

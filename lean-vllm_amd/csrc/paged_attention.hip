@@ -23,7 +23,7 @@ constexpr int kTile = 16;          // decode tokens per tile; block sizes are mu
 constexpr int kWaves = 4;          // waves per workgroup
 constexpr int kPlanMaxRows = 4096;  // rows of a step with prompts (the work-list scan lives in LDS)
 
-constexpr int kPromptRing = 2;        // LDS stages of the prompt tiles' ring (pages a multiple of 64 tokens)
+constexpr int kPromptRing = 2;        // LDS stages of the prompt tiles' ring
 constexpr int kOverlapCusPct = 50;    // percent of the CUs that hold a prompt workgroup in a mixed step by default
 constexpr int kOverlapCusMaxPct = 75;  // at most this percent when the caller sizes the prompt share
 constexpr int kDecodeWgs = 2;         // persistent decode workgroups per CU outside the overlap
@@ -355,14 +355,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_num_vgpr(160))) void dec
   decode_persistent<T, D, GS>(p);
 }
 
-// RING > 0: pages are a multiple of 64 tokens, so prompt tiles stream through an LDS ring of RING stages.
-template <typename T, int D, int RING>
+// TP: pages per 64-key prompt tile. TP > 0 (pages of a multiple of 64 keys, or of 32 or 16): the tiles stream
+// through an LDS ring of kPromptRing stages; TP = 0 (other page sizes): through registers.
+template <int TP>
+constexpr int kRingOf = TP > 0 ? kPromptRing : 0;
+
+template <typename T, int D, int TP>
 __global__ __launch_bounds__(256, 2) void prompt_list_kernel(AttnParams p) {
+  constexpr int RING = kRingOf<TP>;
   __shared__ __attribute__((aligned(16))) char smem[(RING > 0 ? RING : 1) * PromptSmem<D, D>::kBytes];
   const int bx = blockIdx.x / p.hkv, kvh = blockIdx.x - bx * p.hkv;
   if (bx >= p.n_items[1]) return;
   const int2 it = p.items[bx];
-  prefill_item<T, D, D, true, false, RING>(p, it.x, -1 - it.y, kvh, smem);
+  prefill_item<T, D, D, true, false, RING, 4, false, (TP > 0 ? TP : 1)>(p, it.x, -1 - it.y, kvh, smem);
 }
 
 // Prompt items of a mixed step, run at the same time as its decode items: one workgroup per CU, each walking the
@@ -370,8 +375,9 @@ __global__ __launch_bounds__(256, 2) void prompt_list_kernel(AttnParams p) {
 // budgets registers for 2 waves per SIMD) leaves room for no second one, and the decode workgroups take the CU's
 // remaining registers: the MFMA work of the prompt tiles hides under the decode rows' memory streaming.
 constexpr int kOverlapLds = 84 * 1024;
-template <typename T, int D, int RING>
+template <typename T, int D, int TP>
 __global__ __launch_bounds__(256, 2) void prompt_overlap_kernel(AttnParams p) {
+  constexpr int RING = kRingOf<TP>;
   __shared__ __attribute__((aligned(16))) char smem[(RING > 0 ? RING : 1) * PromptSmem<D, D>::kBytes];
   // The prompt tiles are the step's critical path beside the decode waves, which need few issue slots: the prompt
   // waves win the SIMD's issue arbitration (1% on the Qwen3-8B mixed step; favouring the decode waves costs 15%).
@@ -380,7 +386,7 @@ __global__ __launch_bounds__(256, 2) void prompt_overlap_kernel(AttnParams p) {
   for (int f = blockIdx.x; f < n; f += gridDim.x) {
     const int bx = f / p.hkv, kvh = f - bx * p.hkv;
     const int2 it = p.items[bx];
-    prefill_item<T, D, D, true, true, RING>(p, it.x, -1 - it.y, kvh, smem);
+    prefill_item<T, D, D, true, true, RING, 4, false, (TP > 0 ? TP : 1)>(p, it.x, -1 - it.y, kvh, smem);
     __syncthreads();  // the next item restages the LDS tiles
   }
 }
@@ -390,8 +396,9 @@ __global__ __launch_bounds__(256, 2) void prompt_overlap_kernel(AttnParams p) {
 // first and the decode workgroups stream through the slots they leave, as in the overlapped schedule but without a
 // second stream, its events and one launch: for steps of a few hundred rows, whose launch sequence is a large share
 // of their time.
-template <typename T, int D, int GS, int RING>
+template <typename T, int D, int GS, int TP>
 __global__ __launch_bounds__(256, 2) void mixed_small_kernel(AttnParams p, int32_t prompt_wgs) {
+  constexpr int RING = kRingOf<TP>;
   static_assert(SmemBytes<D, GS>::kDecode <= (RING > 0 ? RING : 1) * PromptSmem<D, D>::kBytes, "LDS for both");
   __shared__ __attribute__((aligned(16))) char smem[(RING > 0 ? RING : 1) * PromptSmem<D, D>::kBytes];
   const int b = blockIdx.x;
@@ -399,7 +406,7 @@ __global__ __launch_bounds__(256, 2) void mixed_small_kernel(AttnParams p, int32
     const int bx = b / p.hkv, kvh = b - bx * p.hkv;
     if (bx >= p.n_items[1]) return;
     const int2 it = p.items[bx];
-    prefill_item<T, D, D, true, false, RING>(p, it.x, -1 - it.y, kvh, smem);
+    prefill_item<T, D, D, true, false, RING, 4, false, (TP > 0 ? TP : 1)>(p, it.x, -1 - it.y, kvh, smem);
   } else {
     const int ny = p.hkv * p.qgroups;
     const int f = b - prompt_wgs, bx = f / ny, by = f - bx * ny;
@@ -670,40 +677,30 @@ static int prompt_grid(const Shape& s, const AttnParams& p, int requested) {
 }
 
 // The prompt items of a step with prompts, one workgroup per item, on the whole GPU.
-template <typename T, int D>
-static void launch_prompt_list(const AttnParams& p, const Shape& s, bool ring, hipStream_t stream) {
-  const dim3 grid(s.max_prompt_items * p.hkv);
-  if (ring)
-    hipLaunchKernelGGL((prompt_list_kernel<T, D, kPromptRing>), grid, dim3(256), 0, stream, p);
-  else
-    hipLaunchKernelGGL((prompt_list_kernel<T, D, 0>), grid, dim3(256), 0, stream, p);
+template <typename T, int D, int TP>
+static void launch_prompt_list(const AttnParams& p, const Shape& s, hipStream_t stream) {
+  hipLaunchKernelGGL((prompt_list_kernel<T, D, TP>), dim3(s.max_prompt_items * p.hkv), dim3(256), 0, stream, p);
 }
 
 // A step's kernels after the plan. An overlapped mixed step forks the decode items onto the device's second stream
 // and joins it back into `stream` with events; if the second stream cannot be set up, or the fork's record or wait
 // fails before anything is launched, the step runs serially instead (the same results). A failure after the decode
 // launch leaves the two streams unordered and is returned as LV_EHIP.
-template <typename T, int D, int GS>
+template <typename T, int D, int GS, int TP>
 static int launch(const AttnParams& p, bool listed, bool mixed, bool overlap, int prompt_wgs, const Shape& s,
                   hipStream_t stream, bool prompts_only) {
   const int ny = p.hkv * p.qgroups;
-  const bool ring = p.bs.d % kPrefillKeys == 0;  // every 64-key tile in one page
   if (prompts_only) {  // a step of prompts: the prompt tiles on the whole GPU, nothing else
-    launch_prompt_list<T, D>(p, s, ring, stream);
+    launch_prompt_list<T, D, TP>(p, s, stream);
     return LV_OK;
   }
   if (overlap && listed && mixed) {
     // A step whose workgroups (bounds: most prompt bounds exit at once) fill the GPU at most kSmallStepRounds times
     // runs as one launch.
     const int64_t pw = (int64_t)s.max_prompt_items * p.hkv, dw = (int64_t)s.max_decode_items * ny;
-    const int resident = ring ? resident_per_cu<mixed_small_kernel<T, D, GS, kPromptRing>>()
-                              : resident_per_cu<mixed_small_kernel<T, D, GS, 0>>();
+    const int resident = resident_per_cu<mixed_small_kernel<T, D, GS, TP>>();
     if (pw + dw <= (int64_t)kSmallStepRounds * resident * device_cus()) {
-      if (ring)
-        hipLaunchKernelGGL((mixed_small_kernel<T, D, GS, kPromptRing>), dim3(pw + dw), dim3(256), 0, stream, p,
-                           (int32_t)pw);
-      else
-        hipLaunchKernelGGL((mixed_small_kernel<T, D, GS, 0>), dim3(pw + dw), dim3(256), 0, stream, p, (int32_t)pw);
+      hipLaunchKernelGGL((mixed_small_kernel<T, D, GS, TP>), dim3(pw + dw), dim3(256), 0, stream, p, (int32_t)pw);
       LV_LAUNCH_CHECK("mixed_small_kernel");
       if (p.max_splits > 1)
         hipLaunchKernelGGL((splitk_merge_kernel<T, D>), dim3(p.rows, p.hq), dim3(64), 0, stream, p);
@@ -723,13 +720,8 @@ static int launch(const AttnParams& p, bool listed, bool mixed, bool overlap, in
       launch_decode<T, D, GS, true>(p, s, kOverlapDecodeWgs, side->stream);
       LV_LAUNCH_CHECK("decode_persistent_kernel");
       LV_HIP_CHECK(hipEventRecord(side->join, side->stream));
-      if (ring) {
-        constexpr int pad = std::max(0, kOverlapLds - kPromptRing * PromptSmem<D, D>::kBytes);
-        hipLaunchKernelGGL((prompt_overlap_kernel<T, D, kPromptRing>), dim3(grid), dim3(256), pad, stream, p);
-      } else {
-        constexpr int pad = kOverlapLds - PromptSmem<D, D>::kBytes;
-        hipLaunchKernelGGL((prompt_overlap_kernel<T, D, 0>), dim3(grid), dim3(256), pad, stream, p);
-      }
+      constexpr int pad = std::max(0, kOverlapLds - std::max(1, kRingOf<TP>) * PromptSmem<D, D>::kBytes);
+      hipLaunchKernelGGL((prompt_overlap_kernel<T, D, TP>), dim3(grid), dim3(256), pad, stream, p);
       LV_LAUNCH_CHECK("prompt_overlap_kernel");
       LV_HIP_CHECK(hipStreamWaitEvent(stream, side->join, 0));
     } else {
@@ -738,7 +730,7 @@ static int launch(const AttnParams& p, bool listed, bool mixed, bool overlap, in
   }
   if (forked) {
   } else if (listed && mixed) {
-    launch_prompt_list<T, D>(p, s, ring, stream);
+    launch_prompt_list<T, D, TP>(p, s, stream);
     launch_decode<T, D, GS>(p, s, kDecodeWgs, stream);
   } else if (listed) {
     launch_decode<T, D, GS>(p, s, kDecodeWgs, stream);
@@ -750,12 +742,32 @@ static int launch(const AttnParams& p, bool listed, bool mixed, bool overlap, in
   return LV_OK;
 }
 
+// Pages per 64-key prompt tile for the LDS ring: 1 for pages of a multiple of 64 keys, 2 or 4 for pages of 32 or
+// 16; 0 (register staging) for any other size.
+static int tile_pages(int block_size) {
+  if (block_size % kPrefillKeys == 0) return 1;
+  if (block_size == 32) return 2;
+  if (block_size == 16) return 4;
+  return 0;
+}
+
+template <typename T, int D, int GS>
+static int launch_tp(const AttnParams& p, bool listed, bool mixed, bool overlap, int prompt_wgs, const Shape& s,
+                     hipStream_t stream, bool prompts_only) {
+  switch (tile_pages((int)p.bs.d)) {
+    case 1: return launch<T, D, GS, 1>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
+    case 2: return launch<T, D, GS, 2>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
+    case 4: return launch<T, D, GS, 4>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
+    default: return launch<T, D, GS, 0>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
+  }
+}
+
 template <typename T, int D>
 static int launch_gs(const AttnParams& p, int gs, bool listed, bool mixed, bool overlap, int prompt_wgs,
                      const Shape& s, hipStream_t stream, bool prompts_only) {
-  if (gs == 4) return launch<T, D, 4>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
-  if (gs == 2) return launch<T, D, 2>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
-  return launch<T, D, 1>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
+  if (gs == 4) return launch_tp<T, D, 4>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
+  if (gs == 2) return launch_tp<T, D, 2>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
+  return launch_tp<T, D, 1>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
 }
 
 template <typename T>

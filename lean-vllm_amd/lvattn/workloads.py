@@ -116,7 +116,7 @@ def qwen3_8b_decode(seed: int = 0, batch: int = 256, block_size: int = 256) -> W
                     1 / math.sqrt(128), num_layers=36)
 
 
-def qwen3_8b_mixed(seed: int = 0) -> Workload:
+def qwen3_8b_mixed(seed: int = 0, block_size: int = 256) -> Workload:
     rng = np.random.default_rng(seed)
     prefix = rng.integers(0, 6144 + 1, size=4)
     dec = rng.integers(256, 4096 + 1, size=2048)
@@ -124,15 +124,18 @@ def qwen3_8b_mixed(seed: int = 0) -> Workload:
     num_cached = [int(p) for p in prefix] + [int(c) - 1 for c in dec]
     num_new = [1536] * 4 + [1] * 2048
     ends = [c + n for c, n in zip(num_cached, num_new)]
-    return Workload("qwen3_8b_mixed", 32, 8, 128, 256, 24_000, num_cached, num_new,
-                    _tables(rng, 24_000, ends, 256), 1 / math.sqrt(128), num_layers=36)
+    pool = 24_000 * 256 // block_size
+    name = "qwen3_8b_mixed" if block_size == 256 else f"qwen3_8b_mixed_bs{block_size}"
+    return Workload(name, 32, 8, 128, block_size, pool, num_cached, num_new, _tables(rng, pool, ends, block_size),
+                    1 / math.sqrt(128), num_layers=36)
 
 
-def qwen3_8b_prefill(seed: int = 0) -> Workload:
+def qwen3_8b_prefill(seed: int = 0, block_size: int = 256) -> Workload:
     """The Qwen3-8B mixed step's four prompt chunks alone (same draws): a step of prompts, MFMA-bound."""
-    mixed = qwen3_8b_mixed(seed)
+    mixed = qwen3_8b_mixed(seed, block_size)
     rows = [i for i, n in enumerate(mixed.num_new) if n > 1]
-    return Workload("qwen3_8b_prefill", 32, 8, 128, 256, 24_000, [mixed.num_cached[i] for i in rows],
+    name = "qwen3_8b_prefill" if block_size == 256 else f"qwen3_8b_prefill_bs{block_size}"
+    return Workload(name, 32, 8, 128, block_size, mixed.pool, [mixed.num_cached[i] for i in rows],
                     [mixed.num_new[i] for i in rows], [mixed.block_lists[i] for i in rows], 1 / math.sqrt(128),
                     num_layers=36)
 
@@ -177,6 +180,8 @@ WORKLOADS = {
     "deepseek_v2_lite_mla_prefill_two_pass": lambda seed=0: dataclasses.replace(
         deepseek_v2_lite_mla_prefill(seed), name="deepseek_v2_lite_mla_prefill_two_pass", two_pass=True),
     "qwen3_8b_decode_bs16": lambda seed=0: qwen3_8b_decode(seed, block_size=16),
+    "qwen3_8b_mixed_bs16": lambda seed=0: qwen3_8b_mixed(seed, block_size=16),
+    "qwen3_8b_prefill_bs16": lambda seed=0: qwen3_8b_prefill(seed, block_size=16),
     "deepseek_v2_lite_mla_bs16": lambda seed=0: deepseek_v2_lite_mla(seed, block_size=16),
 }
 

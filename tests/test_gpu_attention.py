@@ -40,18 +40,24 @@ def run_step(backend, dtype, dim, device, num_cached, num_new, tables, nblocks, 
     return out, dense_expected(qs, kf, vf, SCALE), (qs, kf, vf, kc, vc, ctx)
 
 
-@pytest.mark.parametrize("bs", [64, 256])
+@pytest.mark.parametrize("bs", [16, 32, 48, 64, 256])
 def test_prefill_through_the_lds_ring(case, bs):
-    """Pages that hold whole 64-key tiles: prompt tiles stream through the LDS ring. Prefixes of several tiles,
-    tails that end mid-tile, a decode row beside the chunks, and NaN in every unused cache slot (a tile's keys
-    past the row's end must never bring one in)."""
+    """Prompt tiles stream through the LDS ring for pages of a multiple of 64 keys (one page per tile) and of 16
+    or 32 keys (four or two pages per tile, each lane loading from its key's page); 48-key pages take the register
+    path. Prefixes of several tiles, tails that end mid-tile and mid-page, a decode row beside the chunks, pages
+    scattered over the pool, and NaN in every unused cache slot (a tile's keys past the row's end must never bring
+    one in)."""
     b, dtype, dim, dev = case
     cached, new = [3 * 64 + 5, 0, 70, bs - 1], [77, 130, 1, 9]
-    pages = [[6 * r + i for i in range(6)] for r in range(4)]  # scattered: row r's pages are 6r .. 6r + 5
-    width = max(-(-(c + n) // bs) for c, n in zip(cached, new))
-    tables = [pg[:-(-(c + n) // bs)] + [-1] * (width - -(-(c + n) // bs)) for pg, c, n in zip(pages, cached, new)]
-    qs, kf, vf, kn, vn, kc, vc, slots = paged_step(cached, new, tables, 24, heads=H, kv_heads=HKV, dim=dim, bs=bs,
-                                                   device=dev, dtype=dtype, fill=float("nan"))
+    need = [-(-(c + n) // bs) for c, n in zip(cached, new)]
+    perm = torch.randperm(sum(need) + 3, generator=torch.Generator().manual_seed(bs)).tolist()
+    width = max(need)
+    tables, at = [], 0
+    for k in need:
+        tables.append(perm[at:at + k] + [-1] * (width - k))
+        at += k
+    qs, kf, vf, kn, vn, kc, vc, slots = paged_step(cached, new, tables, sum(need) + 3, heads=H, kv_heads=HKV,
+                                                   dim=dim, bs=bs, device=dev, dtype=dtype, fill=float("nan"))
     b.store_kvcache(kn, vn, kc, vc, slots)
     out = b.forward(torch.cat(qs), kn, vn, kc, vc, context_for(cached, new, tables, dev))
     torch.cuda.synchronize()
@@ -79,7 +85,7 @@ def test_mixed_batch_of_chunks_and_decodes(case):
     check(out, want, dtype)
 
 
-@pytest.mark.parametrize("bs", [16, 64])
+@pytest.mark.parametrize("bs", [16, 32, 64])
 @pytest.mark.parametrize("poison", [None, float("nan")], ids=["clean", "nan-slots"])
 def test_both_launch_schedules_give_the_same_step(case, bs, poison, monkeypatch):
     """A mixed step (chunks on cached prefixes, decode rows, a cold prompt) under the serial schedule (prompt

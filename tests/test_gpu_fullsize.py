@@ -112,6 +112,19 @@ def test_qwen3_8b_prompt_chunks_alone(cuda):
     assert check_prompt_queries(wl, t, out, order, cu_q, every=64) == 4 * 25
 
 
+def test_qwen3_8b_mixed_step_on_16_token_pages(cuda):
+    """The mixed step on lean-vLLM's default page size (16 keys: four pages per prompt tile, each lane loading from
+    its key's page): every 64th query of the chunks and their last, and every decode row."""
+    wl, t, out, order, cu_q = run_step("qwen3_8b_mixed_bs16", cuda)
+    assert check_prompt_queries(wl, t, out, order, cu_q, every=64) == 4 * 25
+    assert check_decode_rows(wl, t, out, order, cu_q) == 2048
+
+
+def test_qwen3_8b_prompt_chunks_alone_on_16_token_pages(cuda):
+    wl, t, out, order, cu_q = run_step("qwen3_8b_prefill_bs16", cuda)
+    assert check_prompt_queries(wl, t, out, order, cu_q, every=64) == 4 * 25
+
+
 @pytest.mark.parametrize("name, rows", [("qwen3_8b_decode", 256), ("qwen3_8b_long", 16)])
 def test_decode_steps_every_row(cuda, name, rows):
     """Batch-256 decode (contexts 512-8192, split into two 4096-key items) and the long-context step (contexts
