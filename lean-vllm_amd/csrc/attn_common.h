@@ -320,12 +320,18 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
         voff = (int64_t)(kbase + kt) * p.v_st + kvh * p.v_sh;
       }
       if constexpr (TP > 1) {
-        // Pages of BS = 64 / TP keys: the tile's TP pages (clamped to the row's last one), then per lane its key's.
+        // Pages of BS = 64 / TP keys: the tile's TP page numbers (clamped to the row's last page), loaded together
+        // through the scalar cache.
         constexpr int BS = kPrefillKeys / TP;
-        const int pg0 = kt / BS, pg_last = (lk - 1) / BS;
+        const int pg_last = (lk - 1) / BS;
+        const int32_t* pp[TP];
+#pragma unroll
+        for (int q = 0; q < TP; ++q) pp[q] = table + min(t * TP + q, pg_last);
+        int pg[TP];
+        sload_n<TP>(pp, pg);
         int64_t pb[TP];
 #pragma unroll
-        for (int q = 0; q < TP; ++q) pb[q] = (int64_t)sload(table + min(pg0 + q, pg_last)) * p.c_sb;
+        for (int q = 0; q < TP; ++q) pb[q] = (int64_t)pg[q] * p.c_sb;
 #pragma unroll
         for (int i = 0; i < (NJ + WAVES - 1) / WAVES; ++i) {
           const int j = wave + WAVES * i;
@@ -333,14 +339,13 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
             const bool isk = j < KJ;  // wave-uniform: a load of key rows, else of value rows
             const int slot = 64 * (isk ? j : j - KJ) + lane;
             const int kkey = slot / KJ, vkey = slot / VJ;
-            const int key = min(isk ? kkey : vkey, last);
+            const uint32_t key = (uint32_t)min(isk ? kkey : vkey, last);  // last >= 0: the tile holds a key
             const int chunk = isk ? min(slot - kkey * KJ, KCH - 1) : min(slot - vkey * VJ, VCH - 1);
             int64_t b = pb[0];
 #pragma unroll
-            for (int q = 1; q < TP; ++q) b = key / BS == q ? pb[q] : b;
-            const char* src = (isk ? p.k_cache : p.v_cache) + b +
-                              (int64_t)(key % BS) * (isk ? p.c_st : p.v_st) + kvh * (isk ? p.c_sh : p.v_sh) +
-                              chunk * 16;
+            for (int q = 1; q < TP; ++q) b = key / BS == (uint32_t)q ? pb[q] : b;
+            const char* src = (isk ? p.k_cache : p.v_cache) + b + (int64_t)(key % BS) * (isk ? p.c_st : p.v_st) +
+                              kvh * (isk ? p.c_sh : p.v_sh) + chunk * 16;
             lds_dma16<false>(src, lds_addr(stage + 64 * 8 * j));  // tiles other query tiles read again
           }
         }

@@ -324,6 +324,23 @@ __device__ __forceinline__ int sload(const int32_t* ptr) {
   return v;
 }
 
+// N such loads (2 or 4) issued together, then one wait.
+template <int N>
+__device__ __forceinline__ void sload_n(const int32_t* const (&ptr)[N], int (&v)[N]) {
+  static_assert(N == 2 || N == 4, "2 or 4 loads");
+  if constexpr (N == 2) {
+    asm volatile("s_load_dword %0, %2, 0x0\n\ts_load_dword %1, %3, 0x0\n\ts_waitcnt lgkmcnt(0)"
+                 : "=&s"(v[0]), "=&s"(v[1])
+                 : "s"(ptr[0]), "s"(ptr[1]));
+  } else {
+    asm volatile(
+        "s_load_dword %0, %4, 0x0\n\ts_load_dword %1, %5, 0x0\n\ts_load_dword %2, %6, 0x0\n\t"
+        "s_load_dword %3, %7, 0x0\n\ts_waitcnt lgkmcnt(0)"
+        : "=&s"(v[0]), "=&s"(v[1]), "=&s"(v[2]), "=&s"(v[3])
+        : "s"(ptr[0]), "s"(ptr[1]), "s"(ptr[2]), "s"(ptr[3]));
+  }
+}
+
 // Wait until at most N of this wave's vector-memory operations are outstanding, then meet the other waves. No
 // fence: a staging ring's LDS writes are exactly the loads waited for, and a fence would also wait for the stages
 // still in flight.
