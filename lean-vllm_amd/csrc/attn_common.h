@@ -58,15 +58,30 @@ __device__ inline int key_len(const AttnParams& p, int row) {
 // sees keys 0 .. lk - lq + j; none if p.causal is 0) is applied only on tiles that cross it.
 // DQK: q.k width; DV: value width.
 
-template <int DQK, int DV>
+// Stage tiles are row-major, laid out so that the operand reads (row = lane % 16, one 16-byte chunk per lane) and the
+// transposing value reads (rows 4 j4 + n / 4, 8 bytes per lane) meet no bank conflicts on gfx950. Its LDS (64 banks
+// of 4 bytes) serves a 16-byte read in passes over lanes {0-7, 16-23}, {8-15, 24-31}, ... and an 8-byte read over
+// lanes {0-31}, {32-63}; counter probes confirm the model (row pitches of 72 and 104 dwords conflict-free; 68, 76,
+// 80, 100 and 108 two-way). Two layouts meet it:
+// - padded (SWZ false): a 32-byte pad per row (pitch 8 mod 16 dwords), the pad slots loaded with copies of the row's
+//   last chunk; every read offset is a compile-time immediate;
+// - swizzled (SWZ true): no padding, chunk c of row r at position c ^ 2 (r mod 8) for rows of 16 chunks, c ^ (r mod 8)
+//   for rows of 8 or 24. A 64-lane load then covers whole key rows, so on pages of 16 or 32 keys each load stays in
+//   one page; the reads take per-lane offsets (measured 1.6% slower on one-page tiles, so those keep the pads).
+template <int DQK, int DV, bool SWZ = false>
 struct PromptSmem {
-  // Row pitches in elements. gfx950 serves the 16-byte operand reads (row = lane % 16) and the transposing 8-byte
-  // reads without bank conflicts when the pitch in dwords is 8 mod 16 (measured: 72 and 104 dwords free, 68, 76, 80,
-  // 100 and 108 two-way): 32 bytes of padding on both tiles, since every width here is a multiple of 64 elements.
-  static constexpr int kKRow = DQK + 16;  // key tile row pitch
-  static constexpr int kVRow = DV + 16;   // value tile row pitch
+  static constexpr int kKRow = SWZ ? DQK : DQK + 16;  // key tile row pitch, elements
+  static constexpr int kVRow = SWZ ? DV : DV + 16;    // value tile row pitch, elements
   static constexpr int kBytes = kPrefillKeys * (kKRow + kVRow) * 2;
 };
+
+// Position of 16-byte chunk c in a stage row r of CH chunks (an involution: it also maps a position to its chunk).
+template <int CH, bool SWZ>
+__device__ __forceinline__ int swz(int r, int c) {
+  static_assert(CH == 8 || CH == 16 || CH == 24, "rows of 8, 16 or 24 chunks");
+  if constexpr (!SWZ) return c;
+  return c ^ (CH == 16 ? 2 * (r & 7) : (r & 7));
+}
 
 // PREFETCH: the next tile's K/V loads are in flight in registers while this tile is consumed (more registers).
 // OPAQUE_TID: for a caller that runs items in a loop; the thread index is hidden from the optimiser, so per-lane
@@ -88,8 +103,9 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
   using E = Elem<T>;
   constexpr int KS = DQK / 32;  // MFMA k-steps over the q.k width
   constexpr int DB = DV / 16;   // 16-dim blocks of the output
-  constexpr int KROW = PromptSmem<DQK, DV>::kKRow;
-  constexpr int VROW = PromptSmem<DQK, DV>::kVRow;
+  constexpr bool SWZ = TP > 1;  // the swizzled stage layout (pages of 16 or 32 keys)
+  constexpr int KROW = PromptSmem<DQK, DV, SWZ>::kKRow;
+  constexpr int VROW = PromptSmem<DQK, DV, SWZ>::kVRow;
   constexpr int KCH = DQK / 8, VCH = DV / 8;  // 16-byte chunks per key / value row
   constexpr int KCHUNKS = kPrefillKeys * KCH;
   constexpr int NT = 64 * WAVES;                        // threads
@@ -189,10 +205,25 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
   auto stash = [&](uint16_t* ks, uint16_t* vs, const u32x4 (&st)[PER]) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      uint16_t* dst = i < KPER ? ks + key_of(i) * KROW : vs + key_of(i) * VROW;
-      st16(reinterpret_cast<char*>(dst + part_of(i) * 8), st[i]);
+      const int key = key_of(i), part = part_of(i);
+      uint16_t* dst =
+          i < KPER ? ks + key * KROW + swz<KCH, SWZ>(key, part) * 8 : vs + key * VROW + swz<VCH, SWZ>(key, part) * 8;
+      st16(reinterpret_cast<char*>(dst), st[i]);
     }
   };
+
+  // Swizzled element offsets of this lane's operand reads inside a stage row, the same for every tile: the key chunk
+  // of k-step k (row 16 kb + n, chunk 4 k + j4), and the value half-chunk of output block b (rows 32 h + 4 j4 + n / 4
+  // (+ 16), dims 16 b + 4 (n % 4) .. + 3).
+  // (Padded layout: 32 k + 8 j4 and 16 b + 4 (n % 4), offsets the compiler folds into the reads' immediates.)
+  int kpos[SWZ ? KS : 1], vpos[SWZ ? DB : 1];
+  if constexpr (SWZ) {
+#pragma unroll
+    for (int k = 0; k < KS; ++k) kpos[k] = 8 * swz<KCH, SWZ>(n, 4 * k + j4);
+#pragma unroll
+    for (int b = 0; b < DB; ++b)
+      vpos[b] = 8 * swz<VCH, SWZ>(4 * j4 + (n >> 2), 2 * b + ((n & 3) >> 1)) + 4 * (n & 1);
+  }
 
   // One 64-key tile (keys kt .. kt + 63 of its source) from the K/V tile in LDS at ks / vs: scores, mask (query row
   // nb sees keys < l[nb]), online softmax, P.V.
@@ -207,7 +238,8 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
     for (int k = 0; k < KS; ++k)
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
-        const u32x4 a = *reinterpret_cast<const u32x4*>(ks + (kb * 16 + n) * KROW + 32 * k + 8 * j4);
+        const u32x4 a = *reinterpret_cast<const u32x4*>(ks + (kb * 16 + n) * KROW +
+                                                         (SWZ ? kpos[SWZ ? k : 0] : 32 * k + 8 * j4));
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) st[kb][nb] = E::mfma16x16x32(a, qb[nb][k], st[kb][nb]);
       }
@@ -266,13 +298,14 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
       l[nb] += psum;
     }
     // V^T operand rows (dims) 16 b + n; transposing reads of rows 32 h + 4 j4 + (n >> 2) (+ 16), dims + 4 (n & 3).
-    const uint16_t* vrow = vs + (4 * j4 + (n >> 2)) * VROW + 4 * (n & 3);
+    const uint16_t* vrow = vs + (4 * j4 + (n >> 2)) * VROW + (SWZ ? 0 : 4 * (n & 3));
 #pragma unroll
     for (int b = 0; b < DB; ++b)
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const u32x2 lo = lds_read_tr16(vrow + 32 * h * VROW + 16 * b);
-        const u32x2 hi = lds_read_tr16(vrow + (32 * h + 16) * VROW + 16 * b);
+        const int vb = SWZ ? vpos[SWZ ? b : 0] : 16 * b;
+        const u32x2 lo = lds_read_tr16(vrow + 32 * h * VROW + vb);
+        const u32x2 hi = lds_read_tr16(vrow + (32 * h + 16) * VROW + vb);
         const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) o[nb][b] = E::mfma16x16x32(a, pb[nb][h], o[nb][b]);
@@ -280,15 +313,17 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
   };
 
   if constexpr (RING > 0) {
-    // Stage layout: key rows of KCH data slots + 2 pad slots, then value rows of VCH + 2 (the tile pitches); the
-    // pad slots hold a copy of the row's last chunk. 64-lane load j covers slots 64 j .. 64 j + 63; wave w issues
-    // j = w, w + WAVES, ... Keys at or past lk load key lk - 1 instead (finite values; their weight is 0).
-    constexpr int KJ = KCH + 2, VJ = VCH + 2;  // loads per stage for the key / value rows (64 keys each)
-    constexpr int NJ = KJ + VJ;
+    // Stage layout: 64 key rows of KJ 16-byte slots, then 64 value rows of VJ (KCH / VCH chunks, plus two pad slots
+    // in the padded layout, which hold copies of the row's last chunk). 64-lane load j covers slots 64 j .. 64 j + 63
+    // (of the key rows for j < KJ, else of the value rows); lane l of it loads the chunk that belongs at its slot.
+    // Wave w issues j = w, w + WAVES, ... Keys at or past lk load key lk - 1 instead (finite values; their weight is
+    // 0).
+    constexpr int KJ = KCH + (SWZ ? 0 : 2), VJ = VCH + (SWZ ? 0 : 2);
+    constexpr int NJ = KJ + VJ;  // loads per stage
     // this wave's loads per stage: waves < NJ % WAVES take HI
     constexpr int CNT_HI = (NJ + WAVES - 1) / WAVES, CNT_LO = NJ / WAVES;
-    constexpr int kStageElems = PromptSmem<DQK, DV>::kBytes / 2;
-    static_assert(PromptSmem<DQK, DV>::kKRow == KJ * 8 && PromptSmem<DQK, DV>::kVRow == VJ * 8, "pitches");
+    constexpr int kStageElems = PromptSmem<DQK, DV, SWZ>::kBytes / 2;
+    static_assert(KROW == KJ * 8 && VROW == VJ * 8, "pitches");
     static_assert(RING >= 2 && RING <= 3, "one or two tiles in flight");
     uint16_t* ring = reinterpret_cast<uint16_t*>(smem);
     const bool hi = wave < NJ % WAVES || NJ % WAVES == 0;
@@ -302,11 +337,51 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
       const int kt = (in_ctx ? t : t - nc) * kPrefillKeys;
       const int last = (in_ctx ? lc : lk) - 1 - kt;
       const int64_t kst = in_ctx ? p.cx_st : p.c_st, vst = in_ctx ? p.cv_st : p.v_st;
+      // Load j of this wave: chunk position slot of the key (isk) or value rows; its key row and source chunk.
+      auto source = [&](int j, bool& isk, int& key, int& chunk) {
+        isk = j < KJ;  // wave-uniform
+        const int slot = 64 * (isk ? j : j - KJ) + lane;
+        const int kkey = slot / KJ, vkey = slot / VJ;
+        key = isk ? kkey : vkey;
+        chunk = isk ? swz<KCH, SWZ>(kkey, min(slot - kkey * KJ, KCH - 1))
+                    : swz<VCH, SWZ>(vkey, min(slot - vkey * VJ, VCH - 1));
+      };
+      if constexpr (TP > 1) {
+        // Pages of BS = 64 / TP keys. A load's 64 lanes cover 64 / KCH (or 64 / VCH) consecutive keys inside one page
+        // (those past the row's end load its last key, on the same page), so each load has a wave-uniform page: the
+        // tile's TP page numbers (clamped to the row's last page) come in with one scalar wait.
+        constexpr int BS = kPrefillKeys / TP;
+        static_assert(SWZ && kPrefillKeys / KCH <= BS && kPrefillKeys / VCH <= BS, "a load within one page");
+        const int pg_last = (lk - 1) / BS;
+        const int32_t* pp[TP];
+#pragma unroll
+        for (int q = 0; q < TP; ++q) pp[q] = table + min(t * TP + q, pg_last);
+        int pg[TP];
+        sload_n<TP>(pp, pg);
+#pragma unroll
+        for (int i = 0; i < (NJ + WAVES - 1) / WAVES; ++i) {
+          const int j = wave + WAVES * i;
+          if (NJ % WAVES == 0 || i < NJ / WAVES || j < NJ) {
+            bool isk;
+            int key, chunk;
+            source(j, isk, key, chunk);
+            const int first = min((isk ? j : j - KJ) * (kPrefillKeys / (isk ? KJ : VJ)), last);
+            const int q = first / BS;  // wave-uniform
+            int page = pg[0];
+#pragma unroll
+            for (int qq = 1; qq < TP; ++qq) page = q == qq ? pg[qq] : page;
+            const char* base = (isk ? p.k_cache : p.v_cache) + (int64_t)page * p.c_sb + kvh * (isk ? p.c_sh : p.v_sh);
+            const uint32_t off = (uint32_t)((min(key, last) - q * BS) * (int)(isk ? p.c_st : p.v_st) + chunk * 16);
+            lds_dma16<false>(base, off, lds_addr(stage + 64 * 8 * j));  // tiles other query tiles read again
+          }
+        }
+        return;
+      }
       int64_t koff, voff;  // wave-uniform byte offsets of key kt of this kv head
       if (in_ctx) {
         koff = (int64_t)(cbase + kt) * p.cx_st + kvh * p.cx_sh;
         voff = (int64_t)(cbase + kt) * p.cv_st + kvh * p.cv_sh;
-      } else if (p.paged && TP == 1) {
+      } else if (p.paged) {
         const int pg = (int)p.bs.div(kt);
         if (pg != cached_pg) {
           cached_pg = pg;
@@ -318,38 +393,6 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
       } else {
         koff = (int64_t)(kbase + kt) * p.c_st + kvh * p.c_sh;
         voff = (int64_t)(kbase + kt) * p.v_st + kvh * p.v_sh;
-      }
-      if constexpr (TP > 1) {
-        // Pages of BS = 64 / TP keys: the tile's TP page numbers (clamped to the row's last page), loaded together
-        // through the scalar cache.
-        constexpr int BS = kPrefillKeys / TP;
-        const int pg_last = (lk - 1) / BS;
-        const int32_t* pp[TP];
-#pragma unroll
-        for (int q = 0; q < TP; ++q) pp[q] = table + min(t * TP + q, pg_last);
-        int pg[TP];
-        sload_n<TP>(pp, pg);
-        int64_t pb[TP];
-#pragma unroll
-        for (int q = 0; q < TP; ++q) pb[q] = (int64_t)pg[q] * p.c_sb;
-#pragma unroll
-        for (int i = 0; i < (NJ + WAVES - 1) / WAVES; ++i) {
-          const int j = wave + WAVES * i;
-          if (NJ % WAVES == 0 || i < NJ / WAVES || j < NJ) {
-            const bool isk = j < KJ;  // wave-uniform: a load of key rows, else of value rows
-            const int slot = 64 * (isk ? j : j - KJ) + lane;
-            const int kkey = slot / KJ, vkey = slot / VJ;
-            const uint32_t key = (uint32_t)min(isk ? kkey : vkey, last);  // last >= 0: the tile holds a key
-            const int chunk = isk ? min(slot - kkey * KJ, KCH - 1) : min(slot - vkey * VJ, VCH - 1);
-            int64_t b = pb[0];
-#pragma unroll
-            for (int q = 1; q < TP; ++q) b = key / BS == (uint32_t)q ? pb[q] : b;
-            const char* src = (isk ? p.k_cache : p.v_cache) + b + (int64_t)(key % BS) * (isk ? p.c_st : p.v_st) +
-                              kvh * (isk ? p.c_sh : p.v_sh) + chunk * 16;
-            lds_dma16<false>(src, lds_addr(stage + 64 * 8 * j));  // tiles other query tiles read again
-          }
-        }
-        return;
       }
       const char* kb = (in_ctx ? p.ctx_k : p.k_cache) + koff;
       const char* vb = (in_ctx ? p.ctx_v : p.v_cache) + voff;

@@ -363,7 +363,7 @@ constexpr int kRingOf = TP > 0 ? kPromptRing : 0;
 template <typename T, int D, int TP>
 __global__ __launch_bounds__(256, 2) void prompt_list_kernel(AttnParams p) {
   constexpr int RING = kRingOf<TP>;
-  __shared__ __attribute__((aligned(16))) char smem[(RING > 0 ? RING : 1) * PromptSmem<D, D>::kBytes];
+  __shared__ __attribute__((aligned(16))) char smem[(RING > 0 ? RING : 1) * PromptSmem<D, D, (TP > 1)>::kBytes];
   const int bx = blockIdx.x / p.hkv, kvh = blockIdx.x - bx * p.hkv;
   if (bx >= p.n_items[1]) return;
   const int2 it = p.items[bx];
@@ -378,7 +378,7 @@ constexpr int kOverlapLds = 84 * 1024;
 template <typename T, int D, int TP>
 __global__ __launch_bounds__(256, 2) void prompt_overlap_kernel(AttnParams p) {
   constexpr int RING = kRingOf<TP>;
-  __shared__ __attribute__((aligned(16))) char smem[(RING > 0 ? RING : 1) * PromptSmem<D, D>::kBytes];
+  __shared__ __attribute__((aligned(16))) char smem[(RING > 0 ? RING : 1) * PromptSmem<D, D, (TP > 1)>::kBytes];
   // The prompt tiles are the step's critical path beside the decode waves, which need few issue slots: the prompt
   // waves win the SIMD's issue arbitration (1% on the Qwen3-8B mixed step; favouring the decode waves costs 15%).
   __builtin_amdgcn_s_setprio(1);
@@ -399,8 +399,9 @@ __global__ __launch_bounds__(256, 2) void prompt_overlap_kernel(AttnParams p) {
 template <typename T, int D, int GS, int TP>
 __global__ __launch_bounds__(256, 2) void mixed_small_kernel(AttnParams p, int32_t prompt_wgs) {
   constexpr int RING = kRingOf<TP>;
-  static_assert(SmemBytes<D, GS>::kDecode <= (RING > 0 ? RING : 1) * PromptSmem<D, D>::kBytes, "LDS for both");
-  __shared__ __attribute__((aligned(16))) char smem[(RING > 0 ? RING : 1) * PromptSmem<D, D>::kBytes];
+  static_assert(SmemBytes<D, GS>::kDecode <= (RING > 0 ? RING : 1) * PromptSmem<D, D, (TP > 1)>::kBytes,
+                "LDS for both");
+  __shared__ __attribute__((aligned(16))) char smem[(RING > 0 ? RING : 1) * PromptSmem<D, D, (TP > 1)>::kBytes];
   const int b = blockIdx.x;
   if (b < prompt_wgs) {
     const int bx = b / p.hkv, kvh = b - bx * p.hkv;
@@ -720,7 +721,7 @@ static int launch(const AttnParams& p, bool listed, bool mixed, bool overlap, in
       launch_decode<T, D, GS, true>(p, s, kOverlapDecodeWgs, side->stream);
       LV_LAUNCH_CHECK("decode_persistent_kernel");
       LV_HIP_CHECK(hipEventRecord(side->join, side->stream));
-      constexpr int pad = std::max(0, kOverlapLds - std::max(1, kRingOf<TP>) * PromptSmem<D, D>::kBytes);
+      constexpr int pad = std::max(0, kOverlapLds - std::max(1, kRingOf<TP>) * PromptSmem<D, D, (TP > 1)>::kBytes);
       hipLaunchKernelGGL((prompt_overlap_kernel<T, D, TP>), dim3(grid), dim3(256), pad, stream, p);
       LV_LAUNCH_CHECK("prompt_overlap_kernel");
       LV_HIP_CHECK(hipStreamWaitEvent(stream, side->join, 0));

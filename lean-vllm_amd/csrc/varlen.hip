@@ -11,11 +11,11 @@
 namespace lv {
 
 // Keys are packed, so every 64-key tile is contiguous: tiles stream through an LDS ring. Up to 128-wide q.k two
-// 4-wave workgroups fit a CU; a 192-wide stage pair (88 KB of LDS) leaves room for one workgroup, which then takes 8
-// waves (256 query rows per item, two waves per SIMD, each staged tile serving twice the rows).
+// 4-wave workgroups fit a CU; the 192-wide tiles (an 88 KB stage pair) run one workgroup per CU of 8 waves (256
+// query rows per item, two waves per SIMD, each staged tile serving twice the rows).
 template <int DQK, int DV>
 struct VarlenCfg {
-  static constexpr int kPerCu = 2 * PromptSmem<DQK, DV>::kBytes <= 80 * 1024 ? 2 : 1;  // workgroups per CU
+  static constexpr int kPerCu = DQK <= 128 ? 2 : 1;  // workgroups per CU
   static constexpr int kRing = 2;  // a third stage for the one-per-CU tiles measured 6% slower
   static constexpr int kSmem = kRing * PromptSmem<DQK, DV>::kBytes;
   static constexpr int kWaves = kPerCu == 2 ? 4 : 8;        // waves per workgroup
