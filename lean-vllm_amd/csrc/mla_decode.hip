@@ -261,13 +261,14 @@ __global__ __launch_bounds__(256) void mla_decode_dma_kernel(MlaParams p) {
 // only where a row crosses a run boundary.
 //
 // Each stage's work (the score MFMAs, their exchange, the softmax, P.V) runs between two barriers of one
-// workgroup, so a CU streams faster with more workgroups than with deeper rings: three workgroups with a two-stage
-// ring (one stage in flight while one is consumed) beat two with a four-stage ring by 7% on DeepSeek-V2-Lite's step,
-// and one workgroup with five or eight stages is 40% slower.
+// workgroup. On DeepSeek-V2-Lite's step, two workgroups per CU with a two-stage ring (one stage in flight while one
+// is consumed) stream fastest. That is 5% faster than three per CU: their extra runs cut more units, and each cut
+// leaves partials to write and merge. It is 3% faster than two per CU with three stages. One workgroup with five or
+// eight stages is 40% slower.
 
 constexpr int kRunMin = 16;          // stages per run at least (256 latents)
 constexpr int kRunStages = 2;        // ring depth of a run
-constexpr int kRunsPerCU = 3;        // run workgroups per CU (three 2-stage rings fit a CU's 160 KB of LDS)
+constexpr int kRunsPerCU = 2;        // run workgroups per CU
 constexpr int kRunMaxUnits = 8192;   // units the in-kernel scan serves
 
 __device__ __forceinline__ int unit_latents(const MlaParams& p, int u) {
