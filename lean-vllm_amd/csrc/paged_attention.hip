@@ -26,7 +26,7 @@ constexpr int kPlanMaxRows = 4096;  // rows of a step with prompts (the work-lis
 constexpr int kPromptRing = 2;        // LDS stages of the prompt tiles' ring
 constexpr int kOverlapCusPct = 50;    // percent of the CUs that hold a prompt workgroup in a mixed step by default
 constexpr int kOverlapCusMaxPct = 75;  // at most this percent when the caller sizes the prompt share
-constexpr int kDecodeWgs = 3;         // persistent decode workgroups per CU outside the overlap
+constexpr int kDecodeWgs = 2;         // persistent decode workgroups per CU outside the overlap
 constexpr int kOverlapDecodeWgs = 2;  // persistent decode workgroups per CU beside a mixed step's prompt workgroups
 constexpr int kSplitTarget = 4096;    // decode items (x kv heads x query-head groups) a split-K grid aims for
 constexpr int kMinSplit = 256;        // keys per decode item at least
@@ -340,10 +340,10 @@ __device__ __forceinline__ void decode_persistent(const AttnParams& p) {
   }
 }
 
-// Alone on the GPU the grid holds three workgroups per CU (their waves within 168 registers). On the batch-256
-// Qwen3-8B decode step that is 3.6% faster than two per CU; on the 16-row long-context step, the same within 1%.
+// Alone on the GPU the grid holds two workgroups per CU, so their waves may take 256 registers (no spills; 1-2%
+// faster than under 128).
 template <typename T, int D, int GS>
-__global__ __launch_bounds__(256, 3) void decode_persistent_kernel(AttnParams p) {
+__global__ __launch_bounds__(256, 2) void decode_persistent_kernel(AttnParams p) {
   decode_persistent<T, D, GS>(p);
 }
 
