@@ -27,7 +27,7 @@ constexpr int kPromptRing = 2;        // LDS stages of the prompt tiles' ring
 constexpr int kOverlapCusPct = 50;    // percent of the CUs that hold a prompt workgroup in a mixed step by default
 constexpr int kOverlapCusMaxPct = 75;  // at most this percent when the caller sizes the prompt share
 constexpr int kDecodeWgs = 2;         // persistent decode workgroups per CU outside the overlap
-constexpr int kOverlapDecodeWgs = 2;  // persistent decode workgroups per CU beside a mixed step's prompt workgroups
+constexpr int kOverlapDecodeWgs = 3;  // persistent decode workgroups per CU beside a mixed step's prompt workgroups
 constexpr int kSplitTarget = 4096;    // decode items (x kv heads x query-head groups) a split-K grid aims for
 constexpr int kMinSplit = 256;        // keys per decode item at least
 constexpr int kSmallStepRounds = 8;   // a mixed step of at most this many GPU-fulls of workgroups is one launch
@@ -349,7 +349,7 @@ __global__ __launch_bounds__(256, 2) void decode_persistent_kernel(AttnParams p)
 
 // Beside a mixed step's prompt workgroups (one per CU, up to 192 registers per wave) two decode workgroups share
 // each SIMD's 512 registers per lane: at most 160 per wave. (The 128 that four workgroups per CU would leave spill
-// the D = 128 item.)
+// the D = 128 item.) The grid asks for three per CU: the CUs without a prompt workgroup take the third.
 template <typename T, int D, int GS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_num_vgpr(160))) void decode_beside_kernel(AttnParams p) {
   decode_persistent<T, D, GS>(p);
