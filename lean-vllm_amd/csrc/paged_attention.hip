@@ -25,7 +25,6 @@ constexpr int kPlanMaxRows = 4096;  // rows of a step with prompts (the work-lis
 
 constexpr int kPromptRing = 2;        // LDS stages of the prompt tiles' ring
 constexpr int kOverlapCusPct = 50;    // percent of the CUs that hold a prompt workgroup in a mixed step by default
-constexpr int kOverlapCusMinPct = 38;  // at least this percent when the caller sizes the prompt share
 constexpr int kOverlapCusMaxPct = 75;  // at most this percent when the caller sizes the prompt share
 constexpr int kDecodeWgs = 2;         // persistent decode workgroups per CU outside the overlap
 constexpr int kOverlapDecodeWgs = 3;  // persistent decode workgroups per CU beside a mixed step's prompt workgroups
@@ -669,15 +668,12 @@ static void launch_decode(const AttnParams& p, const Shape& s, int per_cu, hipSt
   }
 }
 
-// CUs that hold a prompt workgroup in an overlapped step: the caller's count clamped to [min, max] and rounded down
-// to a multiple of 8, or the default share for 0; never more than there are prompt items. (With the third decode
-// workgroup on every CU without a prompt workgroup, the Qwen3-8B mixed step runs fastest at the 44% its host
-// sizing asks for: 0.6% faster than at 50%.)
+// CUs that hold a prompt workgroup in an overlapped step: the caller's count clamped to [default, max] and
+// rounded down to a multiple of 8, or the default share for 0; never more than there are prompt items.
 static int prompt_grid(const Shape& s, const AttnParams& p, int requested) {
   const int cus = device_cus();
-  const int def = std::max(8, cus * kOverlapCusPct / 100 / 8 * 8);
-  const int lo = std::max(8, cus * kOverlapCusMinPct / 100 / 8 * 8), hi = std::max(def, cus * kOverlapCusMaxPct / 100);
-  const int n = requested > 0 ? std::min(hi, std::max(lo, requested / 8 * 8)) : def;
+  const int lo = std::max(8, cus * kOverlapCusPct / 100 / 8 * 8), hi = std::max(lo, cus * kOverlapCusMaxPct / 100);
+  const int n = requested > 0 ? std::min(hi, std::max(lo, requested / 8 * 8)) : lo;
   return std::min(s.max_prompt_items * p.hkv, n);
 }
 
