@@ -347,9 +347,11 @@ __global__ __launch_bounds__(256, 2) void decode_persistent_kernel(AttnParams p)
   decode_persistent<T, D, GS>(p);
 }
 
-// Beside a mixed step's prompt workgroups (one per CU, up to 192 registers per wave) two decode workgroups share
-// each SIMD's 512 registers per lane: at most 160 per wave. (The 128 that four workgroups per CU would leave spill
-// the D = 128 item.) The grid asks for three per CU: the CUs without a prompt workgroup take the third.
+// Beside a mixed step's prompt workgroups (one per CU) two decode workgroups share each SIMD's 512 registers per
+// lane. As compiled, a prompt wave takes 193 (allocated as 200) and a decode wave 131 (136): 472 in all. The cap
+// below keeps the decode waves off the 256 a lone workgroup could take; the compiler rounds it to an occupancy level
+// (three waves per SIMD, 168). The 128 of four workgroups per CU would spill the D = 128 item. The grid asks for
+// three per CU: the CUs without a prompt workgroup take the third.
 template <typename T, int D, int GS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_num_vgpr(160))) void decode_beside_kernel(AttnParams p) {
   decode_persistent<T, D, GS>(p);
