@@ -24,6 +24,12 @@ struct VarlenCfg {
 
 constexpr int kXcds = 8;  // workgroups are dealt round-robin over the XCDs by their linear index
 
+// XCDs that share one (kv head, row) group's query tiles: 1 when there are at least as many groups as XCDs, else
+// enough that every XCD gets a share (a group's tiles dealt every S-th to each of S virtual groups).
+__host__ __device__ inline int xcds_per_group(int groups) {
+  return groups >= kXcds ? 1 : (kXcds + groups - 1) / groups;
+}
+
 // Items (kv head, row, query tile) are dealt to the XCDs in contiguous ranges of (kv head, row) groups: the query
 // tiles of one (row, kv head), which read the same key and value tiles, share an L2 instead of fetching them once
 // per XCD. Workgroup b runs on XCD b % 8 and is that XCD's (b / 8)-th workgroup. Unmasked, every query tile of a row
@@ -32,19 +38,25 @@ constexpr int kXcds = 8;  // workgroups are dealt round-robin over the XCDs by t
 // tile t walks t + 1 tiles' worth of keys: the items go out by descending query tile, then group, so the long ones
 // start first and the short ones fill the tail (0.67x the time of group order on its 1536-token chunks). With
 // context keys (CTX) every query tile walks the whole context first: items go out group by group, as unmasked ones,
-// the longest query tile of each group first.
+// the longest query tile of each group first. With fewer groups than XCDs (a few rows of few kv heads), each group
+// is split into S = xcds_per_group virtual groups, every S-th query tile each, so that no XCD idles; each of the S
+// XCDs then reads the group's key and value tiles.
 template <typename T, int DQK, int DV, bool CTX>
 __global__ __launch_bounds__((64 * VarlenCfg<DQK, DV>::kWaves), (VarlenCfg<DQK, DV>::kPerCu)) void varlen_kernel(
     AttnParams p, int32_t qtiles) {
   using Cfg = VarlenCfg<DQK, DV>;
   __shared__ __attribute__((aligned(16))) char smem[Cfg::kSmem];
   const int groups = p.rows * p.hkv;  // (kv head, row) groups
+  const int S = xcds_per_group(groups);
+  const int vgroups = groups * S, nq = (qtiles + S - 1) / S;  // virtual groups and their query tiles
   const int x = blockIdx.x % kXcds, k = blockIdx.x / kXcds;
-  const int g0 = x * (groups / kXcds) + min(x, groups % kXcds);   // this XCD's first group
-  const int ng = groups / kXcds + (x < groups % kXcds ? 1 : 0);    // and its number of groups
-  if (k >= ng * qtiles) return;  // the grid is rounded up to whole XCD rounds
-  const int qt = CTX ? qtiles - 1 - k % qtiles : p.causal ? qtiles - 1 - k / ng : k % qtiles;
-  const int g = g0 + (CTX || !p.causal ? k / qtiles : k % ng);
+  const int v0 = x * (vgroups / kXcds) + min(x, vgroups % kXcds);  // this XCD's first virtual group
+  const int nv = vgroups / kXcds + (x < vgroups % kXcds ? 1 : 0);   // and its number of them
+  if (k >= nv * nq) return;  // the grid is rounded up to whole XCD rounds
+  const int qi = CTX ? nq - 1 - k % nq : p.causal ? nq - 1 - k / nv : k % nq;
+  const int v = v0 + (CTX || !p.causal ? k / nq : k % nv);
+  const int g = v / S, qt = v - g * S + S * qi;
+  if (qt >= qtiles) return;  // a virtual group's last tile past the row's (S does not divide qtiles)
   const int kvh = g / p.rows, row = g - kvh * p.rows;
   prefill_item<T, DQK, DV, true, false, Cfg::kRing, Cfg::kWaves, CTX>(p, row, qt, kvh, smem);
 }
@@ -63,9 +75,10 @@ static int64_t varlen_qtiles(int dqk, int dv, int group, int max_seqlen_q) {
 
 template <typename T, int DQK, int DV>
 static void launch_one(const AttnParams& p, int qtiles, hipStream_t st) {
-  // Each XCD gets a whole number of (kv head, row) groups: ceil(groups / 8) groups' items per XCD.
+  // Each XCD gets a whole number of virtual groups: ceil(virtual groups / 8) times their query tiles.
   const int64_t groups = (int64_t)p.rows * p.hkv;
-  const int64_t per_xcd = (groups + kXcds - 1) / kXcds * qtiles;
+  const int S = xcds_per_group((int)std::min<int64_t>(groups, kXcds));
+  const int64_t per_xcd = (groups * S + kXcds - 1) / kXcds * ((qtiles + S - 1) / S);
   const dim3 grid(per_xcd * kXcds), block(64 * VarlenCfg<DQK, DV>::kWaves);
   if (p.cu_ctx)
     hipLaunchKernelGGL((varlen_kernel<T, DQK, DV, true>), grid, block, 0, st, p, qtiles);
