@@ -439,12 +439,16 @@ __device__ inline int len_bucket(int keys, int split) {
 // Work list of a step, longest work first: prompt items (row, -1 - tile), then every full decode split (row, s),
 // then each decode row's last split (row, n - 1) by decreasing key count (counting sort over length buckets).
 // In-order dispatch of that list approximates longest-processing-time scheduling, so the launch ends with short
-// items instead of a tail of full ones.
+// items instead of a tail of full ones. A prompt row's tiles go last tile first (most keys) when the prompt items
+// have the GPU to themselves (last_first: a step of prompts, or the serial schedule): the Qwen3-8B chunks 5-6%
+// faster than first tile first. Beside the decode rows (the overlapped schedule) the order made no measurable
+// difference, and the first tile goes first there as before.
 __global__ __launch_bounds__(kScanThreads) void plan_kernel(const int32_t* __restrict__ cu_q,
                                                             const int32_t* __restrict__ lens_k,
                                                             const int32_t* __restrict__ cu_k, int32_t rows,
                                                             int32_t split, int32_t qp, int32_t max_items,
-                                                            int2* __restrict__ items, int32_t* __restrict__ n_items) {
+                                                            int32_t last_first, int2* __restrict__ items,
+                                                            int32_t* __restrict__ n_items) {
   __shared__ int pre[kPlanMaxRows + 1];
   __shared__ int full[kPlanMaxRows + 1];
   __shared__ int bucket[kLenBuckets + 1];
@@ -476,7 +480,7 @@ __global__ __launch_bounds__(kScanThreads) void plan_kernel(const int32_t* __res
   const int npre = pre[rows], nfull = full[rows], npart = bucket[kLenBuckets];
   for (int r = tid; r < rows; r += kScanThreads) {
     for (int i = pre[r]; i < pre[r + 1]; ++i)
-      if (i < max_items) items[i] = make_int2(r, -1 - (i - pre[r]));
+      if (i < max_items) items[i] = make_int2(r, -1 - (last_first ? pre[r + 1] - 1 - i : i - pre[r]));
     for (int i = full[r]; i < full[r + 1]; ++i)
       if (npre + i < max_items) items[npre + i] = make_int2(r, i - full[r]);
     const int lq = cu_q ? cu_q[r + 1] - cu_q[r] : 1;
@@ -824,11 +828,11 @@ struct PlanSig {
   const void* ws = nullptr;
   const int32_t *cu_q = nullptr, *lens = nullptr, *cu_k = nullptr;
   int64_t rows = 0, tokens = 0, max_k = 0, split = 0, qp = 0, max_items = 0, bytes = 0;
-  bool mixed = false;
+  bool mixed = false, last_first = false;
   bool operator==(const PlanSig& o) const {
     return ws == o.ws && cu_q == o.cu_q && lens == o.lens && cu_k == o.cu_k && rows == o.rows &&
            tokens == o.tokens && max_k == o.max_k && split == o.split && qp == o.qp && max_items == o.max_items &&
-           bytes == o.bytes && mixed == o.mixed;
+           bytes == o.bytes && mixed == o.mixed && last_first == o.last_first;
   }
 };
 constexpr int kPlanRecords = 32;
@@ -968,14 +972,15 @@ static int paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h
   sig.max_items = s.max_items;
   sig.bytes = (int64_t)s.bytes;
   sig.mixed = mixed;
-  if (listed && !plan_is_current(sig, (flags & LV_ATTN_REUSE_PLAN) != 0)) {
-    hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kScanThreads), 0, st, mixed ? cu_seqlens_q : nullptr, seqlens_k,
-                       cu_seqlens_k, num_rows, s.split, qp, s.max_items, reinterpret_cast<int2*>(ws + s.items_off),
-                       reinterpret_cast<int32_t*>(ws + s.count_off));
-    LV_LAUNCH_CHECK("plan_kernel");
-  }
   const bool overlap = schedule != LV_SCHEDULE_SERIAL;
   const bool prompts_only = (flags & LV_ATTN_PROMPTS_ONLY) != 0;
+  sig.last_first = prompts_only || !overlap;  // prompt items with the GPU to themselves: last tile first
+  if (listed && !plan_is_current(sig, (flags & LV_ATTN_REUSE_PLAN) != 0)) {
+    hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kScanThreads), 0, st, mixed ? cu_seqlens_q : nullptr, seqlens_k,
+                       cu_seqlens_k, num_rows, s.split, qp, s.max_items, (int32_t)sig.last_first,
+                       reinterpret_cast<int2*>(ws + s.items_off), reinterpret_cast<int32_t*>(ws + s.count_off));
+    LV_LAUNCH_CHECK("plan_kernel");
+  }
   const int rc =
       dtype == LV_DTYPE_BF16
           ? launch_d<BF16>(p, head_dim, s.gs, listed, mixed, overlap, prompt_workgroups, s, st, prompts_only)
