@@ -52,11 +52,17 @@ __device__ inline int key_len(const AttnParams& p, int row) {
 // per wave, as two 16-row MFMA blocks that share every K and V operand read) run against 64-key tiles staged
 // row-major in LDS, the next tile's K/V loads in flight in registers meanwhile. S^T = K Q^T and O^T += V^T P^T on
 // MFMA 16x16x32 with fp32 accumulation; the V^T operands come from the row-major value tile by the transposing
-// LDS read. Online softmax per query row with the scale folded into the exp2 argument; the running max is
-// replaced only when a tile raises it by more than kRescaleSlack (log2 units), so rescaling the accumulators is
-// rare and probabilities stay <= 2^kRescaleSlack. The causal mask (query j of a row with lq queries and lk keys
-// sees keys 0 .. lk - lq + j; none if p.causal is 0) is applied only on tiles that cross it.
-// DQK: q.k width; DV: value width.
+// LDS read. Online softmax per query row with the scale folded into the exp2 argument. The causal mask (query j of
+// a row with lq queries and lk keys sees keys 0 .. lk - lq + j; none if p.causal is 0) is applied only on tiles
+// that cross it. DQK: q.k width; DV: value width.
+// The row max, in at most two passes over the item's tiles:
+// - held (the first pass): taken from the item's first tile and held, so later tiles compute no max and never
+//   rescale. Every query row sees its first tile's keys (key 0, or the context keys, come first), so on ordinary
+//   data a row's first-tile max sits within a few log2 units of its final one. After the last tile every row sum
+//   must be finite and below kHeldLimit (all probabilities <= 2^kHeldSlack); otherwise (scores that rose far above
+//   a row's first tile, or non-finite ones) the workgroup makes the second pass;
+// - running (the second pass): replaced only when a tile raises it by more than kRescaleSlack (log2 units), so
+//   rescaling the accumulators is rare and probabilities stay <= 2^kRescaleSlack.
 
 // Stage tiles are row-major, laid out so that the operand reads (row = lane % 16, one 16-byte chunk per lane) and the
 // transposing value reads (rows 4 j4 + n / 4, 8 bytes per lane) meet no bank conflicts on gfx950. Its LDS (64 banks
@@ -157,12 +163,8 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
   const int nc = (lc + kPrefillKeys - 1) / kPrefillKeys;                  // context tiles
   const int ntiles = nc + (kmax + kPrefillKeys - 1) / kPrefillKeys;       // all tiles of the item
 
-  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};  // raw-score running max and row sums
+  float m[2], l[2];  // raw-score max (held or running) and row sums
   f32x4 o[2][DB];
-#pragma unroll
-  for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-    for (int b = 0; b < DB; ++b) o[nb][b] = f32x4{0, 0, 0, 0};
 
   // Staging: chunk i of this thread is key key_of(i) (a tile row), 16-byte part part_of(i).
   auto key_of = [&](int i) { return i < KPER ? (tid + NT * i) / KCH : (tid + NT * i - KCHUNKS) / VCH; };
@@ -226,8 +228,9 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
   }
 
   // One 64-key tile (keys kt .. kt + 63 of its source) from the K/V tile in LDS at ks / vs: scores, mask (query row
-  // nb sees keys < l[nb]), online softmax, P.V.
-  auto consume = [&](int kt, const int (&lm)[2], const uint16_t* ks, const uint16_t* vs) {
+  // nb sees keys < l[nb]), online softmax, P.V. first: the item's first tile; running: the second pass (both
+  // wave-uniform).
+  auto consume = [&](int kt, const int (&lm)[2], const uint16_t* ks, const uint16_t* vs, bool first, bool running) {
     // S^T (keys x query rows): st[kb][nb] lane holds keys kt + 16 kb + 4 j4 + r of query row (nb, n).
     f32x4 st[4][2];
 #pragma unroll
@@ -254,26 +257,33 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
           for (int nb = 0; nb < 2; ++nb) st[kb][nb][r] = key < lm[nb] ? st[kb][nb][r] : -INFINITY;
         }
     }
-    float mx[2];
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      float x = -INFINITY;
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-        x = vmax(x, vmax(vmax(st[kb][nb][0], st[kb][nb][1]), vmax(st[kb][nb][2], st[kb][nb][3])));
-      mx[nb] = xor32_max(xor16_max(x));  // over the row's 64 keys of this tile
-    }
-    const bool grow = (mx[0] > m[0] && (m[0] == -INFINITY || (mx[0] - m[0]) * c > kRescaleSlack)) ||
-                      (mx[1] > m[1] && (m[1] == -INFINITY || (mx[1] - m[1]) * c > kRescaleSlack));
-    if (__any(grow)) {
+    if (first || running) {  // held: only the first tile takes a max
+      float mx[2];
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
-        const float mn = vmax(m[nb], mx[nb]);
-        const float alpha = m[nb] == -INFINITY ? 0.f : fast_exp2((m[nb] - mn) * c);
-        m[nb] = mn;
-        l[nb] *= alpha;
+        float x = -INFINITY;
 #pragma unroll
-        for (int b = 0; b < DB; ++b) o[nb][b] *= alpha;
+        for (int kb = 0; kb < 4; ++kb)
+          x = vmax(x, vmax(vmax(st[kb][nb][0], st[kb][nb][1]), vmax(st[kb][nb][2], st[kb][nb][3])));
+        mx[nb] = xor32_max(xor16_max(x));  // over the row's 64 keys of this tile
+      }
+      if (!running) {  // the held max: nothing is accumulated yet
+        m[0] = mx[0];
+        m[1] = mx[1];
+      } else {
+        const bool grow = (mx[0] > m[0] && (m[0] == -INFINITY || (mx[0] - m[0]) * c > kRescaleSlack)) ||
+                          (mx[1] > m[1] && (m[1] == -INFINITY || (mx[1] - m[1]) * c > kRescaleSlack));
+        if (__any(grow)) {
+#pragma unroll
+          for (int nb = 0; nb < 2; ++nb) {
+            const float mn = vmax(m[nb], mx[nb]);
+            const float alpha = m[nb] == -INFINITY ? 0.f : fast_exp2((m[nb] - mn) * c);
+            m[nb] = mn;
+            l[nb] *= alpha;
+#pragma unroll
+            for (int b = 0; b < DB; ++b) o[nb][b] *= alpha;
+          }
+        }
       }
     }
     // P^T operands: k slots 8 j4 .. 8 j4 + 7 = keys 32 h + 4 j4 + 0..3, then 32 h + 16 + 4 j4 + 0..3.
@@ -312,6 +322,16 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
       }
   };
 
+  // A pass over the item's tiles, with the held max (RUNNING false) or the running one.
+  auto run_pass = [&](auto running_tag) {
+  constexpr bool running = decltype(running_tag)::value;
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+    m[nb] = -INFINITY;
+    l[nb] = 0.f;
+#pragma unroll
+    for (int b = 0; b < DB; ++b) o[nb][b] = f32x4{0, 0, 0, 0};
+  }
   if constexpr (RING > 0) {
     // Stage layout: 64 key rows of KJ 16-byte slots, then 64 value rows of VJ (KCH / VCH chunks, plus two pad slots
     // in the padded layout, which hold copies of the row's last chunk). 64-lane load j covers slots 64 j .. 64 j + 63
@@ -435,7 +455,7 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
       const uint16_t* ks = ring + (it % RING) * kStageElems;
       const bool in_ctx = CTX && it < nc;  // a context tile: every query sees its keys < lc
       const int lcur[2] = {in_ctx ? lc : lim[0], in_ctx ? lc : lim[1]};
-      consume((in_ctx ? it : it - nc) * kPrefillKeys, lcur, ks, ks + kPrefillKeys * KROW);
+      consume((in_ctx ? it : it - nc) * kPrefillKeys, lcur, ks, ks + kPrefillKeys * KROW, it == 0, running);
     }
   } else {
     uint16_t* ks = reinterpret_cast<uint16_t*>(smem);  // [64 keys][KROW]
@@ -448,8 +468,24 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
       stash(ks, vs, stage);
       __syncthreads();
       if (PREFETCH && kt + kPrefillKeys < kmax) fetch(kt + kPrefillKeys, stage);
-      consume(kt, lim, ks, vs);
+      consume(kt, lim, ks, vs, kt == 0, running);
     }
+  }
+  };
+  // The held pass, for one-page and multi-page LDS rings of up to 128-wide values in 4-wave items; the register-staged
+  // tiles (other page sizes) and 192-wide values have no registers to spare for it, and 8-wave items (MLA prefill)
+  // measured 4% slower with it. Those make one running pass.
+  constexpr bool kHeld = RING > 0 && DV <= 128 && WAVES == 4;
+  if constexpr (kHeld) {
+    run_pass(std::false_type{});
+    bool held = true;
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)  // false for a NaN sum
+      held = held && (!qvalid[nb] || xor32_sum(xor16_sum(l[nb])) < kHeldLimit);
+    // Every wave has consumed its last tile here, so the stages are free for a second pass.
+    if (__syncthreads_or(!held)) run_pass(std::true_type{});
+  } else {
+    run_pass(std::true_type{});
   }
 
 #pragma unroll

@@ -517,3 +517,34 @@ def test_layers_of_one_step_share_one_plan(cuda, kind, monkeypatch):
         torch.cuda.synchronize()
         for i, (x, y) in enumerate(zip(outs, eager)):
             assert torch.equal(x, y), f"replay {rep} layer {i}"
+
+
+@pytest.mark.parametrize("bs", [16, 64, 256])
+def test_scores_far_above_the_first_tile(case, bs, monkeypatch):
+    """Prompt tiles take a row's max from the item's first key tile and hold it; when later keys score far above it
+    (here keys 64 onward scaled 40x, some 200 log2 units higher), the item's row sums fail their check and the
+    workgroup runs the item again with a running max. Cold prompts whose queries past 64 see the scaled keys, next
+    to a row whose keys stay unscaled, under both launch schedules, against the fp32 oracle."""
+    from lvattn import backend as B
+
+    b, dtype, dim, dev = case
+    cached, new = [0, 0, 0], [200, 130, 70]
+    need = [-(-(c + n) // bs) for c, n in zip(cached, new)]
+    width = max(need)
+    tables, at = [], 0
+    for k in need:
+        tables.append(list(range(at, at + k)) + [-1] * (width - k))
+        at += k
+    qs, kf, vf, kn, vn, kc, vc, slots = paged_step(cached, new, tables, at + 1, heads=H, kv_heads=HKV, dim=dim,
+                                                   bs=bs, device=dev, dtype=dtype)
+    for i in (0, 1):
+        kf[i][64:] *= 40
+    kn = torch.cat(kf)
+    b.store_kvcache(kn, vn, kc, vc, slots)
+    want = dense_expected(qs, kf, vf, SCALE)
+    for sched in (B.SCHEDULE_SERIAL, B.SCHEDULE_OVERLAP):
+        monkeypatch.setattr(b, "_schedule", lambda context, elem_bytes, s=sched: s)
+        out = b.forward(torch.cat(qs), kn, vn, kc, vc, context_for(cached, new, tables, dev))
+        torch.cuda.synchronize()
+        assert torch.isfinite(out).all()
+        check(out, want, dtype)

@@ -268,3 +268,25 @@ def test_prefill_with_context_writes_into_a_strided_out(cuda):
     want = b.prefill_with_context(q, k, v, kc, vc, cu_q, cu_c, max(lens_q))
     torch.cuda.synchronize()
     assert torch.equal(wide[..., :vd], want) and (wide[..., vd:] == 3.0).all()
+
+
+@pytest.mark.parametrize("causal", [True, False], ids=["causal", "unmasked"])
+@pytest.mark.parametrize("dtype, dim", CASES, ids=IDS)
+def test_scores_far_above_the_first_tile(cuda, dtype, dim, causal):
+    """Keys from 64 onward scaled 40x: the held max of the item's first tile fails its check and the item runs
+    again with a running max. Output and log-sum-exp against the fp32 oracle."""
+    gen = torch.Generator().manual_seed(2)
+    lens_q = [150, 3, 90]
+    lens_k = lens_q if causal else [170, 80, 200]
+    qs = [rnd(n, H, dim, gen=gen, dtype=dtype, device=cuda) for n in lens_q]
+    ks = [rnd(n, HKV, dim, gen=gen, dtype=dtype, device=cuda) for n in lens_k]
+    vs = [rnd(n, HKV, dim, gen=gen, dtype=dtype, device=cuda) for n in lens_k]
+    for k in ks:
+        k[64:] *= 40
+    out, lse = MI355XAttention(H, dim, SCALE, HKV).varlen_with_lse(
+        torch.cat(qs), torch.cat(ks), torch.cat(vs), cumulative(lens_q, cuda), cumulative(lens_k, cuda),
+        max(lens_q), max(lens_k), causal)
+    want, want_lse = dense_rows(qs, ks, vs, causal)
+    assert torch.isfinite(out).all() and torch.isfinite(lse).all()
+    torch.testing.assert_close(out.float().cpu(), want, **TOL[dtype])
+    torch.testing.assert_close(lse.cpu(), want_lse, rtol=1e-4, atol=1e-4)
