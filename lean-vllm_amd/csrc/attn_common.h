@@ -472,10 +472,11 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
     }
   }
   };
-  // The held pass, for one-page and multi-page LDS rings of up to 128-wide values in 4-wave items; the register-staged
-  // tiles (other page sizes) and 192-wide values have no registers to spare for it, and 8-wave items (MLA prefill)
-  // measured 4% slower with it. Those make one running pass.
-  constexpr bool kHeld = RING > 0 && DV <= 128 && WAVES == 4;
+  // The held pass, for one-page and multi-page LDS rings of up to 128-wide values; the register-staged tiles (other
+  // page sizes) and 192-wide values have no registers to spare for it, and 8-wave items over context keys (MLA
+  // prefill in one call) measured 2.4% slower with it (without context keys, as the reference layer's two calls
+  // run, 7.8% faster). Those make one running pass.
+  constexpr bool kHeld = RING > 0 && DV <= 128 && (WAVES == 4 || !CTX);
   if constexpr (kHeld) {
     run_pass(std::false_type{});
     bool held = true;

@@ -290,3 +290,25 @@ def test_scores_far_above_the_first_tile(cuda, dtype, dim, causal):
     assert torch.isfinite(out).all() and torch.isfinite(lse).all()
     torch.testing.assert_close(out.float().cpu(), want, **TOL[dtype])
     torch.testing.assert_close(lse.cpu(), want_lse, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("causal", [True, False], ids=["causal", "unmasked"])
+def test_scores_far_above_the_first_tile_mla_widths(cuda, causal):
+    """The same for MLA prefill's expanded heads (q.k 192, values 128 as a view), which run 8-wave items: keys from 64
+    onward scaled 40x, so the held max fails its check and the item runs again with a running max."""
+    dtype, heads, qk, vd = torch.bfloat16, 16, 192, 128
+    gen = torch.Generator().manual_seed(3)
+    lens_q = [300, 5, 140]
+    lens_k = lens_q if causal else [310, 90, 150]
+    q = rnd(sum(lens_q), heads, qk, gen=gen, dtype=dtype, device=cuda)
+    k = rnd(sum(lens_k), heads, qk, gen=gen, dtype=dtype, device=cuda)
+    v = rnd(sum(lens_k), heads, qk, gen=gen, dtype=dtype, device=cuda)[..., :vd]
+    ks = list(torch.split(k, lens_k))
+    for kr in ks:
+        kr[64:] *= 40
+    out, lse = MI355XAttention(heads, qk, SCALE, heads).varlen_with_lse(
+        q, k, v, cumulative(lens_q, cuda), cumulative(lens_k, cuda), max(lens_q), max(lens_k), causal)
+    want, want_lse = dense_rows(list(torch.split(q, lens_q)), ks, list(torch.split(v, lens_k)), causal)
+    assert torch.isfinite(out).all() and torch.isfinite(lse).all()
+    torch.testing.assert_close(out.float().cpu(), want, **TOL[dtype])
+    torch.testing.assert_close(lse.cpu(), want_lse, rtol=1e-4, atol=1e-4)
