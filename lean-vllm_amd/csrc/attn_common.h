@@ -56,8 +56,8 @@ __device__ inline int key_len(const AttnParams& p, int row) {
 // a row with lq queries and lk keys sees keys 0 .. lk - lq + j; none if p.causal is 0) is applied only on tiles
 // that cross it. DQK: q.k width; DV: value width.
 // The row max, in at most two passes over the item's tiles:
-// - held (the first pass): taken from the item's first tile and held, so later tiles compute no max and never
-//   rescale. Every query row sees its first tile's keys (key 0, or the context keys, come first), so on ordinary
+// - held (the first pass; bf16 only, whose P operands hold the fp32 range): taken from the item's first tile and
+//   held, so later tiles compute no max and never rescale. Every query row sees its first tile's keys (key 0, or the context keys, come first), so on ordinary
 //   data a row's first-tile max sits within a few log2 units of its final one. After the last tile every row sum
 //   must be finite and below kHeldLimit (all probabilities <= 2^kHeldSlack); otherwise (scores that rose far above
 //   a row's first tile, or non-finite ones) the workgroup makes the second pass;
@@ -472,11 +472,12 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
     }
   }
   };
-  // The held pass, for one-page and multi-page LDS rings of up to 128-wide values; the register-staged tiles (other
-  // page sizes) and 192-wide values have no registers to spare for it, and 8-wave items over context keys (MLA
-  // prefill in one call) measured 2.4% slower with it (without context keys, as the reference layer's two calls
-  // run, 7.8% faster). Those make one running pass.
-  constexpr bool kHeld = RING > 0 && DV <= 128 && (WAVES == 4 || !CTX);
+  // The held pass, for bf16 on one-page and multi-page LDS rings of up to 128-wide values. fp16 P operands overflow
+  // past 65504 (2^16), far below the 2^64 that the row sums bound; the register-staged tiles (other page sizes) and
+  // 192-wide values have no registers to spare for it; 8-wave items over context keys (MLA prefill in one call)
+  // measured 2.4% slower with it (without context keys, as the reference layer's two calls run, 7.8% faster). Those
+  // make one running pass.
+  constexpr bool kHeld = std::is_same<T, BF16>::value && RING > 0 && DV <= 128 && (WAVES == 4 || !CTX);
   if constexpr (kHeld) {
     run_pass(std::false_type{});
     bool held = true;

@@ -263,7 +263,8 @@ constexpr float kLog2e = 1.4426950408889634f;
 // rescaled: probabilities then stay below 2^kRescaleSlack, well inside bf16 / fp16 and fp32 range.
 constexpr float kRescaleSlack = 8.f;
 // An online softmax may instead hold a row's max from its first key tile: later scores up to kHeldSlack log2 units
-// above it give probabilities up to 2^kHeldSlack, exact in fp32 and in 16-bit P operands. A row sum below
+// above it give probabilities up to 2^kHeldSlack, exact in fp32 and in bf16 P operands (not fp16, whose range ends
+// at 65504). A row sum below
 // kHeldLimit (= 2^kHeldSlack, finite) shows that every probability of the row stayed in that range.
 constexpr float kHeldSlack = 64.f;
 constexpr float kHeldLimit = 18446744073709551616.f;

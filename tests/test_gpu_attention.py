@@ -519,12 +519,15 @@ def test_layers_of_one_step_share_one_plan(cuda, kind, monkeypatch):
             assert torch.equal(x, y), f"replay {rep} layer {i}"
 
 
+@pytest.mark.parametrize("factor", [6, 40])
 @pytest.mark.parametrize("bs", [16, 64, 256])
-def test_scores_far_above_the_first_tile(case, bs, monkeypatch):
-    """Prompt tiles take a row's max from the item's first key tile and hold it; when later keys score far above it
-    (here keys 64 onward scaled 40x, some 200 log2 units higher), the item's row sums fail their check and the
-    workgroup runs the item again with a running max. Cold prompts whose queries past 64 see the scaled keys, next
-    to a row whose keys stay unscaled, under both launch schedules, against the fp32 oracle."""
+def test_scores_far_above_the_first_tile(case, bs, factor, monkeypatch):
+    """bf16 prompt tiles take a row's max from the item's first key tile and hold it; when later keys score far
+    above it (keys 64 onward scaled 40x, some 200 log2 units higher), the item's row sums fail their check and the
+    workgroup runs the item again with a running max. Scaled 6x (some 20-30 units higher) the held max stands: the
+    probabilities reach 2^30, which bf16 P holds; fp16, whose P would overflow there, keeps the running max. Cold
+    prompts whose queries past 64 see the scaled keys, next to a row whose keys stay unscaled, under both launch
+    schedules, against the fp32 oracle."""
     from lvattn import backend as B
 
     b, dtype, dim, dev = case
@@ -538,7 +541,7 @@ def test_scores_far_above_the_first_tile(case, bs, monkeypatch):
     qs, kf, vf, kn, vn, kc, vc, slots = paged_step(cached, new, tables, at + 1, heads=H, kv_heads=HKV, dim=dim,
                                                    bs=bs, device=dev, dtype=dtype)
     for i in (0, 1):
-        kf[i][64:] *= 40
+        kf[i][64:] *= factor
     kn = torch.cat(kf)
     b.store_kvcache(kn, vn, kc, vc, slots)
     want = dense_expected(qs, kf, vf, SCALE)

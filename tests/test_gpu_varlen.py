@@ -270,11 +270,13 @@ def test_prefill_with_context_writes_into_a_strided_out(cuda):
     assert torch.equal(wide[..., :vd], want) and (wide[..., vd:] == 3.0).all()
 
 
+@pytest.mark.parametrize("factor", [6, 40])
 @pytest.mark.parametrize("causal", [True, False], ids=["causal", "unmasked"])
 @pytest.mark.parametrize("dtype, dim", CASES, ids=IDS)
-def test_scores_far_above_the_first_tile(cuda, dtype, dim, causal):
+def test_scores_far_above_the_first_tile(cuda, dtype, dim, causal, factor):
     """Keys from 64 onward scaled 40x: the held max of the item's first tile fails its check and the item runs
-    again with a running max. Output and log-sum-exp against the fp32 oracle."""
+    again with a running max. Scaled 6x, some 20-30 log2 units higher: the held max stands in bf16 (P up to 2^30)
+    and fp16 keeps the running max (its P would overflow). Output and log-sum-exp against the fp32 oracle."""
     gen = torch.Generator().manual_seed(2)
     lens_q = [150, 3, 90]
     lens_k = lens_q if causal else [170, 80, 200]
@@ -282,7 +284,7 @@ def test_scores_far_above_the_first_tile(cuda, dtype, dim, causal):
     ks = [rnd(n, HKV, dim, gen=gen, dtype=dtype, device=cuda) for n in lens_k]
     vs = [rnd(n, HKV, dim, gen=gen, dtype=dtype, device=cuda) for n in lens_k]
     for k in ks:
-        k[64:] *= 40
+        k[64:] *= factor
     out, lse = MI355XAttention(H, dim, SCALE, HKV).varlen_with_lse(
         torch.cat(qs), torch.cat(ks), torch.cat(vs), cumulative(lens_q, cuda), cumulative(lens_k, cuda),
         max(lens_q), max(lens_k), causal)
