@@ -480,10 +480,18 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
   constexpr bool kHeld = std::is_same<T, BF16>::value && RING > 0 && DV <= 128 && (WAVES == 4 || !CTX);
   if constexpr (kHeld) {
     run_pass(std::false_type{});
+    // Held rows: every sum finite and below kHeldLimit (false for a NaN sum), and every accumulator finite (a value
+    // of magnitude past 2^63 times a probability near 2^64 would overflow where the running max does not).
     bool held = true;
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb)  // false for a NaN sum
-      held = held && (!qvalid[nb] || xor32_sum(xor16_sum(l[nb])) < kHeldLimit);
+    for (int nb = 0; nb < 2; ++nb) {
+      bool fin = true;
+#pragma unroll
+      for (int b = 0; b < DB; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) fin = fin && __builtin_isfinite(o[nb][b][r]);
+      held = held && (!qvalid[nb] || (xor32_sum(xor16_sum(l[nb])) < kHeldLimit && fin));
+    }
     // Every wave has consumed its last tile here, so the stages are free for a second pass.
     if (__syncthreads_or(!held)) run_pass(std::true_type{});
   } else {

@@ -551,3 +551,33 @@ def test_scores_far_above_the_first_tile(case, bs, factor, monkeypatch):
         torch.cuda.synchronize()
         assert torch.isfinite(out).all()
         check(out, want, dtype)
+
+
+@pytest.mark.parametrize("dim", [64, 128])
+def test_huge_values_with_scores_above_the_first_tile(cuda, dim):
+    """bf16 values near 2^100 and keys from 64 onward scaled 9x (some 35-50 log2 units above the first tile): the held
+    max's row sums stay below their bound, but its accumulators (probabilities near 2^45 times the values) overflow,
+    where the fp32 oracle's do not. The accumulator check sends the item to the running max."""
+    dtype, bs = torch.bfloat16, 64
+    b = MI355XAttention(H, dim, SCALE, HKV)
+    cached, new = [0, 0], [200, 130]
+    need = [-(-(c + n) // bs) for c, n in zip(cached, new)]
+    width = max(need)
+    tables, at = [], 0
+    for k in need:
+        tables.append(list(range(at, at + k)) + [-1] * (width - k))
+        at += k
+    qs, kf, vf, kn, vn, kc, vc, slots = paged_step(cached, new, tables, at + 1, heads=H, kv_heads=HKV, dim=dim,
+                                                   bs=bs, device=cuda, dtype=dtype)
+    for i in (0, 1):
+        kf[i][64:] *= 9
+        vf[i] *= 2.0 ** 100
+    kn, vn = torch.cat(kf), torch.cat(vf)
+    b.store_kvcache(kn, vn, kc, vc, slots)
+    want = dense_expected(qs, kf, vf, SCALE)
+    assert torch.isfinite(want).all()
+    out = b.forward(torch.cat(qs), kn, vn, kc, vc, context_for(cached, new, tables, cuda))
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    # The path's bf16 bar (2e-2 absolute, 1e-2 relative) at the values' scale.
+    torch.testing.assert_close(out.float().cpu(), want.float(), atol=2e-2 * 2.0 ** 100, rtol=1e-2)
