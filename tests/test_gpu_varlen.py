@@ -294,10 +294,12 @@ def test_scores_far_above_the_first_tile(cuda, dtype, dim, causal, factor):
     torch.testing.assert_close(lse.cpu(), want_lse, rtol=1e-4, atol=1e-4)
 
 
+@pytest.mark.parametrize("factor", [6, 40])
 @pytest.mark.parametrize("causal", [True, False], ids=["causal", "unmasked"])
-def test_scores_far_above_the_first_tile_mla_widths(cuda, causal):
+def test_scores_far_above_the_first_tile_mla_widths(cuda, causal, factor):
     """The same for MLA prefill's expanded heads (q.k 192, values 128 as a view), which run 8-wave items: keys from 64
-    onward scaled 40x, so the held max fails its check and the item runs again with a running max."""
+    onward scaled 40x, so the held max fails its check and the item runs again with a running max, or 6x, so that
+    the held max stands with probabilities up to about 2^30."""
     dtype, heads, qk, vd = torch.bfloat16, 16, 192, 128
     gen = torch.Generator().manual_seed(3)
     lens_q = [300, 5, 140]
@@ -307,7 +309,7 @@ def test_scores_far_above_the_first_tile_mla_widths(cuda, causal):
     v = rnd(sum(lens_k), heads, qk, gen=gen, dtype=dtype, device=cuda)[..., :vd]
     ks = list(torch.split(k, lens_k))
     for kr in ks:
-        kr[64:] *= 40
+        kr[64:] *= factor
     out, lse = MI355XAttention(heads, qk, SCALE, heads).varlen_with_lse(
         q, k, v, cumulative(lens_q, cuda), cumulative(lens_k, cuda), max(lens_q), max(lens_k), causal)
     want, want_lse = dense_rows(list(torch.split(q, lens_q)), ks, list(torch.split(v, lens_k)), causal)
