@@ -113,8 +113,8 @@ int lv_store_latents(const void* latent, int64_t latent_stride_t, int32_t num_to
  * prompt tiles on the whole GPU, then the decode rows -- the faster choice when the decode rows' bytes take less
  * time than the prompt tiles' MFMA work (e.g. a step of prompts only). LV_SCHEDULE_AUTO overlaps. The result is
  * the same either way.
- * prompt_workgroups (overlap only): how many CUs run a prompt workgroup beside the decode rows; 0 picks half of
- * them. Other values are clamped to [half, three quarters] of the CUs and rounded down to a multiple of 8 (each
+ * prompt_workgroups (overlap only): how many CUs run a prompt workgroup beside the decode rows; 0 picks 44% of
+ * them. Other values are clamped to [44%, three quarters] of the CUs and rounded down to a multiple of 8 (each
  * kv head's prompt items then stay on one XCD). A step heavy in prompt tiles ends sooner with more.
  * flags: 0, or LV_ATTN_REUSE_PLAN for the later layers of a step: the workspace already holds the work list a previous
  * call planned for this step (the same rows, lengths, shape and max_seqlen_k, through the same cu_seqlens_q /

@@ -24,7 +24,7 @@ constexpr int kWaves = 4;          // waves per workgroup
 constexpr int kPlanMaxRows = 4096;  // rows of a step with prompts (the work-list scan lives in LDS)
 
 constexpr int kPromptRing = 2;        // LDS stages of the prompt tiles' ring
-constexpr int kOverlapCusPct = 50;    // percent of the CUs that hold a prompt workgroup in a mixed step by default
+constexpr int kOverlapCusPct = 44;    // percent of the CUs that hold a prompt workgroup in a mixed step by default
 constexpr int kOverlapCusMaxPct = 75;  // at most this percent when the caller sizes the prompt share
 constexpr int kDecodeWgs = 2;         // persistent decode workgroups per CU outside the overlap
 constexpr int kOverlapDecodeWgs = 3;  // persistent decode workgroups per CU beside a mixed step's prompt workgroups

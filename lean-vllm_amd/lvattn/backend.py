@@ -66,7 +66,7 @@ DECODE_BYTES_PER_S = 6.6e12
 PROMPT_FLOPS_PER_S = 1 / (1 / 1.8e14 - 1 / 8.4e14)  # 2.3e14
 # One overlapped prompt workgroup (one per CU) runs about 1.3-1.4 TFLOP/s of prompt tiles beside the decode rows. An
 # overlapped step asks for enough of them that the prompt tiles end with the decode rows; the library keeps the
-# count between half and three quarters of the CUs.
+# count between 44% and three quarters of the CUs.
 PROMPT_WORKGROUP_FLOPS_PER_S = 1.3e12
 
 
