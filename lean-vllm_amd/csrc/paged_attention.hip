@@ -1,11 +1,12 @@
 // Paged attention for a continuous-batching step on gfx950: pure decode, chunked prefill, or both in one launch.
 //
 // Work items (one workgroup of 4 waves each):
-//   decode item  = (row, split, kv head, query-head group): a row with one query, keys [split*S, (split+1)*S).
-//                  Streaming, bandwidth-bound: each wave takes every 4th 16-token tile of the range; a token's
-//                  head row (D elements) is spread over 16 lanes as 16-byte loads; q.k by v_dot2 with a DPP
-//                  butterfly inside the 16-lane row; online softmax per tile; p.v on the VALU in fp32. The four
-//                  waves and, for long rows, the splits are merged by log-sum-exp.
+//   decode item  = (row, split, kv head or pair of kv heads, query-head group): a row with one query, keys
+//                  [split*S, (split+1)*S). Streaming, bandwidth-bound: each wave takes every 4th tile of the
+//                  range; a token's head row (D elements) is spread over 16 lanes as 16-byte loads (the two head
+//                  rows of a pair, adjacent in the cache, over 32); q.k by v_dot2 with a DPP butterfly inside the
+//                  16-lane row; online softmax per tile; p.v on the VALU in fp32. The four waves and, for long
+//                  rows, the splits are merged by log-sum-exp.
 //   prompt item  = (row, q tile, kv head): a row with several queries; the MFMA tile of attn_common.h.
 // Launches read a work list built on the device by plan_kernel from the key lengths (and cu_seqlens_q), longest
 // work first. Rows whose keys were split are combined by splitk_merge_kernel.
@@ -35,40 +36,48 @@ constexpr int kSmallStepRounds = 8;   // a mixed step of at most this many GPU-f
 // ---------------------------------------------------------------------------------------------------------
 // Decode item.
 //
-// Lane layout (D = 128): 16 lanes hold one token's head row, 16 bytes (8 dims) each; the wave's 4 lane groups take
-// 4 tokens at a time, 4 times per 16-token tile. Scores stay in raw q.k units; the softmax scale (positive) and
-// log2(e) are folded into the exp2 argument. The running max is wave-uniform, so rescaling the accumulators is a
-// uniform branch taken only when a tile raises the max. p.v runs as 2-term dot products over token pairs with p in
+// Lane layout (D = 128): 16 lanes hold one token's head row, 16 bytes (8 dims) each. With one kv head per item
+// (HP = 1) the wave's 4 lane groups take 4 tokens at a time, 4 times per 16-token tile; with a pair (HP = 2) lanes
+// 0-31 take one token's two head rows (512 contiguous bytes of an NHD token row) and lanes 32-63 the next token's.
+// Scores stay in raw q.k units; the softmax scale (positive) and log2(e) are folded into the exp2 argument. The
+// running max is uniform over the lanes of a head, so rescaling the accumulators is a branch taken only when a
+// tile raises some head's max. p.v runs as 2-term dot products over token pairs with p in
 // the 16-bit format of the cache (fp32 accumulation), as the MFMA path does with its probability tiles.
 
-// Reduce over the lane groups of a wave that hold different tokens (lanes i, i + LPT, i + 2 LPT, ...).
-template <int LPT>
+// Reduce over the lane groups of a wave that hold different tokens of one head (lanes i, i + LPH, i + 2 LPH, ...;
+// LPH lanes hold a token's piece of the item's head rows).
+template <int LPH>
 __device__ inline float groups_max(float x) {
-  static_assert(LPT == 8 || LPT == 16, "8 or 16 lanes per token");
-  if constexpr (LPT == 8) x = vmax(x, dpp_ror8(x));  // lanes i and i ^ 8 of each 16-lane row
-  return xor32_max(xor16_max(x));
+  static_assert(LPH == 8 || LPH == 16 || LPH == 32, "8, 16 or 32 lanes per token piece");
+  if constexpr (LPH == 8) x = vmax(x, dpp_ror8(x));  // lanes i and i ^ 8 of each 16-lane row
+  if constexpr (LPH <= 16) x = xor16_max(x);
+  return xor32_max(x);
 }
-template <int LPT>
+template <int LPH>
 __device__ inline float groups_sum(float x) {
-  static_assert(LPT == 8 || LPT == 16, "8 or 16 lanes per token");
-  if constexpr (LPT == 8) x += dpp_ror8(x);
-  return xor32_sum(xor16_sum(x));
+  static_assert(LPH == 8 || LPH == 16 || LPH == 32, "8, 16 or 32 lanes per token piece");
+  if constexpr (LPH == 8) x += dpp_ror8(x);
+  if constexpr (LPH <= 16) x = xor16_sum(x);
+  return xor32_sum(x);
 }
 
 // publish (persistent launches): thread 0 stores publish_value there before the item's merge barrier, and the
 // barrier is met even by an item with nothing to do, so the whole workgroup reads the value after the call.
-template <typename T, int D, int GS>
+template <typename T, int D, int GS, int HP>
 __device__ void decode_item(const AttnParams& p, int row, int split, int kvh, int qg, char* smem,
                             int* publish = nullptr, int publish_value = 0) {
   using E = Elem<T>;
   static_assert(D == 64 || D == 128, "head_dim 64 or 128");
+  static_assert(HP == 1 || HP == 2, "one or two kv heads per item");
   constexpr int LPT = D / 8;      // lanes per token head row, 16 bytes each
-  constexpr int TPI = 64 / LPT;   // tokens per wave step
-  constexpr int U = kTile / TPI;  // steps per 16-token tile
+  constexpr int LPH = LPT * HP;   // lanes per token piece: the item's HP head rows, adjacent in a token's NHD row
+  constexpr int TPI = 64 / LPH;   // tokens per wave step
+  constexpr int KT = kTile / HP;  // tokens per wave tile (U load steps whatever HP)
+  constexpr int U = KT / TPI;     // load steps per wave tile
   static_assert(U % 2 == 0, "token pairs");
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int grp = lane / LPT, part = lane % LPT;
+  const int grp = lane / LPH, hs = (lane / LPT) % HP, part = lane % LPT;
 
   const int lk = key_len(p, row);
   const int kbeg = split * p.split;
@@ -78,7 +87,7 @@ __device__ void decode_item(const AttnParams& p, int row, int split, int kvh, in
   const int kend = valid ? min(lk, kbeg + p.split) : kbeg;
   const int nsplit = min((lk + p.split - 1) / p.split, p.max_splits);
   const int tok = p.cu_q ? p.cu_q[row] : row;
-  const int head0 = kvh * p.group + qg * GS;
+  const int head0 = (kvh + hs) * p.group + qg * GS;  // this lane's query heads (kvh: the item's first kv head)
   const float c = p.scale_log2;
 
   u32x4 qv[GS];
@@ -97,7 +106,7 @@ __device__ void decode_item(const AttnParams& p, int row, int split, int kvh, in
   // Byte offset of this lane's 16 bytes of step u inside a tile (tile rows are p.c_st apart; fits 32 bits).
   uint32_t loff[U];
 #pragma unroll
-  for (int u = 0; u < U; ++u) loff[u] = (uint32_t)((u * TPI + grp) * p.c_st + part * 16);
+  for (int u = 0; u < U; ++u) loff[u] = (uint32_t)((u * TPI + grp) * p.c_st + hs * p.c_sh + part * 16);
   const int32_t* table = p.tables + (int64_t)row * p.t_stride;
 
   // Page numbers come through the scalar cache, once per page this wave enters: a vector load of the table would
@@ -129,7 +138,7 @@ __device__ void decode_item(const AttnParams& p, int row, int split, int kvh, in
         for (int w = 1; w < 4; ++w) d = E::dot2(qv[g][w], kv[u][w], d);
         s[u][g] = group_sum<LPT>(d);
       }
-    if (t0 + kTile > kend) {  // wave-uniform: the row's last tile; tokens past it get no weight
+    if (t0 + KT > kend) {  // wave-uniform: the row's last tile; tokens past it get no weight
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const bool in = t0 + u * TPI + grp < kend;
@@ -144,10 +153,12 @@ __device__ void decode_item(const AttnParams& p, int row, int split, int kvh, in
       float x = s[0][g];
 #pragma unroll
       for (int u = 1; u < U; ++u) x = vmax(x, s[u][g]);
-      mt[g] = groups_max<LPT>(x);  // finite: every tile holds a token in range
+      mt[g] = groups_max<LPH>(x);  // finite: every tile holds a token in range
       grow |= mt[g] > m[g];
     }
-    if (__builtin_amdgcn_readfirstlane(grow)) {
+    // One kv head per item: the max is wave-uniform. Two: each head's lanes hold their own, and a lane whose max did
+    // not grow rescales by 1.
+    if (HP == 1 ? __builtin_amdgcn_readfirstlane(grow) != 0 : __builtin_amdgcn_ballot_w64(grow) != 0) {
 #pragma unroll
       for (int g = 0; g < GS; ++g) {
         const float mn = vmax(m[g], mt[g]);
@@ -172,7 +183,7 @@ __device__ void decode_item(const AttnParams& p, int row, int split, int kvh, in
   };
   // acc += p . V over the tile: value rows of token pairs interleaved per dim, 2-term dot products.
   auto pv = [&](int t0, u32x4 (&vv)[U], const uint32_t (&pp)[GS][U / 2]) {
-    if (t0 + kTile > kend) {  // values past the range may be NaN: zero them (their p is 0)
+    if (t0 + KT > kend) {  // values past the range may be NaN: zero them (their p is 0)
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const bool in = t0 + u * TPI + grp < kend;
@@ -194,8 +205,8 @@ __device__ void decode_item(const AttnParams& p, int row, int split, int kvh, in
       }
   };
 
-  constexpr int kStride = kTile * kWaves;
-  int t0 = kbeg + kTile * wave;
+  constexpr int kStride = KT * kWaves;
+  int t0 = kbeg + KT * wave;
   if (t0 < kend) {
     // Staggered: the next tile's keys load during this tile's p.v, its values during its own q.k.
     u32x4 kv[U], vv[U];
@@ -221,27 +232,26 @@ __device__ void decode_item(const AttnParams& p, int row, int split, int kvh, in
   // Sum the token groups of the wave (they share m); m moves to the log2 domain of the merges.
 #pragma unroll
   for (int g = 0; g < GS; ++g) {
-    l[g] = groups_sum<LPT>(l[g]);
+    l[g] = groups_sum<LPH>(l[g]);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[g][e] = groups_sum<LPT>(acc[g][e]);
+    for (int e = 0; e < 8; ++e) acc[g][e] = groups_sum<LPH>(acc[g][e]);
     m[g] *= c;
   }
-  constexpr int VPL = 1;
-
-  // Merge the waves through LDS: wm/wl [kWaves][GS], wacc [kWaves][GS][D].
+  // Merge the waves through LDS: wm/wl [kWaves][HG], wacc [kWaves][HG][D] for the item's HG = HP GS query heads
+  // (lanes of token group 0 hold their head's sums).
+  constexpr int HG = HP * GS;
   float* wm = reinterpret_cast<float*>(smem);
-  float* wl = wm + kWaves * GS;
-  float* wacc = wl + kWaves * GS;
-  if (lane < LPT) {
+  float* wl = wm + kWaves * HG;
+  float* wacc = wl + kWaves * HG;
+  if (lane < LPH) {
 #pragma unroll
     for (int g = 0; g < GS; ++g) {
+      const int hg = wave * HG + hs * GS + g;
 #pragma unroll
-      for (int v = 0; v < VPL; ++v)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) wacc[(wave * GS + g) * D + (v * LPT + part) * 8 + e] = acc[g][v * 8 + e];
-      if (lane == 0) {
-        wm[wave * GS + g] = m[g];
-        wl[wave * GS + g] = l[g];
+      for (int e = 0; e < 8; ++e) wacc[hg * D + part * 8 + e] = acc[g][e];
+      if (part == 0) {
+        wm[hg] = m[g];
+        wl[hg] = l[g];
       }
     }
   }
@@ -249,26 +259,26 @@ __device__ void decode_item(const AttnParams& p, int row, int split, int kvh, in
   __syncthreads();
   if (!valid) return;
   // One thread per 8 output elements.
-  for (int c = threadIdx.x; c < GS * D / 8; c += blockDim.x) {
-    const int g = c / (D / 8), d0 = (c % (D / 8)) * 8;
+  for (int c = threadIdx.x; c < HG * D / 8; c += blockDim.x) {
+    const int g = c / (D / 8), d0 = (c % (D / 8)) * 8;  // g: query head of the item, hs-major
     float mmax = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) mmax = fmaxf(mmax, wm[w * GS + g]);
+    for (int w = 0; w < kWaves; ++w) mmax = fmaxf(mmax, wm[w * HG + g]);
     float o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     float den = 0.f;
     if (mmax != -INFINITY) {
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) {
-        const float wt = fast_exp2(wm[w * GS + g] - mmax);
-        den += wt * wl[w * GS + g];
+        const float wt = fast_exp2(wm[w * HG + g] - mmax);
+        den += wt * wl[w * HG + g];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] += wt * wacc[(w * GS + g) * D + d0 + e];
+        for (int e = 0; e < 8; ++e) o[e] += wt * wacc[(w * HG + g) * D + d0 + e];
       }
       const float inv = 1.f / den;
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] *= inv;
     }
-    const int head = head0 + g;
+    const int head = (kvh + g / GS) * p.group + qg * GS + g % GS;
     if (nsplit <= 1) {
       u32x4 packed;
 #pragma unroll
@@ -287,25 +297,25 @@ __device__ void decode_item(const AttnParams& p, int row, int split, int kvh, in
 // ---------------------------------------------------------------------------------------------------------
 // Kernels.
 
-template <int D, int GS>
+template <int D, int GS, int HP>
 struct SmemBytes {
-  static constexpr int kDecode = kWaves * GS * (D + 2) * 4;
+  static constexpr int kDecode = kWaves * HP * GS * (D + 2) * 4;
 };
 
 // Work-list kernels. blockIdx.x walks the device work list with the query-head groups innermost, so workgroups
 // are dispatched in list order (longest first). The list holds a step's prompt items first (n_items[1] of them),
 // then its decode items (n_items[0] in all). Decode items run in decode_list_kernel at the decode item's register
 // budget; prompt items in prompt_list_kernel, whose MFMA tile needs more registers and LDS.
-template <typename T, int D, int GS>
+template <typename T, int D, int GS, int HP>
 __global__ __launch_bounds__(256) void decode_list_kernel(AttnParams p) {
-  __shared__ __attribute__((aligned(16))) char smem[SmemBytes<D, GS>::kDecode];
-  const int ny = p.hkv * p.qgroups;
+  __shared__ __attribute__((aligned(16))) char smem[SmemBytes<D, GS, HP>::kDecode];
+  const int ny = p.hkv / HP * p.qgroups;
   const int bx = blockIdx.x / ny, by = blockIdx.x - bx * ny;
-  const int kvh = by / p.qgroups, qg = by - kvh * p.qgroups;
+  const int kh = by / p.qgroups, qg = by - kh * p.qgroups;
   const int i = bx + p.n_items[1];
   if (i >= p.n_items[0]) return;
   const int2 it = p.items[i];
-  decode_item<T, D, GS>(p, it.x, it.y, kvh, qg, smem);
+  decode_item<T, D, GS, HP>(p, it.x, it.y, kh * HP, qg, smem);
 }
 
 // Decode items of the work list on a persistent grid: each workgroup takes items by ticket (an atomic counter the
@@ -315,11 +325,11 @@ __global__ __launch_bounds__(256) void decode_list_kernel(AttnParams p) {
 // The last workgroup to finish puts the ticket and the exit count back to zero, so the next layer of the step can
 // run on the same plan without a plan launch: every workgroup's ticket draws have returned (their values were
 // read) before it counts itself out, so no draw can follow the reset.
-template <typename T, int D, int GS>
+template <typename T, int D, int GS, int HP>
 __device__ __forceinline__ void decode_persistent(const AttnParams& p) {
-  __shared__ __attribute__((aligned(16))) char smem[2][SmemBytes<D, GS>::kDecode];
+  __shared__ __attribute__((aligned(16))) char smem[2][SmemBytes<D, GS, HP>::kDecode];
   __shared__ int s_ticket[2];
-  const int ny = p.hkv * p.qgroups;
+  const int ny = p.hkv / HP * p.qgroups;
   const int first = p.n_items[1];
   const int total = (p.n_items[0] - first) * ny;
   if (threadIdx.x == 0) s_ticket[0] = atomicAdd(p.ticket, 1);
@@ -329,9 +339,9 @@ __device__ __forceinline__ void decode_persistent(const AttnParams& p) {
     int next = 0;
     if (threadIdx.x == 0) next = atomicAdd(p.ticket, 1);
     const int bx = f / ny, by = f - bx * ny;
-    const int kvh = by / p.qgroups, qg = by - kvh * p.qgroups;
+    const int kh = by / p.qgroups, qg = by - kh * p.qgroups;
     const int2 it = p.items[first + bx];
-    decode_item<T, D, GS>(p, it.x, it.y, kvh, qg, smem[k & 1], &s_ticket[(k + 1) & 1], next);
+    decode_item<T, D, GS, HP>(p, it.x, it.y, kh * HP, qg, smem[k & 1], &s_ticket[(k + 1) & 1], next);
     f = __builtin_amdgcn_readfirstlane(s_ticket[(k + 1) & 1]);
   }
   if (threadIdx.x == 0 && atomicAdd(p.ticket + 1, 1) == (int)gridDim.x - 1) {
@@ -344,7 +354,7 @@ __device__ __forceinline__ void decode_persistent(const AttnParams& p) {
 // faster than under 128).
 template <typename T, int D, int GS>
 __global__ __launch_bounds__(256, 2) void decode_persistent_kernel(AttnParams p) {
-  decode_persistent<T, D, GS>(p);
+  decode_persistent<T, D, GS, 1>(p);
 }
 
 // Beside a mixed step's prompt workgroups (one per CU) two decode workgroups share each SIMD's 512 registers per
@@ -352,9 +362,9 @@ __global__ __launch_bounds__(256, 2) void decode_persistent_kernel(AttnParams p)
 // below keeps the decode waves off the 256 a lone workgroup could take; the compiler rounds it to an occupancy level
 // (three waves per SIMD, 168). The 128 of four workgroups per CU would spill the D = 128 item. The grid asks for
 // three per CU: the CUs without a prompt workgroup take the third.
-template <typename T, int D, int GS>
+template <typename T, int D, int GS, int HP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_num_vgpr(160))) void decode_beside_kernel(AttnParams p) {
-  decode_persistent<T, D, GS>(p);
+  decode_persistent<T, D, GS, HP>(p);
 }
 
 // TP: pages per 64-key prompt tile. TP > 0 (pages of a multiple of 64 keys, or of 32 or 16): the tiles stream
@@ -398,10 +408,10 @@ __global__ __launch_bounds__(256, 2) void prompt_overlap_kernel(AttnParams p) {
 // first and the decode workgroups stream through the slots they leave, as in the overlapped schedule but without a
 // second stream, its events and one launch: for steps of a few hundred rows, whose launch sequence is a large share
 // of their time.
-template <typename T, int D, int GS, int TP>
+template <typename T, int D, int GS, int TP, int HP>
 __global__ __launch_bounds__(256, 2) void mixed_small_kernel(AttnParams p, int32_t prompt_wgs) {
   constexpr int RING = kRingOf<TP>;
-  static_assert(SmemBytes<D, GS>::kDecode <= (RING > 0 ? RING : 1) * PromptSmem<D, D, (TP > 1)>::kBytes,
+  static_assert(SmemBytes<D, GS, HP>::kDecode <= (RING > 0 ? RING : 1) * PromptSmem<D, D, (TP > 1)>::kBytes,
                 "LDS for both");
   __shared__ __attribute__((aligned(16))) char smem[(RING > 0 ? RING : 1) * PromptSmem<D, D, (TP > 1)>::kBytes];
   const int b = blockIdx.x;
@@ -411,22 +421,22 @@ __global__ __launch_bounds__(256, 2) void mixed_small_kernel(AttnParams p, int32
     const int2 it = p.items[bx];
     prefill_item<T, D, D, true, false, RING, 4, false, (TP > 0 ? TP : 1)>(p, it.x, -1 - it.y, kvh, smem);
   } else {
-    const int ny = p.hkv * p.qgroups;
+    const int ny = p.hkv / HP * p.qgroups;
     const int f = b - prompt_wgs, bx = f / ny, by = f - bx * ny;
-    const int kvh = by / p.qgroups, qg = by - kvh * p.qgroups;
+    const int kh = by / p.qgroups, qg = by - kh * p.qgroups;
     const int i = bx + p.n_items[1];
     if (i >= p.n_items[0]) return;
     const int2 it = p.items[i];
-    decode_item<T, D, GS>(p, it.x, it.y, kvh, qg, smem);
+    decode_item<T, D, GS, HP>(p, it.x, it.y, kh * HP, qg, smem);
   }
 }
 
 // Decode of more rows than the planner holds: blockIdx.x is (row, split), blockIdx.y the query-head group.
-template <typename T, int D, int GS>
+template <typename T, int D, int GS, int HP>
 __global__ __launch_bounds__(256) void decode_grid_kernel(AttnParams p) {
-  __shared__ __attribute__((aligned(16))) char smem[SmemBytes<D, GS>::kDecode];
-  const int kvh = blockIdx.y / p.qgroups, qg = blockIdx.y % p.qgroups;
-  decode_item<T, D, GS>(p, blockIdx.x / p.max_splits, blockIdx.x % p.max_splits, kvh, qg, smem);
+  __shared__ __attribute__((aligned(16))) char smem[SmemBytes<D, GS, HP>::kDecode];
+  const int kh = blockIdx.y / p.qgroups, qg = blockIdx.y % p.qgroups;
+  decode_item<T, D, GS, HP>(p, blockIdx.x / p.max_splits, blockIdx.x % p.max_splits, kh * HP, qg, smem);
 }
 
 constexpr int kLenBuckets = 64;
@@ -656,22 +666,27 @@ static int resident_per_cu() {
 
 // The decode items of a listed launch: a persistent grid of at most per_cu workgroups per CU taking items by
 // ticket (beside a mixed step's prompt workgroups a fixed share of every CU keeps both kernels resident), or one
-// workgroup per item -- for per_cu 0, and for steps whose item bound is under eight items per persistent
-// workgroup, whose few short items finish sooner all at once than in rounds.
-template <typename T, int D, int GS, bool BESIDE = false>
+// workgroup per item -- for per_cu 0, for steps whose item bound is under eight items per persistent workgroup,
+// whose few short items finish sooner all at once than in rounds, and for items of kv-head pairs outside the
+// overlap: those ran faster one workgroup per item than on the persistent grid (same box, medians of 3: Qwen3-8B
+// batch-256 decode 0.727 against 0.771 ms, long-context 0.855 against 0.865, on 16-token pages 0.744 against
+// 0.783).
+template <typename T, int D, int GS, int HP, bool BESIDE = false>
 static void launch_decode(const AttnParams& p, const Shape& s, int per_cu, hipStream_t stream) {
-  const int items = s.max_decode_items * p.hkv * p.qgroups;  // a bound: the plan lists no more
-  const int resident = BESIDE ? resident_per_cu<decode_beside_kernel<T, D, GS>>()
-                              : resident_per_cu<decode_persistent_kernel<T, D, GS>>();
-  const int grid = per_cu > 0 ? std::min(per_cu, resident) * device_cus() : 0;
-  if (grid > 0 && items >= 8 * grid) {
-    if (BESIDE)
-      hipLaunchKernelGGL((decode_beside_kernel<T, D, GS>), dim3(grid), dim3(256), 0, stream, p);
-    else
-      hipLaunchKernelGGL((decode_persistent_kernel<T, D, GS>), dim3(grid), dim3(256), 0, stream, p);
-  } else {
-    hipLaunchKernelGGL((decode_list_kernel<T, D, GS>), dim3(items), dim3(256), 0, stream, p);
+  const int items = s.max_decode_items * (p.hkv / HP) * p.qgroups;  // a bound: the plan lists no more
+  if constexpr (BESIDE || HP == 1) {
+    const int resident = BESIDE ? resident_per_cu<decode_beside_kernel<T, D, GS, HP>>()
+                                : resident_per_cu<decode_persistent_kernel<T, D, GS>>();
+    const int grid = per_cu > 0 ? std::min(per_cu, resident) * device_cus() : 0;
+    if (grid > 0 && items >= 8 * grid) {
+      if constexpr (BESIDE)
+        hipLaunchKernelGGL((decode_beside_kernel<T, D, GS, HP>), dim3(grid), dim3(256), 0, stream, p);
+      else
+        hipLaunchKernelGGL((decode_persistent_kernel<T, D, GS>), dim3(grid), dim3(256), 0, stream, p);
+      return;
+    }
   }
+  hipLaunchKernelGGL((decode_list_kernel<T, D, GS, HP>), dim3(items), dim3(256), 0, stream, p);
 }
 
 // CUs that hold a prompt workgroup in an overlapped step: the caller's count clamped to [default, max] and
@@ -693,10 +708,10 @@ static void launch_prompt_list(const AttnParams& p, const Shape& s, hipStream_t 
 // and joins it back into `stream` with events; if the second stream cannot be set up, or the fork's record or wait
 // fails before anything is launched, the step runs serially instead (the same results). A failure after the decode
 // launch leaves the two streams unordered and is returned as LV_EHIP.
-template <typename T, int D, int GS, int TP>
+template <typename T, int D, int GS, int TP, int HP>
 static int launch(const AttnParams& p, bool listed, bool mixed, bool overlap, int prompt_wgs, const Shape& s,
                   hipStream_t stream, bool prompts_only) {
-  const int ny = p.hkv * p.qgroups;
+  const int ny = p.hkv / HP * p.qgroups;
   if (prompts_only) {  // a step of prompts: the prompt tiles on the whole GPU, nothing else
     launch_prompt_list<T, D, TP>(p, s, stream);
     return LV_OK;
@@ -705,9 +720,9 @@ static int launch(const AttnParams& p, bool listed, bool mixed, bool overlap, in
     // A step whose workgroups (bounds: most prompt bounds exit at once) fill the GPU at most kSmallStepRounds times
     // runs as one launch.
     const int64_t pw = (int64_t)s.max_prompt_items * p.hkv, dw = (int64_t)s.max_decode_items * ny;
-    const int resident = resident_per_cu<mixed_small_kernel<T, D, GS, TP>>();
+    const int resident = resident_per_cu<mixed_small_kernel<T, D, GS, TP, HP>>();
     if (pw + dw <= (int64_t)kSmallStepRounds * resident * device_cus()) {
-      hipLaunchKernelGGL((mixed_small_kernel<T, D, GS, TP>), dim3(pw + dw), dim3(256), 0, stream, p, (int32_t)pw);
+      hipLaunchKernelGGL((mixed_small_kernel<T, D, GS, TP, HP>), dim3(pw + dw), dim3(256), 0, stream, p, (int32_t)pw);
       LV_LAUNCH_CHECK("mixed_small_kernel");
       if (p.max_splits > 1)
         hipLaunchKernelGGL((splitk_merge_kernel<T, D>), dim3(p.rows, p.hq), dim3(64), 0, stream, p);
@@ -724,7 +739,7 @@ static int launch(const AttnParams& p, bool listed, bool mixed, bool overlap, in
     if (hipEventRecord(side->fork, stream) == hipSuccess &&
         hipStreamWaitEvent(side->stream, side->fork, 0) == hipSuccess) {
       forked = true;
-      launch_decode<T, D, GS, true>(p, s, kOverlapDecodeWgs, side->stream);
+      launch_decode<T, D, GS, HP, true>(p, s, kOverlapDecodeWgs, side->stream);
       LV_LAUNCH_CHECK("decode_persistent_kernel");
       LV_HIP_CHECK(hipEventRecord(side->join, side->stream));
       constexpr int pad = std::max(0, kOverlapLds - std::max(1, kRingOf<TP>) * PromptSmem<D, D, (TP > 1)>::kBytes);
@@ -738,11 +753,11 @@ static int launch(const AttnParams& p, bool listed, bool mixed, bool overlap, in
   if (forked) {
   } else if (listed && mixed) {
     launch_prompt_list<T, D, TP>(p, s, stream);
-    launch_decode<T, D, GS>(p, s, kDecodeWgs, stream);
+    launch_decode<T, D, GS, HP>(p, s, kDecodeWgs, stream);
   } else if (listed) {
-    launch_decode<T, D, GS>(p, s, kDecodeWgs, stream);
+    launch_decode<T, D, GS, HP>(p, s, kDecodeWgs, stream);
   } else {
-    hipLaunchKernelGGL((decode_grid_kernel<T, D, GS>), dim3(p.rows * p.max_splits, ny), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((decode_grid_kernel<T, D, GS, HP>), dim3(p.rows * p.max_splits, ny), dim3(256), 0, stream, p);
   }
   if (p.max_splits > 1)
     hipLaunchKernelGGL((splitk_merge_kernel<T, D>), dim3(p.rows, p.hq), dim3(64), 0, stream, p);
@@ -758,23 +773,38 @@ static int tile_pages(int block_size) {
   return 0;
 }
 
-template <typename T, int D, int GS>
+template <typename T, int D, int GS, int HP>
 static int launch_tp(const AttnParams& p, bool listed, bool mixed, bool overlap, int prompt_wgs, const Shape& s,
                      hipStream_t stream, bool prompts_only) {
   switch (tile_pages((int)p.bs.d)) {
-    case 1: return launch<T, D, GS, 1>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
-    case 2: return launch<T, D, GS, 2>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
-    case 4: return launch<T, D, GS, 4>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
-    default: return launch<T, D, GS, 0>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
+    case 1: return launch<T, D, GS, 1, HP>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
+    case 2: return launch<T, D, GS, 2, HP>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
+    case 4: return launch<T, D, GS, 4, HP>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
+    default: return launch<T, D, GS, 0, HP>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
   }
+}
+
+// Decode items of a streaming step take two kv heads where the step has an even number: a token's two head rows are
+// adjacent in the NHD cache, so each 64-lane load covers 512-byte pieces of token rows instead of 256-byte ones (a
+// math-free stream of 512-byte pieces at a 2 KB stride reads 7.15 TB/s on an MI355X, of 256-byte pieces
+// 6.5-6.7 TB/s). The split of a row's keys stays as planned, so such items are half as many and twice as long;
+// steps of fewer than kPairItems one-head items per CU (a few short rows, latency-bound) keep one head per item.
+constexpr int kPairItems = 8;
+template <typename T, int D, int GS>
+static int launch_hp(const AttnParams& p, bool listed, bool mixed, bool overlap, int prompt_wgs, const Shape& s,
+                     hipStream_t stream, bool prompts_only) {
+  const int64_t items = (int64_t)(listed ? s.max_decode_items : p.rows * p.max_splits) * p.hkv * p.qgroups;
+  if (p.hkv % 2 == 0 && items >= (int64_t)kPairItems * device_cus())
+    return launch_tp<T, D, GS, 2>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
+  return launch_tp<T, D, GS, 1>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
 }
 
 template <typename T, int D>
 static int launch_gs(const AttnParams& p, int gs, bool listed, bool mixed, bool overlap, int prompt_wgs,
                      const Shape& s, hipStream_t stream, bool prompts_only) {
-  if (gs == 4) return launch_tp<T, D, 4>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
-  if (gs == 2) return launch_tp<T, D, 2>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
-  return launch_tp<T, D, 1>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
+  if (gs == 4) return launch_hp<T, D, 4>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
+  if (gs == 2) return launch_hp<T, D, 2>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
+  return launch_hp<T, D, 1>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
 }
 
 template <typename T>

@@ -154,3 +154,52 @@ def test_random_mla_decode_matches_the_oracle(cuda, seed):
         tables.append(perm[at:at + k] + [-1] * (width - k))
         at += k
     check_mla(cuda, dtype, bs, lens, tables, queries=queries, heads=heads, seed=seed)
+
+
+WIDE_HEADS = [(8, 2), (16, 4), (32, 8), (12, 4), (24, 8), (6, 2), (64, 8), (8, 1)]
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_wide_decode_steps_match_the_oracle(cuda, seed, monkeypatch):
+    """Steps of 300-1200 decode rows (some with one or two prompt chunks too): enough items that decode items take
+    a pair of kv heads where the kv heads are even (one-workgroup-per-item and persistent launches, the 16-token
+    tiles of the persistent kernel and the 8-token tiles beside prompt tiles), and one head where they are odd."""
+    rng = np.random.default_rng(9500 + seed)
+    hq, hkv = WIDE_HEADS[seed % len(WIDE_HEADS)]
+    dim = int(rng.choice([64, 128]))
+    dtype = (torch.bfloat16, torch.float16)[int(rng.integers(2))]
+    bs = int(rng.choice([16, 64, 256]))
+    layout = ("NHD", "HND")[int(rng.integers(2))]
+    n_dec = int(rng.integers(300, 1200))
+    cached = [int(rng.integers(0, 2500)) for _ in range(n_dec)]
+    new = [1] * n_dec
+    for _ in range(int(rng.integers(0, 3))):
+        cached.append(int(rng.integers(0, 500)))
+        new.append(int(rng.integers(2, 300)))
+    need = [-(-(c + n) // bs) for c, n in zip(cached, new)]
+    pool = sum(need) + 3
+    perm = rng.permutation(pool).tolist()
+    width = max(need)
+    tables, at = [], 0
+    for k in need:
+        tables.append(perm[at:at + k] + [-1] * (width - k))
+        at += k
+    scale = float(rng.uniform(0.05, 0.2))
+    label = (f"seed {seed}: heads {hq}/{hkv} dim {dim} {dtype} bs {bs} {layout} decode rows {n_dec} "
+             f"prompts {list(zip(cached[n_dec:], new[n_dec:]))}")
+    print(label, flush=True)
+    backend = MI355XAttention(hq, dim, scale, hkv)
+    qs, kf, vf, kn, vn, kc, vc, slots = paged_step(cached, new, tables, pool, heads=hq, kv_heads=hkv, dim=dim,
+                                                   bs=bs, device=cuda, dtype=dtype, seed=seed, layout=layout)
+    backend.store_kvcache(kn, vn, kc, vc, slots)
+    decode_only = len(new) == n_dec
+    if not decode_only:
+        sched = (B.SCHEDULE_SERIAL, B.SCHEDULE_OVERLAP)[seed % 2]
+        monkeypatch.setattr(backend, "_schedule", lambda context, elem_bytes, s=sched: s)
+        label += f" schedule {'serial' if sched == B.SCHEDULE_SERIAL else 'overlap'}"
+    ctx = context_for(cached, new, tables, cuda, is_prefill=not decode_only)
+    out = backend.forward(torch.cat(qs), kn, vn, kc, vc, ctx)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all(), label
+    want = dense_expected(qs, kf, vf, scale)
+    torch.testing.assert_close(out.float().cpu(), want.float(), **TOL[dtype], msg=lambda m: f"{label}: {m}")
