@@ -29,6 +29,7 @@ constexpr int kOverlapCusPct = 44;    // percent of the CUs that hold a prompt w
 constexpr int kOverlapCusMaxPct = 75;  // at most this percent when the caller sizes the prompt share
 constexpr int kDecodeWgs = 2;         // persistent decode workgroups per CU outside the overlap
 constexpr int kOverlapDecodeWgs = 3;  // persistent decode workgroups per CU beside a mixed step's prompt workgroups
+                                      // (at most: pair items at D = 128 fit two)
 constexpr int kSplitTarget = 4096;    // decode items (x kv heads x query-head groups) a split-K grid aims for
 constexpr int kMinSplit = 256;        // keys per decode item at least
 constexpr int kSmallStepRounds = 8;   // a mixed step of at most this many GPU-fulls of workgroups is one launch
@@ -63,7 +64,7 @@ __device__ inline float groups_sum(float x) {
 
 // publish (persistent launches): thread 0 stores publish_value there before the item's merge barrier, and the
 // barrier is met even by an item with nothing to do, so the whole workgroup reads the value after the call.
-template <typename T, int D, int GS, int HP>
+template <typename T, int D, int GS, int HP, int US = 0>
 __device__ void decode_item(const AttnParams& p, int row, int split, int kvh, int qg, char* smem,
                             int* publish = nullptr, int publish_value = 0) {
   using E = Elem<T>;
@@ -72,7 +73,7 @@ __device__ void decode_item(const AttnParams& p, int row, int split, int kvh, in
   constexpr int LPT = D / 8;      // lanes per token head row, 16 bytes each
   constexpr int LPH = LPT * HP;   // lanes per token piece: the item's HP head rows, adjacent in a token's NHD row
   constexpr int TPI = 64 / LPH;   // tokens per wave step
-  constexpr int KT = kTile / HP;  // tokens per wave tile (U load steps whatever HP)
+  constexpr int KT = US > 0 ? TPI * US : kTile / HP;  // tokens per wave tile
   constexpr int U = KT / TPI;     // load steps per wave tile
   static_assert(U % 2 == 0, "token pairs");
   const int lane = threadIdx.x & 63;
@@ -306,7 +307,7 @@ struct SmemBytes {
 // are dispatched in list order (longest first). The list holds a step's prompt items first (n_items[1] of them),
 // then its decode items (n_items[0] in all). Decode items run in decode_list_kernel at the decode item's register
 // budget; prompt items in prompt_list_kernel, whose MFMA tile needs more registers and LDS.
-template <typename T, int D, int GS, int HP>
+template <typename T, int D, int GS, int HP, int US = 0>
 __global__ __launch_bounds__(256) void decode_list_kernel(AttnParams p) {
   __shared__ __attribute__((aligned(16))) char smem[SmemBytes<D, GS, HP>::kDecode];
   const int ny = p.hkv / HP * p.qgroups;
@@ -315,7 +316,7 @@ __global__ __launch_bounds__(256) void decode_list_kernel(AttnParams p) {
   const int i = bx + p.n_items[1];
   if (i >= p.n_items[0]) return;
   const int2 it = p.items[i];
-  decode_item<T, D, GS, HP>(p, it.x, it.y, kh * HP, qg, smem);
+  decode_item<T, D, GS, HP, US>(p, it.x, it.y, kh * HP, qg, smem);
 }
 
 // Decode items of the work list on a persistent grid: each workgroup takes items by ticket (an atomic counter the
@@ -325,7 +326,7 @@ __global__ __launch_bounds__(256) void decode_list_kernel(AttnParams p) {
 // The last workgroup to finish puts the ticket and the exit count back to zero, so the next layer of the step can
 // run on the same plan without a plan launch: every workgroup's ticket draws have returned (their values were
 // read) before it counts itself out, so no draw can follow the reset.
-template <typename T, int D, int GS, int HP>
+template <typename T, int D, int GS, int HP, int US = 0>
 __device__ __forceinline__ void decode_persistent(const AttnParams& p) {
   __shared__ __attribute__((aligned(16))) char smem[2][SmemBytes<D, GS, HP>::kDecode];
   __shared__ int s_ticket[2];
@@ -341,7 +342,7 @@ __device__ __forceinline__ void decode_persistent(const AttnParams& p) {
     const int bx = f / ny, by = f - bx * ny;
     const int kh = by / p.qgroups, qg = by - kh * p.qgroups;
     const int2 it = p.items[first + bx];
-    decode_item<T, D, GS, HP>(p, it.x, it.y, kh * HP, qg, smem[k & 1], &s_ticket[(k + 1) & 1], next);
+    decode_item<T, D, GS, HP, US>(p, it.x, it.y, kh * HP, qg, smem[k & 1], &s_ticket[(k + 1) & 1], next);
     f = __builtin_amdgcn_readfirstlane(s_ticket[(k + 1) & 1]);
   }
   if (threadIdx.x == 0 && atomicAdd(p.ticket + 1, 1) == (int)gridDim.x - 1) {
@@ -365,6 +366,15 @@ __global__ __launch_bounds__(256, 2) void decode_persistent_kernel(AttnParams p)
 template <typename T, int D, int GS, int HP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_num_vgpr(160))) void decode_beside_kernel(AttnParams p) {
   decode_persistent<T, D, GS, HP>(p);
+}
+// Pair items at D = 128 beside the prompt workgroups: 16-token wave tiles (8 load steps, twice the bytes in flight
+// per wave of the 8-token tile) at 210 registers, so one such workgroup shares a prompt CU and two fill the others
+// (the mixed step 2.934 -> 2.919 ms against the capped kernel at three per CU, same box, medians of 3).
+template <int D, int HP>
+constexpr int kWideSteps = HP == 2 && D == 128 ? 8 : 0;  // load steps of a wave tile where registers allow 16 tokens
+template <typename T, int D, int GS>
+__global__ __launch_bounds__(256, 2) void decode_beside_pairs_kernel(AttnParams p) {
+  decode_persistent<T, D, GS, 2, kWideSteps<D, 2>>(p);
 }
 
 // TP: pages per 64-key prompt tile. TP > 0 (pages of a multiple of 64 keys, or of 32 or 16): the tiles stream
@@ -675,18 +685,28 @@ template <typename T, int D, int GS, int HP, bool BESIDE = false>
 static void launch_decode(const AttnParams& p, const Shape& s, int per_cu, hipStream_t stream) {
   const int items = s.max_decode_items * (p.hkv / HP) * p.qgroups;  // a bound: the plan lists no more
   if constexpr (BESIDE || HP == 1) {
-    const int resident = BESIDE ? resident_per_cu<decode_beside_kernel<T, D, GS, HP>>()
-                                : resident_per_cu<decode_persistent_kernel<T, D, GS>>();
+    constexpr bool kWide = BESIDE && kWideSteps<D, HP> > 0;
+    int resident = 0;
+    if constexpr (kWide)
+      resident = resident_per_cu<decode_beside_pairs_kernel<T, D, GS>>();
+    else if constexpr (BESIDE)
+      resident = resident_per_cu<decode_beside_kernel<T, D, GS, HP>>();
+    else
+      resident = resident_per_cu<decode_persistent_kernel<T, D, GS>>();
     const int grid = per_cu > 0 ? std::min(per_cu, resident) * device_cus() : 0;
     if (grid > 0 && items >= 8 * grid) {
-      if constexpr (BESIDE)
+      if constexpr (kWide)
+        hipLaunchKernelGGL((decode_beside_pairs_kernel<T, D, GS>), dim3(grid), dim3(256), 0, stream, p);
+      else if constexpr (BESIDE)
         hipLaunchKernelGGL((decode_beside_kernel<T, D, GS, HP>), dim3(grid), dim3(256), 0, stream, p);
       else
         hipLaunchKernelGGL((decode_persistent_kernel<T, D, GS>), dim3(grid), dim3(256), 0, stream, p);
       return;
     }
   }
-  hipLaunchKernelGGL((decode_list_kernel<T, D, GS, HP>), dim3(items), dim3(256), 0, stream, p);
+  // Pair items at D = 128 one workgroup per item take 16-token wave tiles too (two workgroups per CU instead of
+  // three of the 8-token tile: batch-256 decode 0.736 -> 0.728 ms, on 16-token pages 0.745 -> 0.738).
+  hipLaunchKernelGGL((decode_list_kernel<T, D, GS, HP, kWideSteps<D, HP>>), dim3(items), dim3(256), 0, stream, p);
 }
 
 // CUs that hold a prompt workgroup in an overlapped step: the caller's count clamped to [default, max] and
