@@ -332,10 +332,13 @@ def attention_op(wl) -> str:
         return "lv_mla_decode (mla_run_kernel + mla_run_merge_kernel)"
     if all(n > 1 for n in wl.num_new):  # a step of prompts: the serial schedule, prompt tiles on the whole GPU
         return "lv_paged_attention (plan_kernel + prompt_list_kernel)"
-    if any(n > 1 for n in wl.num_new):
-        return ("lv_paged_attention (plan_kernel + decode_persistent_kernel on a second stream beside "
-                "prompt_overlap_kernel + splitk_merge_kernel)")
-    return "lv_paged_attention (plan_kernel + decode_persistent_kernel + splitk_merge_kernel)"
+    # The paged steps' kernels as the committed kernel trace of this workload names them.
+    f = ROOT / "profiles" / f"traffic_{wl.name}.json"
+    if f.exists():
+        kernels = [k.removeprefix("lv::") for k in json.loads(f.read_text()).get("kernels", [])]
+        if kernels:
+            return f"lv_paged_attention ({' + '.join(kernels)})"
+    return "lv_paged_attention (plan_kernel + decode kernels + splitk_merge_kernel)"
 
 
 def traffic_of(name: str):
