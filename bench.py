@@ -17,7 +17,8 @@ mixed batch at token budget 8192 (4 chunks of 1536 new tokens on a cached prefix
 with context U[256, 4096]; 32/8 heads, d128, bf16, 256-token pages). The line also carries per-kernel times from
 HIP events on the launch stream (per layer: store and attention, the attention of the first layer -- which plans
 -- and of the later ones), a ``roofline`` object for the attention op (mean over layers), a ``cpu_baseline`` (the
-oracle's restatement of the reference PyTorch backend timed on a bounded sample on the host cores) and, under
+oracle's restatement of the reference PyTorch backend timed over the whole step on the host cores, after every GPU
+measurement; batch-256 decode carries one too) and, under
 ``workloads``, the same figures for the other shapes this path is measured on (Qwen3-8B pure decode at batch 256,
 long-context split-K decode, DeepSeek-V2-Lite MLA decode, Qwen3-0.6B mixed, both decode steps again on
 lean-vLLM's default 16-token pages, and two steps of prompts -- the Qwen3-8B mixed step's four chunks alone and
@@ -45,6 +46,7 @@ EXTRA = ("qwen3_8b_decode,qwen3_8b_long,deepseek_v2_lite_mla,qwen3_0_6b_mixed,qw
          "deepseek_v2_lite_mla_prefill,deepseek_v2_lite_mla_prefill_two_pass,qwen3_8b_decode_bs16,"
          "deepseek_v2_lite_mla_bs16,qwen3_8b_mixed_bs16,qwen3_8b_prefill_bs16")
 RIDGE_FLOP_PER_BYTE = PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)  # above it a step is MFMA-bound
+CPU_ALSO = "qwen3_8b_decode"  # a CPU baseline is also timed for this workload (batch-256 Qwen3-8B decode)
 
 
 def parse():
@@ -183,6 +185,11 @@ def measure(name: str, steps: int, warmup: int, seed: int, dev, layers: int | No
     attn_ms = mean([e[1].elapsed_time(e[2]) for st in ev_layer for e in st])
     attn_first = mean([st[0][1].elapsed_time(st[0][2]) for st in ev_layer])
     attn_later = mean([e[1].elapsed_time(e[2]) for st in ev_layer for e in st[1:]]) if layers > 1 else attn_first
+    # The attention of the layers on each copy of the cache (later layers): copies are separate allocations, and
+    # their placement in HBM moves a decode step's time by a few percent from one allocation to the next.
+    by_set = [mean([st[layer][1].elapsed_time(st[layer][2]) for st in ev_layer
+                    for layer in range(c, layers, sets) if layer > 0 or layers == 1])
+              for c in range(min(sets, layers)) if c > 0 or layers == 1 or sets < layers]
     step_ms = wall_ms
     layer_ms = step_ms / layers
     flops = W.algorithmic_flops(wl)
@@ -200,7 +207,8 @@ def measure(name: str, steps: int, warmup: int, seed: int, dev, layers: int | No
         "pct_of_peak_hbm": round(100 * step_bytes / (step_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 2),
         "tokens_per_s_per_layer": round(wl.tokens / (layer_ms * 1e-3), 1),
         "kernel_ms": {"pack": round(pack_ms, 4), "store": round(store_ms, 4), "attention": round(attn_ms, 4),
-                      "attention_first_layer": round(attn_first, 4), "attention_later_layers": round(attn_later, 4)},
+                      "attention_first_layer": round(attn_first, 4), "attention_later_layers": round(attn_later, 4),
+                      "attention_by_cache_set": [round(x, 4) for x in by_set]},
         "host_stage_ms": round(host_stage_ms, 4),
         "attention_GBs": round(attn_gbs, 1),
         "attention_frac_of_peak": round(attn_gbs / PEAK_HBM_GBS, 4),
@@ -214,49 +222,46 @@ def measure(name: str, steps: int, warmup: int, seed: int, dev, layers: int | No
     return figures, wl, t
 
 
-def cpu_baseline(wl, t, dec_sample: int = 256, passes: int = 5):
-    """The oracle's TorchAttention restatement (page gather, zeroed padding, row padding, bottom-right mask,
-    GQA-folded SDPA) in fp32 on the host cores, on a bounded sample of the step: every prompt chunk in full plus the
-    first ``dec_sample`` decode rows, with the rows' pages copied to the host beforehand. One warmup pass, whose
-    outputs are first checked against the textbook dense oracle (a few decode rows and prompt queries, max-abs
-    1e-3), then the median of ``passes`` timed passes; the decode time is scaled to all decode rows. Returns the
-    object for the JSON line, in the same algorithmic-byte GB/s as the GPU figures (and tokens/s per layer)."""
+def cpu_inputs(wl, t, check_rows: int = 64):
+    """Host copies of what the CPU baseline reads, taken right after the workload's GPU measurement so that its
+    device tensors can be freed: the step's queries, and the pages of every decode row and of every prompt chunk
+    (bf16, renumbered). The timing itself runs after every GPU measurement (``cpu_baseline``)."""
     import numpy as np
     import torch
 
     from lvattn import workloads as W
     from oracle import attention as A
 
-    torch.set_num_threads(len(os.sched_getaffinity(0)))
-    cores = torch.get_num_threads()
     order = W.batch_order(wl)
     num_new = np.asarray(wl.num_new)[order]
     num_cached = np.asarray(wl.num_cached)[order]
     lists = [wl.block_lists[i] for i in order]
     dec_rows = [r for r in range(wl.rows) if num_new[r] == 1]
     pre_rows = [r for r in range(wl.rows) if num_new[r] > 1]
-    sample_dec = dec_rows[:dec_sample]
     q_start = np.concatenate([[0], np.cumsum(num_new)])
 
     def compact(rows):
         """The rows' pages copied to the host (bf16), renumbered 0..n-1 (the oracle reads only these)."""
         pages = sorted({p for r in rows for p in lists[r]})
         index = {p: i for i, p in enumerate(pages)}
-        sel = torch.tensor(pages, dtype=torch.long, device=t.k_cache.device)
-        kc, vc = t.k_cache[sel].cpu(), t.v_cache[sel].cpu()
+        kc = torch.empty((len(pages),) + tuple(t.k_cache.shape[1:]), dtype=t.k_cache.dtype)
+        vc = torch.empty_like(kc)
+        for i in range(0, len(pages), 2048):  # bounded device temporaries
+            sel = torch.tensor(pages[i:i + 2048], dtype=torch.long, device=t.k_cache.device)
+            kc[i:i + 2048] = t.k_cache[sel].cpu()
+            vc[i:i + 2048] = t.v_cache[sel].cpu()
         width = max(len(lists[r]) for r in rows)
         bt = torch.full((len(rows), width), -1, dtype=torch.int32)
         for j, r in enumerate(rows):
             bt[j, : len(lists[r])] = torch.tensor([index[p] for p in lists[r]], dtype=torch.int32)
         return kc, vc, bt
 
-    math_ = A.TorchMath(wl.num_heads, wl.head_dim, wl.scale, wl.num_kv_heads)
     q_all = t.q.float().cpu()
     dec = None
-    if sample_dec:
-        kc, vc, bt = compact(sample_dec)
-        q = q_all[[int(q_start[r]) for r in sample_dec]]
-        lens = torch.tensor([int(num_cached[r] + 1) for r in sample_dec], dtype=torch.int32)
+    if dec_rows:
+        kc, vc, bt = compact(dec_rows)
+        q = q_all[[int(q_start[r]) for r in dec_rows]]
+        lens = torch.tensor([int(num_cached[r] + 1) for r in dec_rows], dtype=torch.int32)
         dec = (q, kc, vc, lens, bt)
     pre = []
     if pre_rows:
@@ -267,12 +272,33 @@ def cpu_baseline(wl, t, dec_sample: int = 256, passes: int = 5):
                             cu_seqlens_k=torch.tensor([0, lk], dtype=torch.int32), max_seqlen_q=lq, max_seqlen_k=lk,
                             block_tables=bt[j:j + 1])
             pre.append((q_all[int(q_start[r]): int(q_start[r]) + lq], kc, vc, ctx))
+    return {"dec": dec, "pre": pre, "check_rows": min(check_rows, len(dec_rows))}
 
-    def one_pass():
+
+def cpu_baseline(wl, inputs):
+    """The oracle's TorchAttention restatement (page gather, zeroed padding, row padding, bottom-right mask,
+    GQA-folded SDPA) in fp32 on all host cores, over the whole step: every decode row and every prompt chunk. One
+    warmup pass over the first ``check_rows`` decode rows and the chunks, whose outputs are checked against the
+    textbook dense oracle (a few decode rows and prompt queries, max-abs 1e-3), then one timed pass over the whole
+    step. Returns the object for the JSON line, in the same algorithmic-byte GB/s as the GPU figures (and tokens/s
+    per layer)."""
+    import torch
+
+    from lvattn import workloads as W
+    from oracle import attention as A
+
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    cores = torch.get_num_threads()
+    dec, pre = inputs["dec"], inputs["pre"]
+    math_ = A.TorchMath(wl.num_heads, wl.head_dim, wl.scale, wl.num_kv_heads)
+
+    def one_pass(rows=None):
         times, outs = {}, {}
         if dec is not None:
+            q, kc, vc, lens, bt = dec
+            n = len(lens) if rows is None else rows
             t0 = time.perf_counter()
-            outs["decode"] = A.decode_in_row_chunks(math_, *dec, rows_per_chunk=16)
+            outs["decode"] = A.decode_in_row_chunks(math_, q[:n], kc, vc, lens[:n], bt[:n], rows_per_chunk=16)
             times["decode"] = time.perf_counter() - t0
         if pre:
             t0 = time.perf_counter()
@@ -280,11 +306,11 @@ def cpu_baseline(wl, t, dec_sample: int = 256, passes: int = 5):
             times["prefill"] = time.perf_counter() - t0
         return times, outs
 
-    _, outs = one_pass()  # warmup, and the outputs the check reads
+    _, outs = one_pass(inputs["check_rows"])  # warmup, and the outputs the check reads
     worst = 0.0
     if dec is not None:
         q, kc, vc, lens, bt = dec
-        for j in sorted({0, len(sample_dec) // 2, len(sample_dec) - 1}):
+        for j in sorted({0, inputs["check_rows"] // 2, inputs["check_rows"] - 1}):
             n = int(lens[j])
             pages = bt[j, : -(-n // wl.block_size)].long()
             k = kc[pages].flatten(0, 1)[:n].float()
@@ -301,22 +327,19 @@ def cpu_baseline(wl, t, dec_sample: int = 256, passes: int = 5):
             worst = max(worst, (o[j:j + 1] - want).abs().max().item())
     if worst > 1e-3:
         raise RuntimeError(f"cpu baseline: the timed restatement differs from the dense oracle by {worst:.2e}")
-    runs = [one_pass()[0] for _ in range(passes)]
-    timings = {k: sorted(r[k] for r in runs)[passes // 2] for k in runs[0]}
-    if "decode" in timings:
-        timings["decode"] *= len(dec_rows) / len(sample_dec)
+    timings, _ = one_pass()
     seconds = sum(timings.values())
     nbytes = W.algorithmic_bytes(wl)["attention"]
+    n_dec = 0 if dec is None else len(dec[3])
     return {
         "value": round(nbytes / seconds / 1e9, 2),
         "unit": "GB/s",
         "cores": cores,
         "kind": "port",
-        "sample": (f"oracle TorchAttention restatement (attention only), fp32, {cores} threads, checked against the "
-                   f"dense oracle (max abs {worst:.1e}), 1 warmup + median of {passes}: all {len(pre_rows)} prompt "
-                   f"chunks in full ({timings.get('prefill', 0):.2f} s) + {len(sample_dec)} of {len(dec_rows)} "
-                   f"decode rows ({timings.get('decode', 0):.2f} s"
-                   f"{'' if len(sample_dec) == len(dec_rows) else ' scaled to all rows'})"),
+        "sample": (f"{wl.name}, the whole step: oracle TorchAttention restatement (attention only), fp32, {cores} "
+                   f"threads, checked against the dense oracle (max abs {worst:.1e}), 1 warmup on {inputs['check_rows']}"
+                   f" decode rows, then one timed pass: {len(pre)} prompt chunks ({timings.get('prefill', 0):.2f} s)"
+                   f" + all {n_dec} decode rows ({timings.get('decode', 0):.2f} s)"),
         "tokens_per_s_per_layer": round(wl.tokens / seconds, 1),
         "seconds_per_step": round(seconds, 3),
     }
@@ -361,16 +384,27 @@ def main():
     import torch
 
     dev = torch.device("cuda:0")
+    # Every GPU measurement first, back to back; the CPU baselines (whose host copies are taken right after their
+    # workload's measurement) run last, so no GPU figure follows a long GPU-idle gap.
+    cpu_wanted = set() if args.no_cpu_baseline else {args.workload, CPU_ALSO}
+    cpu_in = {}
     primary, wl, t = measure(args.workload, args.steps, args.warmup, args.seed, dev, args.layers)
-    cpu = None if args.no_cpu_baseline or wl.is_mla else cpu_baseline(wl, t)
+    if args.workload in cpu_wanted and not wl.is_mla:
+        cpu_in[args.workload] = (wl, cpu_inputs(wl, t))
     del t
     torch.cuda.empty_cache()
     extras = []
     for name in [n for n in args.extra.split(",") if n and n != "none" and n != args.workload]:
-        fig, _, t = measure(name, args.steps, args.warmup, args.seed, dev, args.layers)
+        fig, xwl, t = measure(name, args.steps, args.warmup, args.seed, dev, args.layers)
         extras.append(fig)
+        if name in cpu_wanted and not xwl.is_mla:
+            cpu_in[name] = (xwl, cpu_inputs(xwl, t))
         del t
         torch.cuda.empty_cache()
+    cpu = {name: cpu_baseline(*cpu_in.pop(name)) for name in list(cpu_in)}
+    for fig in extras:
+        if fig["workload"] in cpu:
+            fig["cpu_baseline"] = cpu[fig["workload"]]
 
     result = {
         "metric": METRIC,
@@ -426,8 +460,8 @@ def main():
         "flops": primary["flops"],
         "workloads": extras,
     }
-    if cpu is not None:
-        result["cpu_baseline"] = cpu
+    if args.workload in cpu:
+        result["cpu_baseline"] = cpu[args.workload]
     print(json.dumps(result), flush=True)
 
 

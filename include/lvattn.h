@@ -29,7 +29,7 @@ extern "C" {
 #define LV_SCHEDULE_SERIAL 1
 #define LV_SCHEDULE_OVERLAP 2
 
-#define LV_ABI_VERSION 8
+#define LV_ABI_VERSION 9
 
 /* The last error message of the calling thread ("" if none). */
 const char* lv_last_error(void);
@@ -139,6 +139,38 @@ int lv_paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h, co
                        void* workspace, size_t workspace_bytes, int32_t schedule, int32_t prompt_workgroups,
                        int32_t flags, int32_t dtype, void* stream);
 
+/* Which kernels lv_paged_attention / lv_paged_attention_static launch for a step of this shape: the host-side
+ * decision those calls make, reported without launching anything (it reads the device's CU count and the kernels'
+ * occupancy, so it needs the device current). No counterpart in the reference, whose backends launch third-party
+ * kernels; for callers and tests that check which path a step takes (the per-step plan of
+ * lean_vllm/attention/flash_backend.py:141-182 is the nearest analogue). Arguments as lv_paged_attention's, plus
+ * has_cu_seqlens_q (whether cu_seqlens_q would be non-NULL). A step with no rows or tokens reports no kernels.
+ * two_streams = 1: the decode items run on the library's second stream beside the prompt launch (if that stream
+ * cannot be created, the call runs the two serially instead, with the same results). */
+#define LV_KERNEL_NONE 0
+#define LV_KERNEL_DECODE_LIST 1    /* one workgroup per decode item of the work list */
+#define LV_KERNEL_DECODE_BESIDE 2  /* persistent grid taking decode items by ticket, beside prompt_overlap */
+#define LV_KERNEL_DECODE_GRID 3    /* one workgroup per (row, split, kv head, head group); no work list (> 4096 rows) */
+#define LV_KERNEL_PROMPT_LIST 4    /* one workgroup per prompt item, on the whole GPU */
+#define LV_KERNEL_PROMPT_OVERLAP 5 /* persistent prompt workgroups on part of the CUs, beside the decode items */
+#define LV_KERNEL_MIXED_SMALL 6    /* prompt and decode items of a small mixed step in one launch */
+typedef struct lv_launch_info {
+  int32_t decode_kernel;      /* LV_KERNEL_*: the launch running the decode items */
+  int32_t decode_workgroups;  /* its grid (a bound: workgroups past the planned items exit at once) */
+  int32_t prompt_kernel;      /* LV_KERNEL_*: the launch running the prompt items (MIXED_SMALL: the same launch) */
+  int32_t prompt_workgroups;
+  int32_t kv_heads_per_item;  /* 1, or 2: a decode item reads two adjacent kv heads of each token */
+  int32_t two_streams;
+  int32_t keys_per_split;     /* keys per decode item */
+  int32_t max_splits;         /* the most decode items one row is split into */
+  int32_t splitk_merge;       /* 1: splitk_merge_kernel combines the rows split over several items */
+} lv_launch_info;
+int lv_paged_attention_launch_info(int32_t num_rows, int32_t num_tokens, int32_t num_heads, int32_t num_kv_heads,
+                                   int32_t head_dim, int32_t block_size, int64_t cache_stride_head,
+                                   int32_t has_cu_seqlens_q, int32_t max_seqlen_q, int32_t max_seqlen_k,
+                                   int32_t schedule, int32_t prompt_workgroups, int32_t flags, int32_t dtype,
+                                   lv_launch_info* info);
+
 /* The same step with no workspace argument and no allocation of any kind. No counterpart in the reference: for
  * callers that cannot call hipMalloc -- code under HIP graph capture, tight serving loops, harnesses that forbid
  * allocation. The work list, its counters and the split-K partials live in a static device array of
@@ -148,7 +180,10 @@ int lv_paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h, co
  * (the plan kernel zeroes the persistent grid's ticket), so no memset is recorded into a captured graph. Every call
  * on one GPU shares that GPU's array, which keeps the last call's contents: calls that overlap on one GPU (two
  * streams, two host threads, or a graph replay beside an eager call) race. Results equal lv_paged_attention's for
- * the same arguments. */
+ * the same arguments. Set-up: the first call on a device resolves the array's address there and creates the
+ * device's second stream and its two fork/join events (which lv_paged_attention creates at its first overlapped
+ * step); no device memory is allocated, and later calls create nothing. A caller that captures graphs makes one
+ * call on each device before capturing. */
 #define LV_STATIC_WORKSPACE_BYTES (16u << 20)
 int lv_paged_attention_static(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_cache,
                               const void* v_cache, int64_t cache_stride_block, int64_t cache_stride_token,

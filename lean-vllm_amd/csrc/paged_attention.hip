@@ -319,9 +319,10 @@ __global__ __launch_bounds__(256) void decode_list_kernel(AttnParams p) {
   decode_item<T, D, GS, HP, US>(p, it.x, it.y, kh * HP, qg, smem);
 }
 
-// Decode items of the work list on a persistent grid: each workgroup takes items by ticket (an atomic counter the
-// plan kernel zeroes), in list order, so the longest still go first. A fixed number of workgroups per CU lets a
-// mixed step's prompt workgroups stay resident beside them. The next ticket is drawn at the start of an item and
+// Decode items of the work list on a persistent grid beside a mixed step's prompt workgroups: each workgroup takes
+// items by ticket (an atomic counter the plan kernel zeroes), in list order, so the longest still go first. A
+// fixed number of workgroups per CU lets the prompt workgroups stay resident beside them (outside the overlap,
+// one workgroup per item measured as fast or faster). The next ticket is drawn at the start of an item and
 // published at its merge barrier; the merge alternates between two LDS buffers, so one barrier per item suffices.
 // The last workgroup to finish puts the ticket and the exit count back to zero, so the next layer of the step can
 // run on the same plan without a plan launch: every workgroup's ticket draws have returned (their values were
@@ -351,30 +352,18 @@ __device__ __forceinline__ void decode_persistent(const AttnParams& p) {
   }
 }
 
-// Alone on the GPU the grid holds two workgroups per CU, so their waves may take 256 registers (no spills; 1-2%
-// faster than under 128).
-template <typename T, int D, int GS>
-__global__ __launch_bounds__(256, 2) void decode_persistent_kernel(AttnParams p) {
-  decode_persistent<T, D, GS, 1>(p);
-}
-
-// Beside a mixed step's prompt workgroups (one per CU) two decode workgroups share each SIMD's 512 registers per
-// lane. As compiled, a prompt wave takes 193 (allocated as 200) and a decode wave 131 (136): 472 in all. The cap
-// below keeps the decode waves off the 256 a lone workgroup could take; the compiler rounds it to an occupancy level
-// (three waves per SIMD, 168). The 128 of four workgroups per CU would spill the D = 128 item. The grid asks for
-// three per CU: the CUs without a prompt workgroup take the third.
-template <typename T, int D, int GS, int HP>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_num_vgpr(160))) void decode_beside_kernel(AttnParams p) {
-  decode_persistent<T, D, GS, HP>(p);
-}
-// Pair items at D = 128 beside the prompt workgroups: 16-token wave tiles (8 load steps, twice the bytes in flight
-// per wave of the 8-token tile) at 210 registers, so one such workgroup shares a prompt CU and two fill the others
-// (the mixed step 2.934 -> 2.919 ms against the capped kernel at three per CU, same box, medians of 3).
+// Load steps of a wave tile: pair items at D = 128 hold 16-token wave tiles (8 load steps, twice the bytes in
+// flight per wave of the 8-token tile, about 210 registers); other shapes keep the kTile / HP default.
 template <int D, int HP>
-constexpr int kWideSteps = HP == 2 && D == 128 ? 8 : 0;  // load steps of a wave tile where registers allow 16 tokens
-template <typename T, int D, int GS>
-__global__ __launch_bounds__(256, 2) void decode_beside_pairs_kernel(AttnParams p) {
-  decode_persistent<T, D, GS, 2, kWideSteps<D, 2>>(p);
+constexpr int kWideSteps = HP == 2 && D == 128 ? 8 : 0;
+
+// Beside a mixed step's prompt workgroups (one per CU; a prompt wave takes 193 registers, allocated as 200) the
+// decode workgroups share each SIMD's 512 registers per lane: one pair-item workgroup at D = 128 (210) beside a
+// prompt wave and two on the other CUs; the smaller items of other shapes (131 or fewer) two beside a prompt wave
+// and three on the others. The grid asks for up to three per CU, as many as fit alone.
+template <typename T, int D, int GS, int HP>
+__global__ __launch_bounds__(256, 2) void decode_beside_kernel(AttnParams p) {
+  decode_persistent<T, D, GS, HP, kWideSteps<D, HP>>(p);
 }
 
 // TP: pages per 64-key prompt tile. TP > 0 (pages of a multiple of 64 keys, or of 32 or 16): the tiles stream
@@ -674,40 +663,22 @@ static int resident_per_cu() {
   return n;
 }
 
-// The decode items of a listed launch: a persistent grid of at most per_cu workgroups per CU taking items by
-// ticket (beside a mixed step's prompt workgroups a fixed share of every CU keeps both kernels resident), or one
-// workgroup per item -- for per_cu 0, for steps whose item bound is under eight items per persistent workgroup,
-// whose few short items finish sooner all at once than in rounds, and for items of kv-head pairs outside the
-// overlap: those ran faster one workgroup per item than on the persistent grid (same box, medians of 3: Qwen3-8B
-// batch-256 decode 0.727 against 0.771 ms, long-context 0.855 against 0.865, on 16-token pages 0.744 against
-// 0.783).
-template <typename T, int D, int GS, int HP, bool BESIDE = false>
-static void launch_decode(const AttnParams& p, const Shape& s, int per_cu, hipStream_t stream) {
-  const int items = s.max_decode_items * (p.hkv / HP) * p.qgroups;  // a bound: the plan lists no more
-  if constexpr (BESIDE || HP == 1) {
-    constexpr bool kWide = BESIDE && kWideSteps<D, HP> > 0;
-    int resident = 0;
-    if constexpr (kWide)
-      resident = resident_per_cu<decode_beside_pairs_kernel<T, D, GS>>();
-    else if constexpr (BESIDE)
-      resident = resident_per_cu<decode_beside_kernel<T, D, GS, HP>>();
-    else
-      resident = resident_per_cu<decode_persistent_kernel<T, D, GS>>();
-    const int grid = per_cu > 0 ? std::min(per_cu, resident) * device_cus() : 0;
-    if (grid > 0 && items >= 8 * grid) {
-      if constexpr (kWide)
-        hipLaunchKernelGGL((decode_beside_pairs_kernel<T, D, GS>), dim3(grid), dim3(256), 0, stream, p);
-      else if constexpr (BESIDE)
-        hipLaunchKernelGGL((decode_beside_kernel<T, D, GS, HP>), dim3(grid), dim3(256), 0, stream, p);
-      else
-        hipLaunchKernelGGL((decode_persistent_kernel<T, D, GS>), dim3(grid), dim3(256), 0, stream, p);
-      return;
-    }
-  }
-  // Pair items at D = 128 one workgroup per item take 16-token wave tiles too (two workgroups per CU instead of
-  // three of the 8-token tile: batch-256 decode 0.736 -> 0.728 ms, on 16-token pages 0.745 -> 0.738).
-  hipLaunchKernelGGL((decode_list_kernel<T, D, GS, HP, kWideSteps<D, HP>>), dim3(items), dim3(256), 0, stream, p);
-}
+// The kernels of one call, decided on the host from the step's shape (the same decision for a launch and for
+// lv_paged_attention_launch_info).
+struct StepKind {
+  bool listed;        // the step's items come from a device work list (at most kPlanMaxRows rows)
+  bool mixed;         // some row has more than one query
+  bool overlap;       // the caller's schedule lets prompt tiles run beside the decode items
+  bool prompts_only;  // the caller says every row has more than one query
+  int prompt_wgs;     // the caller's prompt share of the CUs in an overlap (0: the default)
+};
+struct Route {
+  int hp = 1;                                    // kv heads per decode item
+  int decode = LV_KERNEL_NONE, decode_grid = 0;  // the launch running the decode items, its workgroups
+  int prompt = LV_KERNEL_NONE, prompt_grid = 0;  // the launch running the prompt items (MIXED_SMALL: the same one)
+  bool two_streams = false;                      // decode items on the second stream beside prompt_overlap_kernel
+  bool merge = false;                            // splitk_merge_kernel after
+};
 
 // CUs that hold a prompt workgroup in an overlapped step: the caller's count clamped to [default, max] and
 // rounded down to a multiple of 8, or the default share for 0; never more than there are prompt items.
@@ -718,69 +689,124 @@ static int prompt_grid(const Shape& s, const AttnParams& p, int requested) {
   return std::min(s.max_prompt_items * p.hkv, n);
 }
 
-// The prompt items of a step with prompts, one workgroup per item, on the whole GPU.
-template <typename T, int D, int TP>
-static void launch_prompt_list(const AttnParams& p, const Shape& s, hipStream_t stream) {
-  hipLaunchKernelGGL((prompt_list_kernel<T, D, TP>), dim3(s.max_prompt_items * p.hkv), dim3(256), 0, stream, p);
+// The route of a step:
+// - a step of prompts: its prompt items one workgroup each on the whole GPU;
+// - more rows than the work list holds (decode only): one workgroup per (row, split, item head group), no list;
+// - a mixed step under the overlapped schedule whose workgroups (bounds: prompt bounds past a row's queries exit at
+//   once) fill the GPU at most kSmallStepRounds times: prompt and decode items in one launch (mixed_small_kernel);
+// - a larger one: prompt items on a persistent share of the CUs, decode items beside them on a second stream, on the
+//   persistent ticket grid where the item bound gives each of its workgroups at least eight items (else one
+//   workgroup per item: few short items finish sooner all at once than in rounds);
+// - otherwise (the serial schedule, or decode only): the prompt items on the whole GPU if any, then the decode items
+//   one workgroup each. Outside the overlap one workgroup per item measured as fast as the persistent grid or faster
+//   (Qwen3-8B batch-256 decode of kv-head pairs 0.727 against 0.771 ms, same box, medians of 3).
+template <typename T, int D, int GS, int TP, int HP>
+static Route route_of(const AttnParams& p, const Shape& s, const StepKind& k) {
+  Route r;
+  r.hp = HP;
+  const int ny = p.hkv / HP * p.qgroups;
+  const int cus = device_cus();
+  const int64_t pw = k.listed && k.mixed ? (int64_t)s.max_prompt_items * p.hkv : 0;
+  const int64_t dw = k.listed ? (int64_t)s.max_decode_items * ny : (int64_t)p.rows * p.max_splits * ny;
+  r.merge = p.max_splits > 1 && !k.prompts_only;
+  if (k.prompts_only) {
+    r.prompt = LV_KERNEL_PROMPT_LIST;
+    r.prompt_grid = (int)pw;
+  } else if (!k.listed) {
+    r.decode = LV_KERNEL_DECODE_GRID;
+    r.decode_grid = (int)dw;
+  } else if (k.mixed && k.overlap &&
+             pw + dw <= (int64_t)kSmallStepRounds * resident_per_cu<mixed_small_kernel<T, D, GS, TP, HP>>() * cus) {
+    r.prompt = r.decode = LV_KERNEL_MIXED_SMALL;
+    r.prompt_grid = (int)pw;
+    r.decode_grid = (int)dw;
+  } else if (k.mixed && k.overlap) {
+    r.two_streams = true;
+    r.prompt = LV_KERNEL_PROMPT_OVERLAP;
+    r.prompt_grid = prompt_grid(s, p, k.prompt_wgs);
+    const int grid = std::min(kOverlapDecodeWgs, resident_per_cu<decode_beside_kernel<T, D, GS, HP>>()) * cus;
+    r.decode = dw >= 8 * (int64_t)grid ? LV_KERNEL_DECODE_BESIDE : LV_KERNEL_DECODE_LIST;
+    r.decode_grid = r.decode == LV_KERNEL_DECODE_BESIDE ? grid : (int)dw;
+  } else {
+    if (k.mixed) {
+      r.prompt = LV_KERNEL_PROMPT_LIST;
+      r.prompt_grid = (int)pw;
+    }
+    r.decode = LV_KERNEL_DECODE_LIST;
+    r.decode_grid = (int)dw;
+  }
+  return r;
+}
+
+// The decode launch of a route on `stream`.
+template <typename T, int D, int GS, int HP>
+static void launch_decode(const AttnParams& p, const Route& r, hipStream_t stream) {
+  if (r.decode == LV_KERNEL_DECODE_BESIDE)
+    hipLaunchKernelGGL((decode_beside_kernel<T, D, GS, HP>), dim3(r.decode_grid), dim3(256), 0, stream, p);
+  else if (r.decode == LV_KERNEL_DECODE_GRID)
+    hipLaunchKernelGGL((decode_grid_kernel<T, D, GS, HP>), dim3(p.rows * p.max_splits, p.hkv / HP * p.qgroups),
+                       dim3(256), 0, stream, p);
+  else if (r.decode == LV_KERNEL_DECODE_LIST)
+    hipLaunchKernelGGL((decode_list_kernel<T, D, GS, HP, kWideSteps<D, HP>>), dim3(r.decode_grid), dim3(256), 0,
+                       stream, p);
 }
 
 // A step's kernels after the plan. An overlapped mixed step forks the decode items onto the device's second stream
 // and joins it back into `stream` with events; if the second stream cannot be set up, or the fork's record or wait
 // fails before anything is launched, the step runs serially instead (the same results). A failure after the decode
-// launch leaves the two streams unordered and is returned as LV_EHIP.
+// launch leaves the two streams unordered and is returned as LV_EHIP. With `info` set nothing is launched: the
+// route is reported instead.
 template <typename T, int D, int GS, int TP, int HP>
-static int launch(const AttnParams& p, bool listed, bool mixed, bool overlap, int prompt_wgs, const Shape& s,
-                  hipStream_t stream, bool prompts_only) {
-  const int ny = p.hkv / HP * p.qgroups;
-  if (prompts_only) {  // a step of prompts: the prompt tiles on the whole GPU, nothing else
-    launch_prompt_list<T, D, TP>(p, s, stream);
+static int launch(const AttnParams& p, const Shape& s, const StepKind& k, hipStream_t stream, Route* info) {
+  const Route r = route_of<T, D, GS, TP, HP>(p, s, k);
+  if (info) {
+    *info = r;
     return LV_OK;
   }
-  if (overlap && listed && mixed) {
-    // A step whose workgroups (bounds: most prompt bounds exit at once) fill the GPU at most kSmallStepRounds times
-    // runs as one launch.
-    const int64_t pw = (int64_t)s.max_prompt_items * p.hkv, dw = (int64_t)s.max_decode_items * ny;
-    const int resident = resident_per_cu<mixed_small_kernel<T, D, GS, TP, HP>>();
-    if (pw + dw <= (int64_t)kSmallStepRounds * resident * device_cus()) {
-      hipLaunchKernelGGL((mixed_small_kernel<T, D, GS, TP, HP>), dim3(pw + dw), dim3(256), 0, stream, p, (int32_t)pw);
-      LV_LAUNCH_CHECK("mixed_small_kernel");
-      if (p.max_splits > 1)
-        hipLaunchKernelGGL((splitk_merge_kernel<T, D>), dim3(p.rows, p.hq), dim3(64), 0, stream, p);
-      return LV_OK;
-    }
-  }
-  SideStream* side = overlap && listed && mixed ? side_stream() : nullptr;
-  bool forked = false;
-  if (side) {
-    // Decode items go to the second stream first, then the prompt items to the caller's stream: the prompt
-    // workgroups (one per CU) are dispatched as soon as the plan ends, the decode workgroups fill the rest.
-    const int grid = prompt_grid(s, p, prompt_wgs);
-    std::lock_guard<std::mutex> g(side->lock);
-    if (hipEventRecord(side->fork, stream) == hipSuccess &&
-        hipStreamWaitEvent(side->stream, side->fork, 0) == hipSuccess) {
-      forked = true;
-      launch_decode<T, D, GS, HP, true>(p, s, kOverlapDecodeWgs, side->stream);
-      LV_LAUNCH_CHECK("decode_persistent_kernel");
-      LV_HIP_CHECK(hipEventRecord(side->join, side->stream));
-      constexpr int pad = std::max(0, kOverlapLds - std::max(1, kRingOf<TP>) * PromptSmem<D, D, (TP > 1)>::kBytes);
-      hipLaunchKernelGGL((prompt_overlap_kernel<T, D, TP>), dim3(grid), dim3(256), pad, stream, p);
-      LV_LAUNCH_CHECK("prompt_overlap_kernel");
-      LV_HIP_CHECK(hipStreamWaitEvent(stream, side->join, 0));
-    } else {
-      (void)hipGetLastError();  // the failed record or wait: fall back to the serial schedule
-    }
-  }
-  if (forked) {
-  } else if (listed && mixed) {
-    launch_prompt_list<T, D, TP>(p, s, stream);
-    launch_decode<T, D, GS, HP>(p, s, kDecodeWgs, stream);
-  } else if (listed) {
-    launch_decode<T, D, GS, HP>(p, s, kDecodeWgs, stream);
+  if (r.prompt == LV_KERNEL_MIXED_SMALL) {
+    hipLaunchKernelGGL((mixed_small_kernel<T, D, GS, TP, HP>), dim3(r.prompt_grid + r.decode_grid), dim3(256), 0,
+                       stream, p, (int32_t)r.prompt_grid);
+    LV_LAUNCH_CHECK("mixed_small_kernel");
   } else {
-    hipLaunchKernelGGL((decode_grid_kernel<T, D, GS, HP>), dim3(p.rows * p.max_splits, ny), dim3(256), 0, stream, p);
+    SideStream* side = r.two_streams ? side_stream() : nullptr;
+    bool forked = false;
+    if (side) {
+      // Decode items go to the second stream first, then the prompt items to the caller's stream: the prompt
+      // workgroups (one per CU) are dispatched as soon as the plan ends, the decode workgroups fill the rest.
+      std::lock_guard<std::mutex> g(side->lock);
+      if (hipEventRecord(side->fork, stream) == hipSuccess &&
+          hipStreamWaitEvent(side->stream, side->fork, 0) == hipSuccess) {
+        forked = true;
+        launch_decode<T, D, GS, HP>(p, r, side->stream);
+        LV_LAUNCH_CHECK("decode kernel beside the prompt tiles");
+        LV_HIP_CHECK(hipEventRecord(side->join, side->stream));
+        constexpr int pad = std::max(0, kOverlapLds - std::max(1, kRingOf<TP>) * PromptSmem<D, D, (TP > 1)>::kBytes);
+        hipLaunchKernelGGL((prompt_overlap_kernel<T, D, TP>), dim3(r.prompt_grid), dim3(256), pad, stream, p);
+        LV_LAUNCH_CHECK("prompt_overlap_kernel");
+        LV_HIP_CHECK(hipStreamWaitEvent(stream, side->join, 0));
+      } else {
+        (void)hipGetLastError();  // the failed record or wait: fall back to the serial schedule
+      }
+    }
+    if (!forked) {
+      if (r.prompt != LV_KERNEL_NONE)  // the serial schedule (or its fallback): prompt items on the whole GPU
+        hipLaunchKernelGGL((prompt_list_kernel<T, D, TP>), dim3(s.max_prompt_items * p.hkv), dim3(256), 0, stream,
+                           p);
+      if (r.decode != LV_KERNEL_NONE) {
+        Route serial = r;
+        if (serial.decode == LV_KERNEL_DECODE_BESIDE) {  // the fallback: one workgroup per item
+          serial.decode = LV_KERNEL_DECODE_LIST;
+          serial.decode_grid = s.max_decode_items * (p.hkv / HP) * p.qgroups;
+        }
+        launch_decode<T, D, GS, HP>(p, serial, stream);
+      }
+      LV_LAUNCH_CHECK("paged attention kernels");
+    }
   }
-  if (p.max_splits > 1)
+  if (r.merge) {
     hipLaunchKernelGGL((splitk_merge_kernel<T, D>), dim3(p.rows, p.hq), dim3(64), 0, stream, p);
+    LV_LAUNCH_CHECK("splitk_merge_kernel");
+  }
   return LV_OK;
 }
 
@@ -794,13 +820,12 @@ static int tile_pages(int block_size) {
 }
 
 template <typename T, int D, int GS, int HP>
-static int launch_tp(const AttnParams& p, bool listed, bool mixed, bool overlap, int prompt_wgs, const Shape& s,
-                     hipStream_t stream, bool prompts_only) {
+static int launch_tp(const AttnParams& p, const Shape& s, const StepKind& k, hipStream_t stream, Route* info) {
   switch (tile_pages((int)p.bs.d)) {
-    case 1: return launch<T, D, GS, 1, HP>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
-    case 2: return launch<T, D, GS, 2, HP>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
-    case 4: return launch<T, D, GS, 4, HP>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
-    default: return launch<T, D, GS, 0, HP>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
+    case 1: return launch<T, D, GS, 1, HP>(p, s, k, stream, info);
+    case 2: return launch<T, D, GS, 2, HP>(p, s, k, stream, info);
+    case 4: return launch<T, D, GS, 4, HP>(p, s, k, stream, info);
+    default: return launch<T, D, GS, 0, HP>(p, s, k, stream, info);
   }
 }
 
@@ -809,30 +834,31 @@ static int launch_tp(const AttnParams& p, bool listed, bool mixed, bool overlap,
 // math-free stream of 512-byte pieces at a 2 KB stride reads 7.15 TB/s on an MI355X, of 256-byte pieces
 // 6.5-6.7 TB/s). The split of a row's keys stays as planned, so such items are half as many and twice as long;
 // steps of fewer than kPairItems one-head items per CU (a few short rows, latency-bound) keep one head per item.
+// A lane addresses the second head's row with a 32-bit offset (the head stride) inside its tile, so pairs also need
+// a head stride under 2^30 bytes.
 constexpr int kPairItems = 8;
 template <typename T, int D, int GS>
-static int launch_hp(const AttnParams& p, bool listed, bool mixed, bool overlap, int prompt_wgs, const Shape& s,
-                     hipStream_t stream, bool prompts_only) {
-  const int64_t items = (int64_t)(listed ? s.max_decode_items : p.rows * p.max_splits) * p.hkv * p.qgroups;
-  if (p.hkv % 2 == 0 && items >= (int64_t)kPairItems * device_cus())
-    return launch_tp<T, D, GS, 2>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
-  return launch_tp<T, D, GS, 1>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
+static int launch_hp(const AttnParams& p, const Shape& s, const StepKind& k, hipStream_t stream, Route* info) {
+  const int64_t items = (int64_t)(k.listed ? s.max_decode_items : p.rows * p.max_splits) * p.hkv * p.qgroups;
+  if (p.hkv % 2 == 0 && p.c_sh >= 0 && p.c_sh < ((int64_t)1 << 30) && items >= (int64_t)kPairItems * device_cus())
+    return launch_tp<T, D, GS, 2>(p, s, k, stream, info);
+  return launch_tp<T, D, GS, 1>(p, s, k, stream, info);
 }
 
 template <typename T, int D>
-static int launch_gs(const AttnParams& p, int gs, bool listed, bool mixed, bool overlap, int prompt_wgs,
-                     const Shape& s, hipStream_t stream, bool prompts_only) {
-  if (gs == 4) return launch_hp<T, D, 4>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
-  if (gs == 2) return launch_hp<T, D, 2>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
-  return launch_hp<T, D, 1>(p, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
+static int launch_gs(const AttnParams& p, int gs, const Shape& s, const StepKind& k, hipStream_t stream,
+                     Route* info) {
+  if (gs == 4) return launch_hp<T, D, 4>(p, s, k, stream, info);
+  if (gs == 2) return launch_hp<T, D, 2>(p, s, k, stream, info);
+  return launch_hp<T, D, 1>(p, s, k, stream, info);
 }
 
 template <typename T>
-static int launch_d(const AttnParams& p, int d, int gs, bool listed, bool mixed, bool overlap, int prompt_wgs,
-                    const Shape& s, hipStream_t stream, bool prompts_only) {
+static int launch_d(const AttnParams& p, int d, int gs, const Shape& s, const StepKind& k, hipStream_t stream,
+                    Route* info) {
   switch (d) {
-    case 64: return launch_gs<T, 64>(p, gs, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
-    case 128: return launch_gs<T, 128>(p, gs, listed, mixed, overlap, prompt_wgs, s, stream, prompts_only);
+    case 64: return launch_gs<T, 64>(p, gs, s, k, stream, info);
+    case 128: return launch_gs<T, 128>(p, gs, s, k, stream, info);
     default: set_error("paged_attention: head_dim %d is not 64 or 128", d); return LV_EINVAL;
   }
 }
@@ -841,7 +867,8 @@ static int launch_d(const AttnParams& p, int d, int gs, bool listed, bool mixed,
 // The workspace of lv_paged_attention_static: a file-scope device array (each GPU that loads the library holds its
 // own copy until the process ends). Host code must not pass the array's name to a kernel -- in host code it is a
 // stand-in, not a device address; its address on the current device comes from hipGetSymbolAddress, resolved once
-// per device and kept.
+// per device and kept. The same set-up creates the device's second stream and its fork/join events, so that no
+// later call creates anything.
 static __device__ __align__(256) char scratch[LV_STATIC_WORKSPACE_BYTES];
 
 static void* scratch_on_current_device() {
@@ -864,6 +891,10 @@ static void* scratch_on_current_device() {
     if (r != hipSuccess || !ptr) {
       set_error("paged_attention_static: hipGetSymbolAddress of the static workspace failed on device %d: %s", dev,
                 hipGetErrorString(r));
+      return nullptr;
+    }
+    if (!side_stream()) {
+      set_error("paged_attention_static: the second stream of device %d could not be created", dev);
       return nullptr;
     }
     addr[dev] = ptr;
@@ -889,13 +920,27 @@ constexpr int kPlanRecords = 32;
 static std::mutex g_plan_lock;
 static PlanSig g_plans[kPlanRecords];
 
-// True if `sig`'s workspace holds the plan `sig` describes; otherwise records that it is about to.
+// True if a caller asks to reuse the plan in `sig`'s workspace and that workspace's last plan is the one `sig`
+// describes.
 static bool plan_is_current(const PlanSig& sig, bool reuse) {
+  if (!reuse) return false;
+  std::lock_guard<std::mutex> g(g_plan_lock);
+  for (int i = 0; i < kPlanRecords; ++i)
+    if (g_plans[i].ws == sig.ws) return g_plans[i] == sig;
+  return false;
+}
+
+// Records what workspace `ws` now holds: the plan `sig` (after its launch was accepted), or nothing (sig null: a
+// call that failed after choosing to plan, whose list may never be written).
+static void record_plan(const void* ws, const PlanSig* sig) {
   std::lock_guard<std::mutex> g(g_plan_lock);
   int slot = -1;
   for (int i = 0; i < kPlanRecords; ++i)
-    if (g_plans[i].ws == sig.ws) slot = i;
-  if (reuse && slot >= 0 && g_plans[slot] == sig) return true;
+    if (g_plans[i].ws == ws) slot = i;
+  if (!sig) {
+    if (slot >= 0) g_plans[slot] = PlanSig{};
+    return;
+  }
   if (slot < 0) {  // a new workspace: take a free record, else the first
     slot = 0;
     for (int i = 0; i < kPlanRecords; ++i)
@@ -904,8 +949,63 @@ static bool plan_is_current(const PlanSig& sig, bool reuse) {
         break;
       }
   }
-  g_plans[slot] = sig;
-  return false;
+  g_plans[slot] = *sig;
+}
+
+// The checks on a step's shape and options, shared by the call and the launch-info query.
+static int check_shape(int32_t num_rows, int32_t num_tokens, int32_t num_heads, int32_t num_kv_heads,
+                       int32_t head_dim, int32_t block_size, bool has_cu_q, int32_t max_seqlen_q,
+                       int32_t max_seqlen_k, int32_t schedule, int32_t prompt_workgroups, int32_t flags,
+                       int32_t dtype) {
+  LV_REQUIRE(dtype == LV_DTYPE_BF16 || dtype == LV_DTYPE_F16, "paged_attention: dtype %d is not bf16 or fp16",
+             dtype);
+  LV_REQUIRE(num_rows >= 0 && num_tokens >= 0, "paged_attention: negative row or token count");
+  LV_REQUIRE(schedule == LV_SCHEDULE_AUTO || schedule == LV_SCHEDULE_SERIAL || schedule == LV_SCHEDULE_OVERLAP,
+             "paged_attention: unknown schedule %d", schedule);
+  LV_REQUIRE(prompt_workgroups >= 0, "paged_attention: negative prompt_workgroups %d", prompt_workgroups);
+  LV_REQUIRE((flags & ~(LV_ATTN_REUSE_PLAN | LV_ATTN_PROMPTS_ONLY)) == 0, "paged_attention: unknown flags 0x%x",
+             flags);
+  LV_REQUIRE(!(flags & LV_ATTN_PROMPTS_ONLY) || (has_cu_q && max_seqlen_q > 1),
+             "paged_attention: LV_ATTN_PROMPTS_ONLY needs cu_seqlens_q and max_seqlen_q > 1");
+  if (num_rows == 0 || num_tokens == 0) return LV_OK;
+  LV_REQUIRE(num_heads > 0 && num_kv_heads > 0 && num_heads % num_kv_heads == 0,
+             "paged_attention: %d query heads do not group over %d key heads", num_heads, num_kv_heads);
+  LV_REQUIRE(num_heads / num_kv_heads <= kPrefillRows, "paged_attention: query group %d exceeds %d",
+             num_heads / num_kv_heads, kPrefillRows);
+  LV_REQUIRE(head_dim == 64 || head_dim == 128, "paged_attention: head_dim %d is not 64 or 128", head_dim);
+  LV_REQUIRE(block_size > 0 && block_size % kTile == 0, "paged_attention: block_size %d is not a multiple of %d",
+             block_size, kTile);
+  LV_REQUIRE(has_cu_q || num_tokens == num_rows, "paged_attention: without cu_seqlens_q, T (%d) must equal B (%d)",
+             num_tokens, num_rows);
+  LV_REQUIRE(max_seqlen_k >= 0, "paged_attention: negative max_seqlen_k");
+  LV_REQUIRE(!(has_cu_q && max_seqlen_q > 1) || num_rows <= kPlanMaxRows,
+             "paged_attention: a step with prompts holds at most %d rows, got %d", kPlanMaxRows, num_rows);
+  return LV_OK;
+}
+
+static StepKind step_kind(int32_t num_rows, bool has_cu_q, int32_t max_seqlen_q, int32_t schedule,
+                          int32_t prompt_workgroups, int32_t flags) {
+  StepKind k;
+  k.mixed = has_cu_q && max_seqlen_q > 1;
+  k.listed = num_rows <= kPlanMaxRows;
+  k.overlap = schedule != LV_SCHEDULE_SERIAL;
+  k.prompts_only = (flags & LV_ATTN_PROMPTS_ONLY) != 0;
+  k.prompt_wgs = prompt_workgroups;
+  return k;
+}
+
+// The shape part of a step's parameters (what the route depends on).
+static void shape_params(AttnParams& p, const Shape& s, int32_t num_rows, int32_t num_heads, int32_t num_kv_heads,
+                         int32_t block_size, int64_t cache_stride_head) {
+  p.bs = FastDiv::make((uint32_t)block_size);
+  p.c_sh = cache_stride_head * 2;
+  p.rows = num_rows;
+  p.hq = num_heads;
+  p.hkv = num_kv_heads;
+  p.group = num_heads / num_kv_heads;
+  p.qgroups = p.group / s.gs;
+  p.split = s.split;
+  p.max_splits = s.max_splits;
 }
 
 // One step, with the workspace given (workspace != nullptr or an empty shape) or, for static_ws, the device's
@@ -919,29 +1019,12 @@ static int paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h
                            int32_t max_seqlen_k, void* out, int64_t out_stride_t, int64_t out_stride_h,
                            void* workspace, size_t workspace_bytes, bool static_ws, int32_t schedule,
                            int32_t prompt_workgroups, int32_t flags, int32_t dtype, void* stream) {
-  LV_REQUIRE(dtype == LV_DTYPE_BF16 || dtype == LV_DTYPE_F16, "paged_attention: dtype %d is not bf16 or fp16",
-             dtype);
-  LV_REQUIRE(num_rows >= 0 && num_tokens >= 0, "paged_attention: negative row or token count");
-  LV_REQUIRE(schedule == LV_SCHEDULE_AUTO || schedule == LV_SCHEDULE_SERIAL || schedule == LV_SCHEDULE_OVERLAP,
-             "paged_attention: unknown schedule %d", schedule);
-  LV_REQUIRE(prompt_workgroups >= 0, "paged_attention: negative prompt_workgroups %d", prompt_workgroups);
-  LV_REQUIRE((flags & ~(LV_ATTN_REUSE_PLAN | LV_ATTN_PROMPTS_ONLY)) == 0, "paged_attention: unknown flags 0x%x",
-             flags);
-  LV_REQUIRE(!(flags & LV_ATTN_PROMPTS_ONLY) || (cu_seqlens_q && max_seqlen_q > 1),
-             "paged_attention: LV_ATTN_PROMPTS_ONLY needs cu_seqlens_q and max_seqlen_q > 1");
-  if (num_rows == 0 || num_tokens == 0) return LV_OK;
-  LV_REQUIRE(num_heads > 0 && num_kv_heads > 0 && num_heads % num_kv_heads == 0,
-             "paged_attention: %d query heads do not group over %d key heads", num_heads, num_kv_heads);
-  LV_REQUIRE(num_heads / num_kv_heads <= kPrefillRows, "paged_attention: query group %d exceeds %d",
-             num_heads / num_kv_heads, kPrefillRows);
-  LV_REQUIRE(head_dim == 64 || head_dim == 128, "paged_attention: head_dim %d is not 64 or 128", head_dim);
-  LV_REQUIRE(block_size > 0 && block_size % kTile == 0, "paged_attention: block_size %d is not a multiple of %d",
-             block_size, kTile);
+  const int rc0 = check_shape(num_rows, num_tokens, num_heads, num_kv_heads, head_dim, block_size,
+                              cu_seqlens_q != nullptr, max_seqlen_q, max_seqlen_k, schedule, prompt_workgroups,
+                              flags, dtype);
+  if (rc0 != LV_OK || num_rows == 0 || num_tokens == 0) return rc0;
   LV_REQUIRE(q && k_cache && v_cache && out && block_tables, "paged_attention: null tensor pointer");
   LV_REQUIRE(seqlens_k || cu_seqlens_k, "paged_attention: neither key lengths nor cu_seqlens_k given");
-  LV_REQUIRE(cu_seqlens_q || num_tokens == num_rows, "paged_attention: without cu_seqlens_q, T (%d) must equal B (%d)",
-             num_tokens, num_rows);
-  LV_REQUIRE(max_seqlen_k >= 0, "paged_attention: negative max_seqlen_k");
   // 16-byte rows: q, out and cache head rows are read and written as 16-byte vectors.
   LV_REQUIRE(aligned(q, 16) && aligned(out, 16) && aligned(k_cache, 16) && aligned(v_cache, 16) &&
                  (q_stride_t * 2) % 16 == 0 && (q_stride_h * 2) % 16 == 0 && (out_stride_t * 2) % 16 == 0 &&
@@ -952,11 +1035,8 @@ static int paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h
   LV_REQUIRE(cache_stride_token >= 0 && (int64_t)kTile * cache_stride_token * 2 < (int64_t)1 << 30,
              "paged_attention: cache token stride %lld is negative or too large", (long long)cache_stride_token);
   LV_REQUIRE(scale > 0.f, "paged_attention: the softmax scale must be positive, got %g", (double)scale);
-  const bool mixed = cu_seqlens_q != nullptr && max_seqlen_q > 1;
-  LV_REQUIRE(!mixed || num_rows <= kPlanMaxRows, "paged_attention: a step with prompts holds at most %d rows, got %d",
-             kPlanMaxRows, num_rows);
-  const bool listed = num_rows <= kPlanMaxRows;
-  const Shape s = plan_shape(num_rows, num_tokens, num_heads, num_kv_heads, head_dim, max_seqlen_k, listed);
+  const StepKind kind = step_kind(num_rows, cu_seqlens_q != nullptr, max_seqlen_q, schedule, prompt_workgroups, flags);
+  const Shape s = plan_shape(num_rows, num_tokens, num_heads, num_kv_heads, head_dim, max_seqlen_k, kind.listed);
   if (static_ws) {
     LV_REQUIRE(s.bytes <= (size_t)LV_STATIC_WORKSPACE_BYTES,
                "paged_attention_static: this step needs %zu bytes of workspace; the static workspace holds %zu "
@@ -971,6 +1051,7 @@ static int paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h
   LV_REQUIRE(aligned(workspace, 256), "paged_attention: workspace must be 256-byte aligned");
 
   AttnParams p{};
+  shape_params(p, s, num_rows, num_heads, num_kv_heads, block_size, cache_stride_head);
   p.q = (const char*)q;
   p.q_st = q_stride_t * 2;
   p.q_sh = q_stride_h * 2;
@@ -978,40 +1059,31 @@ static int paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h
   p.v_cache = (const char*)v_cache;
   p.c_sb = cache_stride_block * 2;
   p.c_st = cache_stride_token * 2;
-  p.c_sh = cache_stride_head * 2;
   p.v_st = p.c_st;
   p.v_sh = p.c_sh;
   p.paged = true;
   p.causal = 1;
-  p.bs = FastDiv::make((uint32_t)block_size);
   p.tables = block_tables;
   p.t_stride = table_stride;
   p.cu_q = cu_seqlens_q;
   p.lens_k = seqlens_k;
   p.cu_k = cu_seqlens_k;
-  p.rows = num_rows;
-  p.hq = num_heads;
-  p.hkv = num_kv_heads;
-  p.group = num_heads / num_kv_heads;
-  p.qgroups = p.group / s.gs;
   p.scale_log2 = scale * kLog2e;
   p.out = (char*)out;
   p.o_st = out_stride_t * 2;
   p.o_sh = out_stride_h * 2;
-  p.split = s.split;
-  p.max_splits = s.max_splits;
   char* ws = (char*)workspace;
   p.part_lse = s.max_splits > 1 ? reinterpret_cast<float*>(ws + s.lse_off) : nullptr;
   p.part_o = s.max_splits > 1 ? reinterpret_cast<float*>(ws + s.o_off) : nullptr;
-  p.items = listed ? reinterpret_cast<const int2*>(ws + s.items_off) : nullptr;
-  p.n_items = listed ? reinterpret_cast<const int32_t*>(ws + s.count_off) : nullptr;
-  p.ticket = listed ? reinterpret_cast<int32_t*>(ws + s.count_off) + 2 : nullptr;
+  p.items = kind.listed ? reinterpret_cast<const int2*>(ws + s.items_off) : nullptr;
+  p.n_items = kind.listed ? reinterpret_cast<const int32_t*>(ws + s.count_off) : nullptr;
+  p.ticket = kind.listed ? reinterpret_cast<int32_t*>(ws + s.count_off) + 2 : nullptr;
 
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int qp = kPrefillRows / p.group;
   PlanSig sig;
   sig.ws = workspace;
-  sig.cu_q = mixed ? cu_seqlens_q : nullptr;
+  sig.cu_q = kind.mixed ? cu_seqlens_q : nullptr;
   sig.lens = seqlens_k;
   sig.cu_k = cu_seqlens_k;
   sig.rows = num_rows;
@@ -1021,22 +1093,25 @@ static int paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h
   sig.qp = qp;
   sig.max_items = s.max_items;
   sig.bytes = (int64_t)s.bytes;
-  sig.mixed = mixed;
-  const bool overlap = schedule != LV_SCHEDULE_SERIAL;
-  const bool prompts_only = (flags & LV_ATTN_PROMPTS_ONLY) != 0;
-  sig.last_first = prompts_only || !overlap;  // prompt items with the GPU to themselves: last tile first
-  if (listed && !plan_is_current(sig, (flags & LV_ATTN_REUSE_PLAN) != 0)) {
-    hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kScanThreads), 0, st, mixed ? cu_seqlens_q : nullptr, seqlens_k,
-                       cu_seqlens_k, num_rows, s.split, qp, s.max_items, (int32_t)sig.last_first,
+  sig.mixed = kind.mixed;
+  sig.last_first = kind.prompts_only || !kind.overlap;  // prompt items with the GPU to themselves: last tile first
+  bool planned = false;
+  if (kind.listed && !plan_is_current(sig, (flags & LV_ATTN_REUSE_PLAN) != 0)) {
+    record_plan(workspace, nullptr);  // until this plan's launch is accepted, the workspace holds no plan
+    hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kScanThreads), 0, st, kind.mixed ? cu_seqlens_q : nullptr,
+                       seqlens_k, cu_seqlens_k, num_rows, s.split, qp, s.max_items, (int32_t)sig.last_first,
                        reinterpret_cast<int2*>(ws + s.items_off), reinterpret_cast<int32_t*>(ws + s.count_off));
     LV_LAUNCH_CHECK("plan_kernel");
+    planned = true;
   }
-  const int rc =
-      dtype == LV_DTYPE_BF16
-          ? launch_d<BF16>(p, head_dim, s.gs, listed, mixed, overlap, prompt_workgroups, s, st, prompts_only)
-          : launch_d<F16>(p, head_dim, s.gs, listed, mixed, overlap, prompt_workgroups, s, st, prompts_only);
-  if (rc != LV_OK) return rc;
-  LV_LAUNCH_CHECK("paged_attention_kernel");
+  const int rc = dtype == LV_DTYPE_BF16 ? launch_d<BF16>(p, head_dim, s.gs, s, kind, st, nullptr)
+                                        : launch_d<F16>(p, head_dim, s.gs, s, kind, st, nullptr);
+  if (rc != LV_OK) {
+    // A failed launch may leave the persistent grid's ticket unreset: the next call on this workspace plans again.
+    record_plan(workspace, nullptr);
+    return rc;
+  }
+  if (planned) record_plan(workspace, &sig);
   return LV_OK;
 }
 
@@ -1051,6 +1126,38 @@ extern "C" size_t lv_paged_attention_workspace_bytes(int32_t num_rows, int32_t n
   const bool mixed = decode_only == 0;
   const bool listed = mixed || num_rows <= kPlanMaxRows;
   return plan_shape(num_rows, num_tokens, num_heads, num_kv_heads, head_dim, max_seqlen_k, listed).bytes;
+}
+
+extern "C" int lv_paged_attention_launch_info(int32_t num_rows, int32_t num_tokens, int32_t num_heads,
+                                              int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                              int64_t cache_stride_head, int32_t has_cu_seqlens_q,
+                                              int32_t max_seqlen_q, int32_t max_seqlen_k, int32_t schedule,
+                                              int32_t prompt_workgroups, int32_t flags, int32_t dtype,
+                                              lv_launch_info* info) {
+  LV_REQUIRE(info, "paged_attention_launch_info: info is null");
+  *info = lv_launch_info{};
+  const int rc0 = check_shape(num_rows, num_tokens, num_heads, num_kv_heads, head_dim, block_size,
+                              has_cu_seqlens_q != 0, max_seqlen_q, max_seqlen_k, schedule, prompt_workgroups, flags,
+                              dtype);
+  if (rc0 != LV_OK || num_rows == 0 || num_tokens == 0) return rc0;
+  const StepKind kind = step_kind(num_rows, has_cu_seqlens_q != 0, max_seqlen_q, schedule, prompt_workgroups, flags);
+  const Shape s = plan_shape(num_rows, num_tokens, num_heads, num_kv_heads, head_dim, max_seqlen_k, kind.listed);
+  AttnParams p{};
+  shape_params(p, s, num_rows, num_heads, num_kv_heads, block_size, cache_stride_head);
+  Route r;
+  const int rc = dtype == LV_DTYPE_BF16 ? launch_d<BF16>(p, head_dim, s.gs, s, kind, nullptr, &r)
+                                        : launch_d<F16>(p, head_dim, s.gs, s, kind, nullptr, &r);
+  if (rc != LV_OK) return rc;
+  info->decode_kernel = r.decode;
+  info->decode_workgroups = r.decode_grid;
+  info->prompt_kernel = r.prompt;
+  info->prompt_workgroups = r.prompt_grid;
+  info->kv_heads_per_item = r.hp;
+  info->two_streams = r.two_streams;
+  info->keys_per_split = s.split;
+  info->max_splits = s.max_splits;
+  info->splitk_merge = r.merge;
+  return LV_OK;
 }
 
 extern "C" int lv_paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_cache,

@@ -31,6 +31,9 @@ _PROTOTYPES = {
                                           c_int64, _P, _P, _P, c_int32, c_int32, c_int32, c_int32, c_int32,
                                           c_float, c_int32, c_int32, _P, c_int64, c_int64, _P, c_size_t,
                                           c_int32, c_int32, c_int32, c_int32, _P]),
+    "lv_paged_attention_launch_info": (ctypes.c_int, [c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_int64,
+                                                      c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,
+                                                      _P]),
     "lv_paged_attention_static": (ctypes.c_int, [_P, c_int64, c_int64, _P, _P, c_int64, c_int64, c_int64, c_int32,
                                                  _P, c_int64, _P, _P, _P, c_int32, c_int32, c_int32, c_int32,
                                                  c_int32, c_float, c_int32, c_int32, _P, c_int64, c_int64, c_int32,
@@ -53,6 +56,26 @@ _PROTOTYPES = {
 
 LV_OK, LV_EINVAL, LV_EHIP = 0, 1, 2
 DTYPES = {torch.bfloat16: 0, torch.float16: 1}
+# LV_KERNEL_* of lv_launch_info: the launches a paged-attention step makes
+KERNELS = {0: "none", 1: "decode_list", 2: "decode_beside", 3: "decode_grid", 4: "prompt_list", 5: "prompt_overlap",
+           6: "mixed_small"}
+
+
+class LaunchInfo(ctypes.Structure):
+    """``lv_launch_info`` of include/lvattn.h."""
+
+    _fields_ = [(name, c_int32) for name in ("decode_kernel", "decode_workgroups", "prompt_kernel",
+                                              "prompt_workgroups", "kv_heads_per_item", "two_streams",
+                                              "keys_per_split", "max_splits", "splitk_merge")]
+
+    def as_dict(self) -> dict:
+        d = {name: getattr(self, name) for name, _ in self._fields_}
+        d["decode_kernel"] = KERNELS[d["decode_kernel"]]
+        d["prompt_kernel"] = KERNELS[d["prompt_kernel"]]
+        d["two_streams"] = bool(d["two_streams"])
+        d["splitk_merge"] = bool(d["splitk_merge"])
+        return d
+
 
 _lib: ctypes.CDLL | None = None
 
@@ -116,3 +139,11 @@ def ptr(t: torch.Tensor | None) -> int | None:
 
 def stream_of(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
+
+
+def launch_info(*args) -> dict:
+    """``lv_paged_attention_launch_info`` for the shape arguments ``args`` (as the header orders them, without the
+    output struct), as a dict with kernel names."""
+    info = LaunchInfo()
+    call("lv_paged_attention_launch_info", *args, ctypes.byref(info))
+    return info.as_dict()

@@ -71,10 +71,15 @@ PROMPT_WORKGROUP_FLOPS_PER_S = 1.3e12
 
 
 class MI355XAttention(AttentionBackend):
-    """Paged attention, cache stores and MLA latent decode on MI355X (gfx950) HIP kernels."""
+    """Paged attention, cache stores and MLA latent decode on MI355X (gfx950) HIP kernels.
+
+    ``launch_trace``: None, or a list to which every paged-attention call appends the launches the library made for
+    it (``lv_paged_attention_launch_info`` on the call's own arguments), for callers and tests that check which path
+    a step takes."""
 
     supported_dtypes = (torch.float16, torch.bfloat16)
     supported_kinds = ("decoder", "mla")
+    launch_trace: list | None = None
 
     @staticmethod
     def get_name() -> str:
@@ -186,6 +191,11 @@ class MI355XAttention(AttentionBackend):
                    float(self.scale), max_seqlen_q, max_seqlen_k, out.data_ptr(), os_[0], os_[1], _capi.ptr(ws),
                    0 if ws is None else ws.numel(), schedule, prompt_workgroups, flags, _capi.DTYPES[q.dtype],
                    _capi.stream_of(q.device))
+        if self.launch_trace is not None:
+            self.launch_trace.append(_capi.launch_info(rows, tokens, heads, self.num_kv_heads, dim, k_cache.size(1),
+                                                       cs[2], int(cu_seqlens_q is not None), max_seqlen_q,
+                                                       max_seqlen_k, schedule, prompt_workgroups, flags,
+                                                       _capi.DTYPES[q.dtype]))
         return out
 
     def _schedule(self, context: Context, elem_bytes: int) -> int:

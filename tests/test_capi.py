@@ -21,7 +21,8 @@ def declared():
 def test_header_declares_the_path():
     names = declared()
     for name in ("lv_pack", "lv_store_kvcache", "lv_store_latents", "lv_paged_attention",
-                 "lv_paged_attention_workspace_bytes", "lv_merge_attn_states", "lv_last_error", "lv_abi_version"):
+                 "lv_paged_attention_workspace_bytes", "lv_paged_attention_launch_info", "lv_merge_attn_states",
+                 "lv_last_error", "lv_abi_version"):
         assert name in names
 
 
@@ -29,7 +30,7 @@ def test_library_exports_every_declared_symbol():
     lib = _capi.load()
     missing = [n for n in declared() if not hasattr(lib, n)]
     assert not missing, f"declared in lvattn.h but not exported: {missing}"
-    assert lib.lv_abi_version() == 8
+    assert lib.lv_abi_version() == 9
     assert all(n in _capi._PROTOTYPES for n in declared()), "every declared function has a ctypes prototype"
 
 
@@ -79,3 +80,18 @@ def test_the_static_workspace_refuses_a_step_that_needs_more():
     with pytest.raises(_capi.LvError, match=rf"needs {need} bytes of workspace; the static workspace holds 16777216"):
         _capi.call("lv_paged_attention_static", 16, 0, 0, 16, 16, 0, 0, 0, 256, 16, 0, 16, None, 16, 4096,
                    tokens, 32, 8, 128, 1.0, 64, 1 << 20, 16, 0, 0, 0, 0, 0, 0, None)
+
+
+def test_the_launch_query_checks_its_shape_before_touching_the_gpu():
+    """lv_paged_attention_launch_info applies the call's own shape checks first (a bad shape is refused with the
+    call's message), and reports no kernels for a step without rows; neither case reads the device."""
+    with pytest.raises(_capi.LvError, match="head_dim 96"):
+        _capi.launch_info(4, 4, 8, 2, 96, 16, 64, 0, 1, 64, 0, 0, 0, 0)
+    with pytest.raises(_capi.LvError, match="unknown schedule 7"):
+        _capi.launch_info(4, 4, 8, 2, 64, 16, 64, 0, 1, 64, 7, 0, 0, 0)
+    with pytest.raises(_capi.LvError, match="LV_ATTN_PROMPTS_ONLY needs cu_seqlens_q"):
+        _capi.launch_info(4, 4, 8, 2, 64, 16, 64, 0, 1, 64, 0, 0, 2, 0)
+    with pytest.raises(_capi.LvError, match="a step with prompts holds at most 4096 rows"):
+        _capi.launch_info(5000, 9000, 8, 2, 64, 16, 64, 1, 8, 64, 0, 0, 0, 0)
+    info = _capi.launch_info(0, 0, 8, 2, 64, 16, 64, 0, 1, 64, 0, 0, 0, 0)
+    assert info["decode_kernel"] == info["prompt_kernel"] == "none"

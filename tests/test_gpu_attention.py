@@ -403,10 +403,11 @@ def _wide_step(cuda, num_cached, num_new, bs=16, seed=0):
     return tables, step
 
 
-def test_a_large_decode_batch_on_the_persistent_grid(cuda):
-    """256 decode rows of up to 600 keys split over 512-key items: enough items for the persistent ticket grid.
-    Checked against the oracle, then replayed from a captured graph with new queries and lengths (the plan kernel
-    re-zeroes the ticket counter on every replay), each replay equal to an eager call."""
+def test_a_large_decode_batch_of_pair_items(cuda):
+    """256 decode rows of up to 600 keys split over 512-key items: enough items that each takes a pair of adjacent
+    kv heads, one workgroup per item. Checked against the oracle, then replayed from a captured graph with new
+    queries and lengths (the plan kernel rebuilds the work list on every replay), each replay equal to an eager
+    call."""
     gen = torch.Generator().manual_seed(3)
     lens = torch.randint(16, 601, (256,), generator=gen).tolist()
     tables, (qs, kf, vf, kn, vn, kc, vc, slots) = _wide_step(cuda, [n - 1 for n in lens], [1] * 256)
@@ -416,8 +417,12 @@ def test_a_large_decode_batch_on_the_persistent_grid(cuda):
     ctx = Context(context_lens=torch.tensor(lens, dtype=torch.int32, device=cuda),
                   block_tables=torch.tensor(tables, dtype=torch.int32, device=cuda))
     out = torch.empty_like(q)
+    b.launch_trace = []
     b.decode(q, kc, vc, ctx, out=out)
     torch.cuda.synchronize()
+    assert_route(b.launch_trace[-1], decode_kernel="decode_list", kv_heads_per_item=2, two_streams=False,
+                 prompt_kernel="none")
+    b.launch_trace = None
     torch.testing.assert_close(out.float().cpu(), dense_expected(qs, kf, vf, 1 / math.sqrt(128)), atol=2e-2, rtol=1e-2)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
@@ -433,8 +438,10 @@ def test_a_large_decode_batch_on_the_persistent_grid(cuda):
 
 
 def test_a_mixed_step_of_many_decode_rows_under_both_schedules(cuda, monkeypatch):
-    """Two prompt chunks beside 600 decode rows (persistent decode grid): the overlapped and the serial schedule
-    both match the oracle and each other bit for bit."""
+    """Two prompt chunks beside 600 decode rows: under the overlapped schedule the decode items (2408 pair items,
+    too few for the persistent grid) run one workgroup per item on the second stream beside the persistent prompt
+    workgroups; under the serial one the prompt items run first on the whole GPU. Both match the oracle and each
+    other bit for bit."""
     from lvattn import backend as B
 
     gen = torch.Generator().manual_seed(4)
@@ -445,64 +452,120 @@ def test_a_mixed_step_of_many_decode_rows_under_both_schedules(cuda, monkeypatch
     b.store_kvcache(kn, vn, kc, vc, slots)
     want = dense_expected(qs, kf, vf, 1 / math.sqrt(128))
     outs = {}
+    routes = {B.SCHEDULE_SERIAL: dict(prompt_kernel="prompt_list", decode_kernel="decode_list", two_streams=False),
+              B.SCHEDULE_OVERLAP: dict(prompt_kernel="prompt_overlap", decode_kernel="decode_list", two_streams=True)}
+    b.launch_trace = []
     for sched in (B.SCHEDULE_SERIAL, B.SCHEDULE_OVERLAP):
         monkeypatch.setattr(b, "_schedule", lambda context, elem_bytes, s=sched: s)
         out = b.forward(torch.cat(qs), kn, vn, kc, vc, context_for(num_cached, num_new, tables, cuda))
         torch.cuda.synchronize()
+        assert_route(b.launch_trace[-1], kv_heads_per_item=2, **routes[sched])
         torch.testing.assert_close(out.float().cpu(), want, atol=2e-2, rtol=1e-2)
         outs[sched] = out
     assert torch.equal(outs[B.SCHEDULE_SERIAL], outs[B.SCHEDULE_OVERLAP])
 
 
-@pytest.mark.parametrize("kind", ["decode", "mixed-overlap", "mixed-serial", "small"])
+# Steps whose layers share one plan, one per launch path of a step: (heads, kv heads, head dim), decode rows
+# (count, key range), prompt rows (cached, new), the schedule, and the route the library takes for them.
+PLAN_STEPS = {
+    "decode-pairs": ((32, 8, 128), (256, 16, 600), [], None,
+                     dict(decode_kernel="decode_list", kv_heads_per_item=2, prompt_kernel="none")),
+    "decode-small": ((32, 8, 128), None, [], None,
+                     dict(decode_kernel="decode_list", kv_heads_per_item=1, prompt_kernel="none")),
+    "mixed-one-launch": ((32, 8, 128), (30, 64, 2048), [(256, 384), (0, 512)], "overlap",
+                         dict(decode_kernel="mixed_small", prompt_kernel="mixed_small", two_streams=False)),
+    "mixed-serial": ((32, 8, 128), (600, 16, 600), [(100, 40), (0, 70)], "serial",
+                     dict(decode_kernel="decode_list", prompt_kernel="prompt_list", two_streams=False)),
+    "mixed-overlap-list": ((32, 8, 128), (600, 16, 600), [(100, 40), (0, 70)], "overlap",
+                           dict(decode_kernel="decode_list", prompt_kernel="prompt_overlap", two_streams=True)),
+    # the persistent ticket grid beside the prompt workgroups: pair items at d128 (the Qwen3-8B shape), one-head
+    # items (odd kv heads), pair items at d64
+    "beside-pairs-d128": ((32, 8, 128), (2048, 16, 256), [(100, 40), (0, 70)], "overlap",
+                          dict(decode_kernel="decode_beside", kv_heads_per_item=2, prompt_kernel="prompt_overlap",
+                               two_streams=True)),
+    "beside-one-head-d128": ((12, 3, 128), (2100, 16, 256), [(100, 40), (0, 70)], "overlap",
+                             dict(decode_kernel="decode_beside", kv_heads_per_item=1, prompt_kernel="prompt_overlap",
+                                  two_streams=True)),
+    "beside-pairs-d64": ((16, 4, 64), (3100, 16, 256), [(100, 40), (0, 70)], "overlap",
+                         dict(decode_kernel="decode_beside", kv_heads_per_item=2, prompt_kernel="prompt_overlap",
+                              two_streams=True)),
+}
+
+
+def assert_route(info, **want):
+    got = {k: info[k] for k in want}
+    assert got == want, f"launch route {info}, expected {want}"
+
+
+@pytest.mark.parametrize("kind", list(PLAN_STEPS))
 def test_layers_of_one_step_share_one_plan(cuda, kind, monkeypatch):
     """Three layers (each with its own cache) attend through one step's Context: the first plans the work list, the
-    next two reuse it (LV_ATTN_REUSE_PLAN), so the persistent decode grid must leave its ticket at zero for them.
-    Each layer equals the same call on a fresh Context (which plans again), bit for bit; then the three layers are
-    captured in one graph (one plan launch in it) and every replay equals the eager layers."""
+    next two reuse it (LV_ATTN_REUSE_PLAN). On the persistent grid, the last workgroup of each layer must leave the
+    ticket counters at zero for the next. Each case asserts the launch path it reaches (lv_paged_attention_launch_info
+    on the call's arguments). Each layer equals the same call on a fresh Context (which plans again), bit for bit;
+    the first matches the fp32 oracle; then the three layers are captured in one graph (one plan launch in it) and
+    every replay equals the eager layers."""
     from lvattn import backend as B
 
+    (heads, kv_heads, dim), dec, prompts, sched, route = PLAN_STEPS[kind]
     gen = torch.Generator().manual_seed(31)
-    b = MI355XAttention(32, 128, 1 / math.sqrt(128), 8)
-    if kind == "decode":  # 256 rows: the persistent grid
-        lens = torch.randint(16, 601, (256,), generator=gen).tolist()
-        num_cached, num_new = [n - 1 for n in lens], [1] * 256
-    elif kind == "small":  # a few rows: one workgroup per item
+    scale = 1 / math.sqrt(dim)
+    b = MI355XAttention(heads, dim, scale, kv_heads)
+    if dec is None:  # a few rows: one workgroup per one-head item
         num_cached, num_new = [300, 5000, 20], [1, 1, 1]
-    else:  # two chunks beside 600 decode rows (persistent grid beside the prompt tiles when overlapped)
-        dec = torch.randint(16, 601, (600,), generator=gen).tolist()
-        num_cached, num_new = [100, 0] + [n - 1 for n in dec], [40, 70] + [1] * 600
-        sched = B.SCHEDULE_OVERLAP if kind == "mixed-overlap" else B.SCHEDULE_SERIAL
-        monkeypatch.setattr(b, "_schedule", lambda context, elem_bytes: sched)
-    tables, step0 = _wide_step(cuda, num_cached, num_new, seed=2)
+    else:
+        n, lo, hi = dec
+        lens = torch.randint(lo, hi + 1, (n,), generator=gen).tolist()
+        num_cached = [c for c, _ in prompts] + [k - 1 for k in lens]
+        num_new = [q for _, q in prompts] + [1] * n
+        order = sorted(range(len(num_new)), key=lambda i: num_new[i] > 1)  # decode rows first
+        num_cached, num_new = [num_cached[i] for i in order], [num_new[i] for i in order]
+    if sched is not None:
+        s_ = B.SCHEDULE_OVERLAP if sched == "overlap" else B.SCHEDULE_SERIAL
+        monkeypatch.setattr(b, "_schedule", lambda context, elem_bytes: s_)
+    tables, at = [], 0
+    bs = 16
+    width = max(-(-(c + q) // bs) for c, q in zip(num_cached, num_new))
+    for c, q in zip(num_cached, num_new):
+        k = -(-(c + q) // bs)
+        tables.append(list(range(at, at + k)) + [-1] * (width - k))
+        at += k
+    step0 = paged_step(num_cached, num_new, tables, at, heads=heads, kv_heads=kv_heads, dim=dim, bs=bs, device=cuda,
+                       dtype=torch.bfloat16, seed=2)
+    print(f"{kind}: {len(num_new)} rows, {sum(num_new)} tokens", flush=True)
     q = torch.cat(step0[0])
     caches = [(step0[5], step0[6])]
+    dgen = torch.Generator(device=cuda).manual_seed(32)
     for layer in range(2):  # two more layers: other keys and values in caches of the same shape
-        kc = torch.randn(step0[5].shape, generator=gen).to(torch.bfloat16).to(cuda)
-        vc = torch.randn(step0[6].shape, generator=gen).to(torch.bfloat16).to(cuda)
-        caches.append((kc, vc))
+        caches.append(tuple(torch.randn(step0[5].shape, generator=dgen, device=cuda).to(torch.bfloat16)
+                            for _ in range(2)))
     b.store_kvcache(step0[3], step0[4], *caches[0], step0[7])
 
-    template = (Context(context_lens=torch.tensor([c + n for c, n in zip(num_cached, num_new)], dtype=torch.int32,
+    decode_only = all(x == 1 for x in num_new)
+    template = (Context(context_lens=torch.tensor([c + x for c, x in zip(num_cached, num_new)], dtype=torch.int32,
                                                   device=cuda),
                         block_tables=torch.tensor(tables, dtype=torch.int32, device=cuda))
-                if kind in ("decode", "small") else context_for(num_cached, num_new, tables, cuda))
+                if decode_only else context_for(num_cached, num_new, tables, cuda))
 
     def context():
         """A new step's Context over the same device tensors (no copies: it is also built inside the capture)."""
         skip = ("attn_metadata", "decode_splits")  # per-step caches
         return Context(**{k: getattr(template, k) for k in Context.__slots__ if k not in skip})
 
+    b.launch_trace = []
     step = context()
     shared = [b.forward(q, None, None, kc, vc, step) for kc, vc in caches]
     torch.cuda.synchronize()
     assert sum(1 for k in step.attn_metadata if k[0] == "plan") == 1
+    for info in b.launch_trace:
+        assert_route(info, **route)
+    b.launch_trace = None
     fresh = [b.forward(q, None, None, kc, vc, context()) for kc, vc in caches]
     torch.cuda.synchronize()
     for i, (x, y) in enumerate(zip(shared, fresh)):
         assert torch.equal(x, y), f"layer {i}"
-    torch.testing.assert_close(shared[0].float().cpu(), dense_expected(step0[0], step0[1], step0[2],
-                                                                       1 / math.sqrt(128)), atol=2e-2, rtol=1e-2)
+    torch.testing.assert_close(shared[0].float().cpu(), dense_expected(step0[0], step0[1], step0[2], scale),
+                               atol=2e-2, rtol=1e-2)
     outs = [torch.empty_like(q) for _ in caches]
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):

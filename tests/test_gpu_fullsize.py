@@ -1,13 +1,15 @@
 """The measured steps at full size, packed, stored and attended as the bench runs them, against the fp32 oracle:
 every decode row of every step (the Qwen3-8B mixed step's 2048, batch-256 decode, the 16 long-context rows, the
-Qwen3-0.6B step's 30), every 64th query of every prompt chunk plus each chunk's last query (every query of the
-Qwen3-0.6B chunks), and every row of DeepSeek-V2-Lite's MLA decode step.
+Qwen3-0.6B step's 30), one query in every prompt item of every chunk (at an offset that moves from item to item)
+plus each chunk's last query (every query of the Qwen3-0.6B chunks), and every row of DeepSeek-V2-Lite's MLA decode
+step.
 
 Decode rows go through the oracle's restatement of the reference backend (``TorchMath.decode`` over slices of
 rows, ``decode_in_row_chunks``) on the rows' pages copied to the host, so the persistent ticket grid, the
 length-bucketed work list, the split-K merge and the overlapped prompt tiles are all checked on every item they
-produce. Prompt queries go through the textbook dense oracle on the keys the query sees. Tolerance: max-abs 2e-2 /
-rel 1e-2 against fp32 (bf16).
+produce; each step asserts the launch route it takes (``lv_paged_attention_launch_info``). Prompt queries go
+through the textbook dense oracle on the keys the query sees. Tolerance: max-abs 2e-2 / rel 1e-2 against fp32
+(bf16).
 """
 
 import pytest
@@ -34,8 +36,21 @@ def compact_pages(cache, lists):
     return host, bt
 
 
+# The launch route each measured paged step takes on an MI355X (256 CUs).
+OVERLAP = dict(prompt_kernel="prompt_overlap", decode_kernel="decode_beside", two_streams=True, kv_heads_per_item=2)
+PROMPTS = dict(prompt_kernel="prompt_list", decode_kernel="none", two_streams=False)
+DECODE = dict(prompt_kernel="none", decode_kernel="decode_list", kv_heads_per_item=2)
+ROUTES = {
+    "qwen3_8b_mixed": OVERLAP, "qwen3_8b_mixed_bs16": OVERLAP,
+    "qwen3_8b_prefill": PROMPTS, "qwen3_8b_prefill_bs16": PROMPTS,
+    "qwen3_8b_decode": DECODE, "qwen3_8b_long": dict(DECODE, splitk_merge=True),
+    "qwen3_0_6b_mixed": dict(prompt_kernel="mixed_small", decode_kernel="mixed_small", kv_heads_per_item=2),
+}
+
+
 def run_step(name, cuda):
-    """Pack, store and attend one workload's step on the GPU; returns what the checks need."""
+    """Pack, store and attend one workload's step on the GPU; asserts the launch route; returns what the checks
+    need."""
     wl = W.WORKLOADS[name]()
     t = W.materialize(wl, cuda)
     b = MI355XAttention(wl.num_heads, wl.head_dim, wl.scale, wl.num_kv_heads)
@@ -43,8 +58,13 @@ def run_step(name, cuda):
     order = fields.pop("order").cpu().tolist()
     b.store_kvcache(t.k_new, t.v_new, t.k_cache, t.v_cache, fields["slot_mapping"])
     ctx = Context(**{k: v for k, v in fields.items() if k in Context.__slots__})
+    b.launch_trace = []
     out = b.forward(t.q, t.k_new, t.v_new, t.k_cache, t.v_cache, ctx)
     torch.cuda.synchronize()
+    info = b.launch_trace[-1]
+    print(f"{name}: {info}", flush=True)
+    want = ROUTES[name]
+    assert {k: info[k] for k in want} == want, f"{name}: route {info}, expected {want}"
     assert torch.isfinite(out).all()
     return wl, t, out, order, fields["cu_seqlens_q"].cpu().tolist()
 
@@ -70,10 +90,19 @@ def check_decode_rows(wl, t, out, order, cu_q, rows_per_slice=128, rows_per_chun
     return len(rows)
 
 
-def check_prompt_queries(wl, t, out, order, cu_q, every):
-    """Every ``every``-th query of each prompt chunk and its last query, each against the dense oracle over the
-    row's keys up to its own position; returns the number of queries checked."""
+def item_queries(lq, per_item):
+    """One query position in every prompt item of a chunk of ``lq`` queries (an item spans ``per_item`` positions:
+    128 (position, head) query rows over the GQA group), at an offset that moves from item to item, plus the chunk's
+    last query."""
+    return sorted({per_item * i + (7 * i) % per_item for i in range(-(-lq // per_item))} | {lq - 1})
+
+
+def check_prompt_queries(wl, t, out, order, cu_q, every=None):
+    """Each prompt chunk's queries -- every ``every``-th one, or by default one in every prompt item
+    (``item_queries``) -- against the dense oracle over the row's keys up to its own position; returns the number
+    of queries checked."""
     bs, n = wl.block_size, 0
+    per_item = 128 // (wl.num_heads // wl.num_kv_heads)
     for i in range(len(order)):
         s = order[i]
         lq = wl.num_new[s]
@@ -84,7 +113,8 @@ def check_prompt_queries(wl, t, out, order, cu_q, every):
         pages = torch.tensor(wl.block_lists[s], dtype=torch.long, device=t.k_cache.device)[pos // bs]
         k = t.k_cache[pages, pos % bs].cpu().float()
         v = t.v_cache[pages, pos % bs].cpu().float()
-        for j in sorted(set(range(0, lq, every)) | {lq - 1}):
+        picks = item_queries(lq, per_item) if every is None else sorted(set(range(0, lq, every)) | {lq - 1})
+        for j in [j for j in picks if j < lq]:
             seen = lk - lq + j + 1
             q = t.q[cu_q[i] + j:cu_q[i] + j + 1].cpu().float()
             want = A.dense_attention(q, k[:seen], v[:seen], wl.scale, causal=False)
@@ -95,34 +125,37 @@ def check_prompt_queries(wl, t, out, order, cu_q, every):
 
 
 def test_qwen3_8b_mixed_step_every_decode_row(cuda):
-    """The bench's primary step: all 2048 decode rows (persistent grid beside the overlapped prompt tiles)."""
+    """The bench's primary step: all 2048 decode rows (the persistent grid of pair items beside the prompt
+    workgroups)."""
     wl, t, out, order, cu_q = run_step("qwen3_8b_mixed", cuda)
     assert check_decode_rows(wl, t, out, order, cu_q) == 2048
 
 
 def test_qwen3_8b_mixed_step_prompt_queries(cuda):
-    """The same step's four 1536-token chunks: every 64th query and the last, on cached prefixes up to 6144."""
+    """The same step's four 1536-token chunks, on cached prefixes up to 6144: one query in each of every chunk's 48
+    prompt items (32 positions each) and the last query."""
     wl, t, out, order, cu_q = run_step("qwen3_8b_mixed", cuda)
-    assert check_prompt_queries(wl, t, out, order, cu_q, every=64) == 4 * 25
+    assert check_prompt_queries(wl, t, out, order, cu_q) == 4 * 49
 
 
 def test_qwen3_8b_prompt_chunks_alone(cuda):
-    """The four chunks as a step of prompts (serial schedule, prompt tiles on the whole GPU)."""
+    """The four chunks as a step of prompts (prompt tiles on the whole GPU): one query per prompt item and the
+    last."""
     wl, t, out, order, cu_q = run_step("qwen3_8b_prefill", cuda)
-    assert check_prompt_queries(wl, t, out, order, cu_q, every=64) == 4 * 25
+    assert check_prompt_queries(wl, t, out, order, cu_q) == 4 * 49
 
 
 def test_qwen3_8b_mixed_step_on_16_token_pages(cuda):
-    """The mixed step on lean-vLLM's default page size (16 keys: four pages per prompt tile, each lane loading from
-    its key's page): every 64th query of the chunks and their last, and every decode row."""
+    """The mixed step on lean-vLLM's default page size (16 keys: four pages per prompt tile): one query per prompt
+    item of the chunks and their last, and every decode row."""
     wl, t, out, order, cu_q = run_step("qwen3_8b_mixed_bs16", cuda)
-    assert check_prompt_queries(wl, t, out, order, cu_q, every=64) == 4 * 25
+    assert check_prompt_queries(wl, t, out, order, cu_q) == 4 * 49
     assert check_decode_rows(wl, t, out, order, cu_q) == 2048
 
 
 def test_qwen3_8b_prompt_chunks_alone_on_16_token_pages(cuda):
     wl, t, out, order, cu_q = run_step("qwen3_8b_prefill_bs16", cuda)
-    assert check_prompt_queries(wl, t, out, order, cu_q, every=64) == 4 * 25
+    assert check_prompt_queries(wl, t, out, order, cu_q) == 4 * 49
 
 
 @pytest.mark.parametrize("name, rows", [("qwen3_8b_decode", 256), ("qwen3_8b_long", 16)])

@@ -162,8 +162,10 @@ WIDE_HEADS = [(8, 2), (16, 4), (32, 8), (12, 4), (24, 8), (6, 2), (64, 8), (8, 1
 @pytest.mark.parametrize("seed", range(8))
 def test_random_wide_decode_steps_match_the_oracle(cuda, seed, monkeypatch):
     """Steps of 300-1200 decode rows (some with one or two prompt chunks too): enough items that decode items take
-    a pair of kv heads where the kv heads are even (one-workgroup-per-item and persistent launches, the 16-token
-    tiles of the persistent kernel and the 8-token tiles beside prompt tiles), and one head where they are odd."""
+    a pair of kv heads where the kv heads are even (16-token wave tiles at d128, 8-token ones at d64), and one head
+    where they are odd; one workgroup per item, alone or beside the prompt workgroups. (The persistent grid beside
+    prompt workgroups needs more items: test_gpu_attention.py's plan-sharing steps reach it.) The launch route each
+    case takes is printed with its label."""
     rng = np.random.default_rng(9500 + seed)
     hq, hkv = WIDE_HEADS[seed % len(WIDE_HEADS)]
     dim = int(rng.choice([64, 128]))
@@ -198,8 +200,14 @@ def test_random_wide_decode_steps_match_the_oracle(cuda, seed, monkeypatch):
         monkeypatch.setattr(backend, "_schedule", lambda context, elem_bytes, s=sched: s)
         label += f" schedule {'serial' if sched == B.SCHEDULE_SERIAL else 'overlap'}"
     ctx = context_for(cached, new, tables, cuda, is_prefill=not decode_only)
+    backend.launch_trace = []
     out = backend.forward(torch.cat(qs), kn, vn, kc, vc, ctx)
     torch.cuda.synchronize()
+    info = backend.launch_trace[-1]
+    label += f" route {info}"
+    print(label, flush=True)
+    if hkv % 2:
+        assert info["kv_heads_per_item"] == 1, label
     assert torch.isfinite(out).all(), label
     want = dense_expected(qs, kf, vf, scale)
     torch.testing.assert_close(out.float().cpu(), want.float(), **TOL[dtype], msg=lambda m: f"{label}: {m}")
