@@ -29,6 +29,7 @@ device. Key lengths include the token(s) stored this step (``context_lens = num_
 from __future__ import annotations
 
 import dataclasses
+import functools
 import math
 from dataclasses import dataclass, field
 
@@ -196,9 +197,10 @@ class Tensors:
     expanded: dict | None = None  # MLA prefill: q, k, v of the new tokens and k, v of the cached prefix
 
 
-def _randn(shape, generator, device, dtype, std: float, chunk: int = 1 << 27):
-    """N(0, std) drawn in fp32 (in chunks, so a multi-GB cache needs no multi-GB fp32 temporary), then cast."""
-    out = torch.empty(shape, dtype=dtype, device=device)
+def _randn_into(shape, generator, device, dtype, std: float, chunk: int = 1 << 27, alloc=None):
+    """N(0, std) drawn in fp32 (in chunks, so a multi-GB cache needs no multi-GB fp32 temporary), then cast, into
+    ``alloc(shape, dtype)`` (default: a new device tensor)."""
+    out = alloc(shape, dtype) if alloc is not None else torch.empty(shape, dtype=dtype, device=device)
     flat = out.view(-1)
     for at in range(0, flat.numel(), chunk):
         n = min(chunk, flat.numel() - at)
@@ -206,13 +208,14 @@ def _randn(shape, generator, device, dtype, std: float, chunk: int = 1 << 27):
     return out
 
 
-def materialize(wl: Workload, device, dtype=torch.bfloat16, seed: int = 0) -> Tensors:
+def materialize(wl: Workload, device, dtype=torch.bfloat16, seed: int = 0, alloc=None) -> Tensors:
     """Draw the step's q, new K/V and a whole cache pool of N(0, std) values (the cache is filled everywhere,
-    so unwritten pages hold finite values too)."""
+    so unwritten pages hold finite values too). ``alloc(shape, dtype)``, if given, provides the tensors' memory."""
     device = torch.device(device)
     gen = torch.Generator(device=device)
     gen.manual_seed(seed)
     std = wl.value_std
+    _randn = functools.partial(_randn_into, alloc=alloc)
     if wl.is_mla_prefill:
         dqk, dv = wl.expanded
         lat = _randn((wl.tokens, wl.latent_dim), gen, device, dtype, std)
