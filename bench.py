@@ -42,7 +42,7 @@ for _p in (ROOT, ROOT / "lean-vllm_amd"):
 PEAK_HBM_GBS = 8000.0
 PEAK_BF16_TFLOPS = 2500.0
 METRIC = "paged-attn HBM GB/s (% of peak) + tokens/s per layer, Qwen3-8B mixed batch"
-EXTRA = ("qwen3_8b_decode,qwen3_8b_long,deepseek_v2_lite_mla,qwen3_0_6b_mixed,qwen3_8b_prefill,"
+EXTRA = ("qwen3_8b_decode,qwen3_8b_long,deepseek_v2_lite_mla,qwen3_0_6b_mixed,qwen3_8b_prefill,qwen3_8b_prefix_chunk,"
          "deepseek_v2_lite_mla_prefill,deepseek_v2_lite_mla_prefill_two_pass,qwen3_8b_decode_bs16,"
          "deepseek_v2_lite_mla_bs16,qwen3_8b_mixed_bs16,qwen3_8b_prefill_bs16")
 RIDGE_FLOP_PER_BYTE = PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)  # above it a step is MFMA-bound

@@ -227,7 +227,8 @@ __device__ inline int wave_incl_scan(int x) {
 }
 
 // Exclusive prefix sum of a[0, n) in LDS, in place, by a block of kScanThreads threads; a[n] receives the total.
-// wave_tot holds kScanThreads / 64 ints of LDS. Every thread of the block must call it. Each thread scans its
+// wave_tot holds kScanThreads / 64 ints of LDS. Every thread of the block must call it, after a barrier that follows
+// the last write of a[] (a thread's chunk holds entries other threads wrote once n > kScanThreads). Each thread scans its
 // chunk, each wave its threads' chunk totals; every thread then sums the wave totals before its own (16 broadcast
 // LDS reads, issued together) instead of one thread scanning them in sequence between two more barriers.
 constexpr int kScanThreads = 1024;

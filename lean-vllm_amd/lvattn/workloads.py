@@ -14,6 +14,8 @@ device. Key lengths include the token(s) stored this step (``context_lens = num_
   U[0, 6144], plus 2048 decode rows with context U[256, 4096] (8192 tokens).
 - ``qwen3_8b_prefill``: the four prompt chunks of ``qwen3_8b_mixed`` alone (a step of prompts; MFMA-bound).
 - ``qwen3_8b_long``: 32/8 heads, d128, bs 256, pool 10,000; 16 decode rows, context U[32768, 131072].
+- ``qwen3_8b_prefix_chunk``: 32/8 heads, d128, bs 256, pool 1024; one prompt chunk of 1024 new tokens on a cached
+  prefix of 30,720 (a step of prompts whose few query tiles each walk a long prefix: MFMA work split over keys).
 - ``deepseek_v2_lite_mla``: 16 heads, latent 576 (512 + 64 rope), values 512, bs 64, pool 34,000; 128 decode
   rows, context U[1024, 16384]; values N(0, 0.5); scale 1/sqrt(192).
 - ``qwen3_8b_decode_bs16``, ``deepseek_v2_lite_mla_bs16``: the same two decode steps (same lengths) on 16-token
@@ -141,6 +143,16 @@ def qwen3_8b_prefill(seed: int = 0, block_size: int = 256) -> Workload:
                     num_layers=36)
 
 
+def qwen3_8b_prefix_chunk(seed: int = 0, block_size: int = 256) -> Workload:
+    """One prompt chunk of 1024 new tokens on a cached prefix of 30,720 (a long prompt's late chunk): 32 query tiles
+    per kv head, each walking some 490 key tiles."""
+    num_cached, num_new = [30_720], [1024]
+    pool = 1024 * 256 // block_size
+    rng = np.random.default_rng(seed)
+    return Workload("qwen3_8b_prefix_chunk", 32, 8, 128, block_size, pool, num_cached, num_new,
+                    _tables(rng, pool, [31_744], block_size), 1 / math.sqrt(128), num_layers=36)
+
+
 def qwen3_8b_long(seed: int = 0) -> Workload:
     rng = np.random.default_rng(seed)
     ctx = rng.integers(32768, 131072 + 1, size=16)
@@ -176,6 +188,7 @@ WORKLOADS = {
     "qwen3_8b_mixed": qwen3_8b_mixed,
     "qwen3_8b_prefill": qwen3_8b_prefill,
     "qwen3_8b_long": qwen3_8b_long,
+    "qwen3_8b_prefix_chunk": qwen3_8b_prefix_chunk,
     "deepseek_v2_lite_mla": deepseek_v2_lite_mla,
     "deepseek_v2_lite_mla_prefill": deepseek_v2_lite_mla_prefill,
     "deepseek_v2_lite_mla_prefill_two_pass": lambda seed=0: dataclasses.replace(

@@ -42,7 +42,7 @@ PROMPTS = dict(prompt_kernel="prompt_list", decode_kernel="none", two_streams=Fa
 DECODE = dict(prompt_kernel="none", decode_kernel="decode_list", kv_heads_per_item=2)
 ROUTES = {
     "qwen3_8b_mixed": OVERLAP, "qwen3_8b_mixed_bs16": OVERLAP,
-    "qwen3_8b_prefill": PROMPTS, "qwen3_8b_prefill_bs16": PROMPTS,
+    "qwen3_8b_prefill": PROMPTS, "qwen3_8b_prefill_bs16": PROMPTS, "qwen3_8b_prefix_chunk": PROMPTS,
     "qwen3_8b_decode": DECODE, "qwen3_8b_long": dict(DECODE, splitk_merge=True),
     "qwen3_0_6b_mixed": dict(prompt_kernel="mixed_small", decode_kernel="mixed_small", kv_heads_per_item=2),
 }
@@ -151,6 +151,13 @@ def test_qwen3_8b_mixed_step_on_16_token_pages(cuda):
     wl, t, out, order, cu_q = run_step("qwen3_8b_mixed_bs16", cuda)
     assert check_prompt_queries(wl, t, out, order, cu_q) == 4 * 49
     assert check_decode_rows(wl, t, out, order, cu_q) == 2048
+
+
+def test_qwen3_8b_chunk_on_a_long_prefix(cuda):
+    """One 1024-token chunk on a 30,720-token prefix (32 prompt items per kv head, each walking some 490 key tiles):
+    one query per prompt item and the last."""
+    wl, t, out, order, cu_q = run_step("qwen3_8b_prefix_chunk", cuda)
+    assert check_prompt_queries(wl, t, out, order, cu_q) == 33
 
 
 def test_qwen3_8b_prompt_chunks_alone_on_16_token_pages(cuda):
