@@ -406,6 +406,19 @@ def traffic_of(name: str):
     return None
 
 
+def traffic_source(name: str):
+    """Where ``roofline.traffic`` comes from: counters can only be read under the profiler, so it is the committed
+    summary of a profiling run (its own box and lease), not this run; its op time is given beside it."""
+    f = ROOT / "profiles" / f"traffic_{name}.json"
+    if not f.exists():
+        return None
+    j = json.loads(f.read_text())
+    return {"file": f"profiles/traffic_{name}.json", "measured": "rocprofv3 FETCH_SIZE + WRITE_SIZE over the op's "
+            "kernels in a profiling run, scaled by the same counters' reading for a 1 GiB copy",
+            "op_span_us_in_that_run": j.get("rocprof_op_span_us_median_later_layers"),
+            "full_bench_attention_us_in_that_lease": j.get("lease_full_bench_attention_us")}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -478,6 +491,7 @@ def main():
             "unit": "GB/s",
             "frac": primary["attention_frac_of_peak"],
             "traffic": traffic_of(primary["workload"]),
+            "traffic_source": traffic_source(primary["workload"]),
             "kernel": attention_op(wl),
             "algorithmic_bytes_per_launch": primary["bytes"]["attention"],
             "tflops": primary["attention_TFLOPs"],
@@ -488,6 +502,7 @@ def main():
             "unit": "TFLOP/s",
             "frac": primary["attention_frac_of_mfma_peak"],
             "traffic": traffic_of(primary["workload"]),
+            "traffic_source": traffic_source(primary["workload"]),
             "kernel": attention_op(wl),
             "algorithmic_flops_per_launch": primary["flops"],
             "GBs": primary["attention_GBs"],
