@@ -994,6 +994,16 @@ static StepKind step_kind(int32_t num_rows, bool has_cu_q, int32_t max_seqlen_q,
   return k;
 }
 
+// A launch counts its work-items (workgroups x 256) in 32 bits: the step's largest grid must stay below that.
+static int check_grids(const Shape& s, int32_t num_rows, int32_t num_heads, int32_t num_kv_heads) {
+  const int64_t prompt = (int64_t)s.max_prompt_items * num_kv_heads;
+  const int64_t decode = std::max<int64_t>(s.max_decode_items, (int64_t)num_rows * s.max_splits) * num_heads;
+  LV_REQUIRE((prompt + decode) * 256 < ((int64_t)1 << 32),
+             "paged_attention: the step needs %lld + %lld workgroups, more than one launch holds", (long long)prompt,
+             (long long)decode);
+  return LV_OK;
+}
+
 // The shape part of a step's parameters (what the route depends on).
 static void shape_params(AttnParams& p, const Shape& s, int32_t num_rows, int32_t num_heads, int32_t num_kv_heads,
                          int32_t block_size, int64_t cache_stride_head) {
@@ -1037,6 +1047,8 @@ static int paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h
   LV_REQUIRE(scale > 0.f, "paged_attention: the softmax scale must be positive, got %g", (double)scale);
   const StepKind kind = step_kind(num_rows, cu_seqlens_q != nullptr, max_seqlen_q, schedule, prompt_workgroups, flags);
   const Shape s = plan_shape(num_rows, num_tokens, num_heads, num_kv_heads, head_dim, max_seqlen_k, kind.listed);
+  const int rg = check_grids(s, num_rows, num_heads, num_kv_heads);
+  if (rg != LV_OK) return rg;
   if (static_ws) {
     LV_REQUIRE(s.bytes <= (size_t)LV_STATIC_WORKSPACE_BYTES,
                "paged_attention_static: this step needs %zu bytes of workspace; the static workspace holds %zu "
@@ -1142,6 +1154,8 @@ extern "C" int lv_paged_attention_launch_info(int32_t num_rows, int32_t num_toke
   if (rc0 != LV_OK || num_rows == 0 || num_tokens == 0) return rc0;
   const StepKind kind = step_kind(num_rows, has_cu_seqlens_q != 0, max_seqlen_q, schedule, prompt_workgroups, flags);
   const Shape s = plan_shape(num_rows, num_tokens, num_heads, num_kv_heads, head_dim, max_seqlen_k, kind.listed);
+  const int rg = check_grids(s, num_rows, num_heads, num_kv_heads);
+  if (rg != LV_OK) return rg;
   AttnParams p{};
   shape_params(p, s, num_rows, num_heads, num_kv_heads, block_size, cache_stride_head);
   Route r;

@@ -71,15 +71,15 @@ def test_the_static_workspace_refuses_a_step_that_needs_more():
     """lv_paged_attention_static sizes the step before it touches the GPU; a step whose work list and split-K
     partials exceed LV_STATIC_WORKSPACE_BYTES is refused with a message naming both sizes. (Arguments are fake
     non-null pointers: the call returns before using them.)"""
-    # Split-K keeps a step's partials under 9 MiB at any context length; a step of 2^27 prompt tokens needs a work
-    # list of 4M items (32 MiB).
+    # Split-K keeps a step's partials under 9 MiB at any context length; a step of 2^25 prompt tokens over one kv
+    # head needs a work list of 2M items (16.8 MB) and still fits one launch.
     assert _capi.query("lv_paged_attention_workspace_bytes", 4096, 4096, 32, 8, 128, (1 << 31) - 1, 1) < 9 << 20
-    tokens = 1 << 27
-    need = _capi.query("lv_paged_attention_workspace_bytes", 4096, tokens, 32, 8, 128, 1 << 20, 0)
+    tokens = 1 << 25
+    need = _capi.query("lv_paged_attention_workspace_bytes", 4096, tokens, 8, 1, 128, 1 << 20, 0)
     assert need > 16 << 20
     with pytest.raises(_capi.LvError, match=rf"needs {need} bytes of workspace; the static workspace holds 16777216"):
         _capi.call("lv_paged_attention_static", 16, 0, 0, 16, 16, 0, 0, 0, 256, 16, 0, 16, None, 16, 4096,
-                   tokens, 32, 8, 128, 1.0, 64, 1 << 20, 16, 0, 0, 0, 0, 0, 0, None)
+                   tokens, 8, 1, 128, 1.0, 64, 1 << 20, 16, 0, 0, 0, 0, 0, 0, None)
 
 
 def test_the_launch_query_checks_its_shape_before_touching_the_gpu():
@@ -95,3 +95,14 @@ def test_the_launch_query_checks_its_shape_before_touching_the_gpu():
         _capi.launch_info(5000, 9000, 8, 2, 64, 16, 64, 1, 8, 64, 0, 0, 0, 0)
     info = _capi.launch_info(0, 0, 8, 2, 64, 16, 64, 0, 1, 64, 0, 0, 0, 0)
     assert info["decode_kernel"] == info["prompt_kernel"] == "none"
+
+
+def test_a_step_too_large_for_one_launch_is_refused():
+    """A step whose prompt grid would pass the 32-bit work-item count of one launch is refused with a message, by
+    the call and by the launch query alike, before anything touches the GPU (fake non-null pointers)."""
+    tokens = 1 << 29
+    with pytest.raises(_capi.LvError, match="more than one launch holds"):
+        _capi.launch_info(4096, tokens, 32, 8, 128, 256, 128, 1, 1 << 20, 1 << 20, 0, 0, 0, 0)
+    with pytest.raises(_capi.LvError, match="more than one launch holds"):
+        _capi.call("lv_paged_attention", 16, 0, 0, 16, 16, 0, 0, 0, 256, 16, 0, 16, None, 16, 4096, tokens, 32, 8, 128,
+                   1.0, 1 << 20, 1 << 20, 16, 0, 0, 256, 1 << 40, 0, 0, 0, 0, None)
