@@ -395,7 +395,7 @@ def attention_op(wl) -> str:
         kernels = [k.removeprefix("lv::") for k in json.loads(f.read_text()).get("kernels", [])]
         if kernels:
             return f"lv_paged_attention ({' + '.join(kernels)})"
-    return "lv_paged_attention (plan_kernel + decode kernels + splitk_merge_kernel)"
+    return "lv_paged_attention (plan_kernel + decode kernels)"
 
 
 def traffic_of(name: str):

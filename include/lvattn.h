@@ -121,7 +121,9 @@ int lv_store_latents(const void* latent, int64_t latent_stride_t, int32_t num_to
  * seqlens_k / cu_seqlens_k pointers, whose contents have not changed since), so the plan launch is skipped -- the
  * per-step plan the reference's backends cache in context.attn_metadata (lean_vllm/attention/flash_backend.py:16-20,
  * 157-160). The library honours the flag only if the last plan it made in this workspace was for the same shape and
- * pointers, and plans again otherwise; unchanged contents are the caller's promise. */
+ * pointers, and plans again otherwise; unchanged contents are the caller's promise. Besides the list, a plan zeroes
+ * the counters of the persistent decode grid and of the split rows' in-kernel merges; every completed call leaves
+ * them at zero again, so a later layer finds them as the plan left them. */
 #define LV_ATTN_REUSE_PLAN 1
 /* flags, also: LV_ATTN_PROMPTS_ONLY -- every row of the step has more than one query (the caller's host lengths say
  * so), so no decode launch and no split-K merge are made. Needs cu_seqlens_q and max_seqlen_q > 1. */
@@ -163,7 +165,8 @@ typedef struct lv_launch_info {
   int32_t two_streams;
   int32_t keys_per_split;     /* keys per decode item */
   int32_t max_splits;         /* the most decode items one row is split into */
-  int32_t splitk_merge;       /* 1: splitk_merge_kernel combines the rows split over several items */
+  int32_t splitk_merge;       /* 1: rows are split over several items; each row's last split to finish merges
+                                 them (log-sum-exp) inside the decode launch */
 } lv_launch_info;
 int lv_paged_attention_launch_info(int32_t num_rows, int32_t num_tokens, int32_t num_heads, int32_t num_kv_heads,
                                    int32_t head_dim, int32_t block_size, int64_t cache_stride_head,
@@ -177,7 +180,8 @@ int lv_paged_attention_launch_info(int32_t num_rows, int32_t num_tokens, int32_t
  * LV_STATIC_WORKSPACE_BYTES that each GPU the library runs on holds until the process ends; a step needing more
  * (lv_paged_attention_workspace_bytes larger than that; the split-K sizing keeps steps of up to 4096 rows at any
  * context length under 9 MiB) is refused with LV_EINVAL. The kernels clear what must start at zero themselves
- * (the plan kernel zeroes the persistent grid's ticket), so no memset is recorded into a captured graph. Every call
+ * (the plan kernel zeroes the persistent grid's ticket and the split rows' merge counters), so no memset is recorded
+ * into a captured graph. Every call
  * on one GPU shares that GPU's array, which keeps the last call's contents: calls that overlap on one GPU (two
  * streams, two host threads, or a graph replay beside an eager call) race. Results equal lv_paged_attention's for
  * the same arguments. Set-up: the first call on a device resolves the array's address there and creates the

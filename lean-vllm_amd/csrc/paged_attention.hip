@@ -6,10 +6,10 @@
 //                  range; a token's head row (D elements) is spread over 16 lanes as 16-byte loads (the two head
 //                  rows of a pair, adjacent in the cache, over 32); q.k by v_dot2 with a DPP butterfly inside the
 //                  16-lane row; online softmax per tile; p.v on the VALU in fp32. The four waves and, for long
-//                  rows, the splits are merged by log-sum-exp.
+//                  rows, the splits are merged by log-sum-exp (a row's splits by whichever finishes last).
 //   prompt item  = (row, q tile, kv head): a row with several queries; the MFMA tile of attn_common.h.
 // Launches read a work list built on the device by plan_kernel from the key lengths (and cu_seqlens_q), longest
-// work first. Rows whose keys were split are combined by splitk_merge_kernel.
+// work first; its workspace also holds the split rows' partials and their merge counters.
 //
 // Math: TorchAttention.decode / prefill (lean_vllm/attention/torch_backend.py:62-103,159-181): query head h reads
 // key head h / (Hq/Hkv); query j of a row with lq queries and lk keys sees keys 0..lk-lq+j.
@@ -60,6 +60,71 @@ __device__ inline float groups_sum(float x) {
   if constexpr (LPH == 8) x += dpp_ror8(x);
   if constexpr (LPH <= 16) x = xor16_sum(x);
   return xor32_sum(x);
+}
+
+// A split row's partials pass between workgroups that may run on different XCDs, whose L2 caches are not coherent
+// with each other. They are stored and loaded as device-scope relaxed atomics (global_store / global_load with sc1:
+// written through to memory, read past the L2), so neither side needs a whole-L2 writeback or invalidate.
+__device__ __forceinline__ void coherent_store(float* ptr, float v) {
+  __hip_atomic_store(ptr, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float coherent_load(const float* ptr) {
+  return __hip_atomic_load(ptr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Merge of a split row's partial outputs for dims d0 .. d0 + PER - 1 of query head `head`, written to the output row
+// `tok`: o = sum_s 2^(lse_s - M) o_s / sum_s 2^(lse_s - M). The partials are read kMergeBatch splits at a time, every
+// load of a batch issued before the first is used, with the max and the sums carried from batch to batch (a long
+// row's 32 splits are two round trips to memory, not 64). Each output element's arithmetic depends only on its own
+// head and dim, so any spread of the elements over threads gives the same bits.
+constexpr int kMergeBatch = 16;
+template <typename T, int D, int PER>
+__device__ __forceinline__ void merge_split_partials(const AttnParams& p, int row, int tok, int head, int nsplit,
+                                                     int d0) {
+  using E = Elem<T>;
+  static_assert(PER == 1 || PER == 2, "one or two dims per thread");
+  const int64_t slot0 = ((int64_t)row * p.hq + head) * p.max_splits;
+  float m = -INFINITY, den = 0.f, o[PER];
+#pragma unroll
+  for (int e = 0; e < PER; ++e) o[e] = 0.f;
+  for (int s0 = 0; s0 < nsplit; s0 += kMergeBatch) {
+    float ls[kMergeBatch], x[kMergeBatch][PER];
+#pragma unroll
+    for (int i = 0; i < kMergeBatch; ++i) {
+      ls[i] = -INFINITY;
+#pragma unroll
+      for (int e = 0; e < PER; ++e) x[i][e] = 0.f;
+      if (s0 + i < nsplit) {  // uniform over the threads of a row
+        ls[i] = coherent_load(p.part_lse + slot0 + s0 + i);
+        const float* src = p.part_o + (slot0 + s0 + i) * D;
+#pragma unroll
+        for (int e = 0; e < PER; ++e) x[i][e] = coherent_load(src + d0 + e);
+      }
+    }
+    float bm = m;
+#pragma unroll
+    for (int i = 0; i < kMergeBatch; ++i) bm = fmaxf(bm, ls[i]);
+    if (bm == -INFINITY) continue;
+    const float alpha = fast_exp2(m - bm);  // 0 while m is -inf
+    den *= alpha;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) o[e] *= alpha;
+#pragma unroll
+    for (int i = 0; i < kMergeBatch; ++i) {
+      const float w = fast_exp2(ls[i] - bm);  // 0 past the last split
+      den += w;
+#pragma unroll
+      for (int e = 0; e < PER; ++e) o[e] = fmaf(w, x[i][e], o[e]);
+    }
+    m = bm;
+  }
+  const float inv = den > 0.f ? 1.f / den : 0.f;
+  char* dst = p.out + tok * p.o_st + head * p.o_sh + (int64_t)d0 * 2;
+  if constexpr (PER == 2) {
+    *reinterpret_cast<uint32_t*>(dst) = E::pack(o[0] * inv, o[1] * inv);
+  } else {
+    *reinterpret_cast<uint16_t*>(dst) = (uint16_t)(E::pack(o[0] * inv, 0.f) & 0xffffu);
+  }
 }
 
 // publish (persistent launches): thread 0 stores publish_value there before the item's merge barrier, and the
@@ -289,8 +354,28 @@ __device__ void decode_item(const AttnParams& p, int row, int split, int kvh, in
       const int64_t slot = ((int64_t)row * p.hq + head) * p.max_splits + split;
       float* dst = p.part_o + slot * D + d0;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) dst[e] = o[e];
-      if (d0 == 0) p.part_lse[slot] = mmax == -INFINITY ? -INFINITY : mmax + fast_log2(den);
+      for (int e = 0; e < 8; ++e) coherent_store(dst + e, o[e]);
+      if (d0 == 0) coherent_store(p.part_lse + slot, mmax == -INFINITY ? -INFINITY : mmax + fast_log2(den));
+    }
+  }
+  // A split row: the split that counts in last merges the item's heads. Each wave waits until its partial stores
+  // are complete (written through to memory) before the barrier that precedes the count, so every split's partials
+  // are in memory before its count; the merger reads them past its L2 after its own count has returned.
+  if (nsplit > 1 && p.merge_count) {
+    __shared__ int s_last;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    int32_t* count = p.merge_count + (row * (p.hkv / HP) + kvh / HP) * p.qgroups + qg;
+    if (threadIdx.x == 0)
+      s_last = __hip_atomic_fetch_add(count, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nsplit - 1;
+    __syncthreads();
+    if (s_last) {
+      for (int c = threadIdx.x; c < HG * D / 2; c += blockDim.x) {
+        const int g = c / (D / 2), d0 = (c % (D / 2)) * 2;
+        merge_split_partials<T, D, 2>(p, row, tok, (kvh + g / GS) * p.group + qg * GS + g % GS, nsplit, d0);
+      }
+      // Back to zero for the next layer on this plan.
+      if (threadIdx.x == 0) __hip_atomic_store(count, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
@@ -451,19 +536,21 @@ __device__ inline int len_bucket(int keys, int split) {
 // items instead of a tail of full ones. A prompt row's tiles go last tile first (most keys) when the prompt items
 // have the GPU to themselves (last_first: a step of prompts, or the serial schedule): the Qwen3-8B chunks 5-6%
 // faster than first tile first. Beside the decode rows (the overlapped schedule) the order made no measurable
-// difference, and the first tile goes first there as before.
+// difference, and the first tile goes first there as before. The split rows' merge counters start at zero.
 __global__ __launch_bounds__(kScanThreads) void plan_kernel(const int32_t* __restrict__ cu_q,
                                                             const int32_t* __restrict__ lens_k,
                                                             const int32_t* __restrict__ cu_k, int32_t rows,
                                                             int32_t split, int32_t qp, int32_t max_items,
                                                             int32_t last_first, int2* __restrict__ items,
-                                                            int32_t* __restrict__ n_items) {
+                                                            int32_t* __restrict__ n_items,
+                                                            int32_t* __restrict__ merge_count, int32_t n_merge) {
   __shared__ int pre[kPlanMaxRows + 1];
   __shared__ int full[kPlanMaxRows + 1];
   __shared__ int bucket[kLenBuckets + 1];
   __shared__ int wave_tot[kScanThreads / 64 + 1];
   const int tid = threadIdx.x;
   for (int b = tid; b <= kLenBuckets; b += kScanThreads) bucket[b] = 0;
+  for (int i = tid; i < n_merge; i += kScanThreads) merge_count[i] = 0;
   __syncthreads();
   for (int r = tid; r < rows; r += kScanThreads) {
     const int lq = cu_q ? cu_q[r + 1] - cu_q[r] : 1;
@@ -508,71 +595,13 @@ __global__ __launch_bounds__(kScanThreads) void plan_kernel(const int32_t* __res
   }
 }
 
-// Combine a split row's partial outputs: o = sum_s 2^(lse_s - M) o_s / sum_s 2^(lse_s - M). The partials are read
-// kMergeBatch splits at a time, every load of a batch issued before the first is used, with the max and the sums
-// carried from batch to batch (a long row's 32 splits are two round trips to memory, not 64).
-constexpr int kMergeBatch = 16;
-template <typename T, int D>
-__global__ __launch_bounds__(64) void splitk_merge_kernel(AttnParams p) {
-  using E = Elem<T>;
-  const int row = blockIdx.x, head = blockIdx.y, lane = threadIdx.x;
-  if (p.cu_q && p.cu_q[row + 1] - p.cu_q[row] != 1) return;  // a prefill row: written by its items
-  const int lk = key_len(p, row);
-  const int nsplit = min((lk + p.split - 1) / p.split, p.max_splits);
-  if (nsplit <= 1) return;
-  const int tok = p.cu_q ? p.cu_q[row] : row;
-  const int64_t slot0 = ((int64_t)row * p.hq + head) * p.max_splits;
-  constexpr int PER = D / 64;  // dims per lane
-  float m = -INFINITY, den = 0.f, o[PER];
-#pragma unroll
-  for (int e = 0; e < PER; ++e) o[e] = 0.f;
-  for (int s0 = 0; s0 < nsplit; s0 += kMergeBatch) {
-    float ls[kMergeBatch], x[kMergeBatch][PER];
-#pragma unroll
-    for (int i = 0; i < kMergeBatch; ++i) {
-      ls[i] = -INFINITY;
-#pragma unroll
-      for (int e = 0; e < PER; ++e) x[i][e] = 0.f;
-      if (s0 + i < nsplit) {  // wave-uniform
-        ls[i] = p.part_lse[slot0 + s0 + i];
-        const float* src = p.part_o + (slot0 + s0 + i) * D;
-#pragma unroll
-        for (int e = 0; e < PER; ++e) x[i][e] = src[lane * PER + e];
-      }
-    }
-    float bm = m;
-#pragma unroll
-    for (int i = 0; i < kMergeBatch; ++i) bm = fmaxf(bm, ls[i]);
-    if (bm == -INFINITY) continue;
-    const float alpha = fast_exp2(m - bm);  // 0 while m is -inf
-    den *= alpha;
-#pragma unroll
-    for (int e = 0; e < PER; ++e) o[e] *= alpha;
-#pragma unroll
-    for (int i = 0; i < kMergeBatch; ++i) {
-      const float w = fast_exp2(ls[i] - bm);  // 0 past the last split
-      den += w;
-#pragma unroll
-      for (int e = 0; e < PER; ++e) o[e] = fmaf(w, x[i][e], o[e]);
-    }
-    m = bm;
-  }
-  const float inv = den > 0.f ? 1.f / den : 0.f;
-  char* dst = p.out + tok * p.o_st + head * p.o_sh + (int64_t)lane * PER * 2;
-  if constexpr (PER == 2) {
-    *reinterpret_cast<uint32_t*>(dst) = E::pack(o[0] * inv, o[1] * inv);
-  } else {
-    static_assert(PER == 1, "D = 64 or 128");
-    *reinterpret_cast<uint16_t*>(dst) = (uint16_t)(E::pack(o[0] * inv, 0.f) & 0xffffu);
-  }
-}
-
 // ---------------------------------------------------------------------------------------------------------
 // Host side.
 
 struct Shape {
   int32_t split, max_splits, max_items, max_prompt_items, max_decode_items, gs;
-  size_t items_off, count_off, lse_off, o_off, bytes;
+  int64_t merges;  // split rows' merge counters (rows x kv heads x query-head groups), listed steps only
+  size_t items_off, count_off, lse_off, o_off, merge_off, bytes;
 };
 
 static int pick_gs(int group) {
@@ -588,10 +617,12 @@ static Shape plan_shape(int32_t rows, int32_t tokens, int32_t hq, int32_t hkv, i
   s.gs = pick_gs(group);
   const int64_t units = (int64_t)rows * hkv * (group / s.gs);
   const int64_t keys = max_k > 0 ? max_k : 1;
-  // Keys per decode item: enough items to fill the chip several times over, at least 256 keys each.
+  // Keys per decode item: enough items to fill the chip several times over, at least 256 keys each. Rows split only
+  // in a listed step (whose workspace holds the merge counters); a step of more rows has units beyond the target
+  // anyway.
   const int64_t target = kSplitTarget;
   int64_t split = kMinSplit;
-  while (split < keys && units * ((keys + split - 1) / split) > target) split *= 2;
+  while (split < keys && (!listed || units * ((keys + split - 1) / split) > target)) split *= 2;
   s.split = (int32_t)split;
   s.max_splits = (int32_t)((keys + split - 1) / split);
   const int qp = kPrefillRows / (group > 0 ? group : 1);
@@ -610,6 +641,10 @@ static Shape plan_shape(int32_t rows, int32_t tokens, int32_t hq, int32_t hkv, i
   off = (off + 255) / 256 * 256;
   s.o_off = off;
   off += parts * d * sizeof(float);
+  off = (off + 255) / 256 * 256;
+  s.merges = listed && s.max_splits > 1 ? (int64_t)rows * hkv * (group / s.gs) : 0;
+  s.merge_off = off;
+  off += (size_t)s.merges * sizeof(int32_t);
   s.bytes = off;
   return s;
 }
@@ -677,7 +712,7 @@ struct Route {
   int decode = LV_KERNEL_NONE, decode_grid = 0;  // the launch running the decode items, its workgroups
   int prompt = LV_KERNEL_NONE, prompt_grid = 0;  // the launch running the prompt items (MIXED_SMALL: the same one)
   bool two_streams = false;                      // decode items on the second stream beside prompt_overlap_kernel
-  bool merge = false;                            // splitk_merge_kernel after
+  bool merge = false;                            // rows split over items, merged by their last split
 };
 
 // CUs that hold a prompt workgroup in an overlapped step: the caller's count clamped to [default, max] and
@@ -802,10 +837,6 @@ static int launch(const AttnParams& p, const Shape& s, const StepKind& k, hipStr
       }
       LV_LAUNCH_CHECK("paged attention kernels");
     }
-  }
-  if (r.merge) {
-    hipLaunchKernelGGL((splitk_merge_kernel<T, D>), dim3(p.rows, p.hq), dim3(64), 0, stream, p);
-    LV_LAUNCH_CHECK("splitk_merge_kernel");
   }
   return LV_OK;
 }
@@ -1090,6 +1121,7 @@ static int paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h
   p.items = kind.listed ? reinterpret_cast<const int2*>(ws + s.items_off) : nullptr;
   p.n_items = kind.listed ? reinterpret_cast<const int32_t*>(ws + s.count_off) : nullptr;
   p.ticket = kind.listed ? reinterpret_cast<int32_t*>(ws + s.count_off) + 2 : nullptr;
+  p.merge_count = s.merges > 0 ? reinterpret_cast<int32_t*>(ws + s.merge_off) : nullptr;
 
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int qp = kPrefillRows / p.group;
@@ -1112,7 +1144,8 @@ static int paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h
     record_plan(workspace, nullptr);  // until this plan's launch is accepted, the workspace holds no plan
     hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kScanThreads), 0, st, kind.mixed ? cu_seqlens_q : nullptr,
                        seqlens_k, cu_seqlens_k, num_rows, s.split, qp, s.max_items, (int32_t)sig.last_first,
-                       reinterpret_cast<int2*>(ws + s.items_off), reinterpret_cast<int32_t*>(ws + s.count_off));
+                       reinterpret_cast<int2*>(ws + s.items_off), reinterpret_cast<int32_t*>(ws + s.count_off),
+                       p.merge_count, (int32_t)s.merges);
     LV_LAUNCH_CHECK("plan_kernel");
     planned = true;
   }

@@ -468,12 +468,15 @@ def test_a_mixed_step_of_many_decode_rows_under_both_schedules(cuda, monkeypatch
 # Steps whose layers share one plan, one per launch path of a step: (heads, kv heads, head dim), decode rows
 # (count, key range), prompt rows (cached, new), the schedule, and the route the library takes for them.
 PLAN_STEPS = {
+    # split rows (the first three): each row's last split merges its partials and puts its counter back to zero,
+    # which the two layers on the reused plan rely on
     "decode-pairs": ((32, 8, 128), (256, 16, 600), [], None,
-                     dict(decode_kernel="decode_list", kv_heads_per_item=2, prompt_kernel="none")),
+                     dict(decode_kernel="decode_list", kv_heads_per_item=2, prompt_kernel="none", splitk_merge=True)),
     "decode-small": ((32, 8, 128), None, [], None,
-                     dict(decode_kernel="decode_list", kv_heads_per_item=1, prompt_kernel="none")),
+                     dict(decode_kernel="decode_list", kv_heads_per_item=1, prompt_kernel="none", splitk_merge=True)),
     "mixed-one-launch": ((32, 8, 128), (30, 64, 2048), [(256, 384), (0, 512)], "overlap",
-                         dict(decode_kernel="mixed_small", prompt_kernel="mixed_small", two_streams=False)),
+                         dict(decode_kernel="mixed_small", prompt_kernel="mixed_small", two_streams=False,
+                              splitk_merge=True)),
     "mixed-serial": ((32, 8, 128), (600, 16, 600), [(100, 40), (0, 70)], "serial",
                      dict(decode_kernel="decode_list", prompt_kernel="prompt_list", two_streams=False)),
     "mixed-overlap-list": ((32, 8, 128), (600, 16, 600), [(100, 40), (0, 70)], "overlap",
@@ -501,7 +504,7 @@ def assert_route(info, **want):
 def test_layers_of_one_step_share_one_plan(cuda, kind, monkeypatch):
     """Three layers (each with its own cache) attend through one step's Context: the first plans the work list, the
     next two reuse it (LV_ATTN_REUSE_PLAN). On the persistent grid, the last workgroup of each layer must leave the
-    ticket counters at zero for the next. Each case asserts the launch path it reaches (lv_paged_attention_launch_info
+    ticket counters at zero for the next, and on split rows each row's last split its merge counter. Each case asserts the launch path it reaches (lv_paged_attention_launch_info
     on the call's arguments). Each layer equals the same call on a fresh Context (which plans again), bit for bit;
     the first matches the fp32 oracle; then the three layers are captured in one graph (one plan launch in it) and
     every replay equals the eager layers."""

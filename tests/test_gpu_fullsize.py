@@ -43,8 +43,9 @@ DECODE = dict(prompt_kernel="none", decode_kernel="decode_list", kv_heads_per_it
 ROUTES = {
     "qwen3_8b_mixed": OVERLAP, "qwen3_8b_mixed_bs16": OVERLAP,
     "qwen3_8b_prefill": PROMPTS, "qwen3_8b_prefill_bs16": PROMPTS, "qwen3_8b_prefix_chunk": PROMPTS,
-    "qwen3_8b_decode": DECODE, "qwen3_8b_long": dict(DECODE, splitk_merge=True),
-    "qwen3_0_6b_mixed": dict(prompt_kernel="mixed_small", decode_kernel="mixed_small", kv_heads_per_item=2),
+    "qwen3_8b_decode": dict(DECODE, splitk_merge=True), "qwen3_8b_long": dict(DECODE, splitk_merge=True),
+    "qwen3_0_6b_mixed": dict(prompt_kernel="mixed_small", decode_kernel="mixed_small", kv_heads_per_item=2,
+                             splitk_merge=True),
 }
 
 
