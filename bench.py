@@ -12,11 +12,14 @@ runs it per step:
   through enough copies of the cache that each one starts cold (none is still in the 256 MB Infinity Cache).
 
 The JSON line's ``value`` is the primary workload's algorithmic HBM bytes per step / step time (GB/s), and
-``tokens_per_s_per_layer`` its tokens / (step time / layers). Default primary: Qwen3-8B-shaped chunked-prefill
-mixed batch at token budget 8192 (4 chunks of 1536 new tokens on a cached prefix U[0, 6144], plus 2048 decode rows
-with context U[256, 4096]; 32/8 heads, d128, bf16, 256-token pages). The line also carries per-kernel times from
-HIP events on the launch stream (per layer: store and attention, the attention of the first layer -- which plans
--- and of the later ones), a ``roofline`` object for the attention op (mean over layers), a ``cpu_baseline`` (the
+``tokens_per_s_per_layer`` its tokens / (step time / layers); the timed steps record no events. Default primary:
+Qwen3-8B-shaped chunked-prefill mixed batch at token budget 8192 (4 chunks of 1536 new tokens on a cached prefix
+U[0, 6144], plus 2048 decode rows with context U[256, 4096]; 32/8 heads, d128, bf16, 256-token pages). The line
+also carries per-kernel times from HIP events on the launch stream: the attention op per launch from launches back
+to back between one event pair (a step's worth of layers per rep, the first planning), and, from a few further
+steps with events around each op, per layer: pack, store and attention (bracketed: these include the events' own
+cost, a few microseconds), the attention of the first layer -- which plans -- and of the later ones. Then a
+``roofline`` object for the attention op (per launch, back to back), a ``cpu_baseline`` (the
 oracle's restatement of the reference PyTorch backend timed over the whole step on the host cores, after every GPU
 measurement; batch-256 decode carries one too) and, under
 ``workloads``, the same figures for the other shapes this path is measured on (Qwen3-8B pure decode at batch 256,
@@ -163,72 +166,101 @@ def measure(name: str, steps: int, warmup: int, seed: int, dev, layers: int | No
         max_ctx = max(max(wl.num_cached), 1)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
-    ev_pack = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
-    ev_layer = [[tuple(torch.cuda.Event(enable_timing=True) for _ in range(3)) for _ in range(layers)]
-                for _ in range(steps)]
 
-    def step(i=None):
-        if i is not None:
-            ev_pack[i][0].record(stream)
+    def attend(x, ctx, context):
+        """One layer's attention op."""
+        if wl.is_mla_prefill:
+            ex = x.expanded
+            cu_q, max_q = ctx["cu_seqlens_q"], ctx["max_seqlen_q"]
+            if wl.two_pass:  # the reference layer's calls
+                o, lse = backend.varlen_with_lse(ex["q"], ex["k"], ex["v"], cu_q, cu_q, max_q, max_q, True)
+                co, clse = backend.varlen_with_lse(ex["q"], ex["k_ctx"], ex["v_ctx"], cu_q, cu_ctx, max_q,
+                                                   max_ctx, False)
+                merge_attention_(co, clse, o, lse, out)
+            else:  # one call over context and new keys
+                backend.prefill_with_context(ex["q"], ex["k"], ex["v"], ex["k_ctx"], ex["v_ctx"], cu_q, cu_ctx,
+                                             max_q, out=out)
+        elif wl.is_mla:
+            backend.mla_decode(x.q, x.k_cache, wl.v_dim, context, out=out)
+        else:
+            backend.forward(x.q, x.k_new, x.v_new, x.k_cache, x.v_cache, context, out=out)
+
+    def step(ev=None):
+        """One step; returns the pack's fields. ev: (pack event pair, per layer (start, after the store, after the
+        attention)) to record, or None."""
+        if ev is not None:
+            ev[0][0].record(stream)
         _, ctx = packer.run(plan)
-        if i is not None:
-            ev_pack[i][1].record(stream)
+        if ev is not None:
+            ev[0][1].record(stream)
         context = Context(**{k: v for k, v in ctx.items() if k in Context.__slots__})
         for layer in range(layers):
             x = ts[layer % sets]
-            if i is not None:
-                ev_layer[i][layer][0].record(stream)
+            if ev is not None:
+                ev[1][layer][0].record(stream)
             if wl.is_mla:
                 backend.store_latents(x.k_new, x.k_cache, ctx["slot_mapping"])
             else:
                 backend.store_kvcache(x.k_new, x.v_new, x.k_cache, x.v_cache, ctx["slot_mapping"])
-            if i is not None:
-                ev_layer[i][layer][1].record(stream)
-            if wl.is_mla_prefill:
-                ex = x.expanded
-                cu_q, max_q = ctx["cu_seqlens_q"], ctx["max_seqlen_q"]
-                if wl.two_pass:  # the reference layer's calls
-                    o, lse = backend.varlen_with_lse(ex["q"], ex["k"], ex["v"], cu_q, cu_q, max_q, max_q, True)
-                    co, clse = backend.varlen_with_lse(ex["q"], ex["k_ctx"], ex["v_ctx"], cu_q, cu_ctx, max_q,
-                                                       max_ctx, False)
-                    merge_attention_(co, clse, o, lse, out)
-                else:  # one call over context and new keys
-                    backend.prefill_with_context(ex["q"], ex["k"], ex["v"], ex["k_ctx"], ex["v_ctx"], cu_q, cu_ctx,
-                                                 max_q, out=out)
-            elif wl.is_mla:
-                backend.mla_decode(x.q, x.k_cache, wl.v_dim, context, out=out)
-            else:
-                backend.forward(x.q, x.k_new, x.v_new, x.k_cache, x.v_cache, context, out=out)
-            if i is not None:
-                ev_layer[i][layer][2].record(stream)
+            if ev is not None:
+                ev[1][layer][1].record(stream)
+            attend(x, ctx, context)
+            if ev is not None:
+                ev[1][layer][2].record(stream)
+        return ctx
+
+    def event():
+        return torch.cuda.Event(enable_timing=True)
 
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
+    # The timed steps carry no events: an event costs the GPU a few microseconds, which the layers of a small step
+    # would feel (a Qwen3-0.6B layer's attention reads 37.6 us between its own events against 31.9 us per launch back
+    # to back).
     t0 = time.perf_counter()
-    for i in range(steps):
-        step(i)
+    for _ in range(steps):
+        ctx = step()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    # The per-layer breakdown: a few more steps with events around the pack and each layer's store and attention.
+    n_ev = min(steps, 5)
+    ev = [((event(), event()), [(event(), event(), event()) for _ in range(layers)]) for _ in range(n_ev)]
+    for i in range(n_ev):
+        step(ev[i])
+    torch.cuda.synchronize()
+    # The attention op alone, back to back between one event pair: reps steps' worth of layers on the step's pack
+    # output, each rep through a fresh Context (its first layer plans, as a step's does), the layers rotating
+    # through the cache copies as in a step.
+    reps = min(steps, 5)
+    e0, e1 = event(), event()
+    e0.record(stream)
+    for _ in range(reps):
+        context = Context(**{k: v for k, v in ctx.items() if k in Context.__slots__})
+        for layer in range(layers):
+            attend(ts[layer % sets], ctx, context)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    attn_b2b = e0.elapsed_time(e1) / (reps * layers)
 
     def mean(xs):
         return sum(xs) / len(xs)
 
-    pack_ms = mean([a.elapsed_time(b) for a, b in ev_pack])
-    store_ms = mean([e[0].elapsed_time(e[1]) for st in ev_layer for e in st])
-    attn_ms = mean([e[1].elapsed_time(e[2]) for st in ev_layer for e in st])
-    attn_first = mean([st[0][1].elapsed_time(st[0][2]) for st in ev_layer])
-    attn_later = mean([e[1].elapsed_time(e[2]) for st in ev_layer for e in st[1:]]) if layers > 1 else attn_first
+    pack_ms = mean([a.elapsed_time(b) for (a, b), _ in ev])
+    store_ms = mean([e[0].elapsed_time(e[1]) for _, st in ev for e in st])
+    attn_ms = mean([e[1].elapsed_time(e[2]) for _, st in ev for e in st])
+    attn_first = mean([st[0][1].elapsed_time(st[0][2]) for _, st in ev])
+    attn_later = mean([e[1].elapsed_time(e[2]) for _, st in ev for e in st[1:]]) if layers > 1 else attn_first
     # The attention of the layers on each copy of the cache (later layers): copies are separate allocations, and
     # their placement in HBM moves a decode step's time by a few percent from one allocation to the next.
-    by_set = [mean([st[layer][1].elapsed_time(st[layer][2]) for st in ev_layer
+    by_set = [mean([st[layer][1].elapsed_time(st[layer][2]) for _, st in ev
                     for layer in range(c, layers, sets) if layer > 0 or layers == 1])
               for c in range(min(sets, layers)) if c > 0 or layers == 1 or sets < layers]
     step_ms = wall_ms
     layer_ms = step_ms / layers
     flops = W.algorithmic_flops(wl)
     step_bytes = layers * (nbytes["attention"] + nbytes["store"]) + nbytes["pack"]
-    attn_gbs = nbytes["attention"] / (attn_ms * 1e-3) / 1e9
+    attn_gbs = nbytes["attention"] / (attn_b2b * 1e-3) / 1e9
     figures = {
         "workload": name,
         "rows": wl.rows,
@@ -240,14 +272,17 @@ def measure(name: str, steps: int, warmup: int, seed: int, dev, layers: int | No
         "GBs": round(step_bytes / (step_ms * 1e-3) / 1e9, 1),
         "pct_of_peak_hbm": round(100 * step_bytes / (step_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 2),
         "tokens_per_s_per_layer": round(wl.tokens / (layer_ms * 1e-3), 1),
-        "kernel_ms": {"pack": round(pack_ms, 4), "store": round(store_ms, 4), "attention": round(attn_ms, 4),
-                      "attention_first_layer": round(attn_first, 4), "attention_later_layers": round(attn_later, 4),
+        # attention: per launch, back to back (a step's mix of planning and reusing layers); the bracketed figures
+        # come from an event pair around each layer's op, which adds the events' own cost.
+        "kernel_ms": {"pack": round(pack_ms, 4), "store": round(store_ms, 4), "attention": round(attn_b2b, 4),
+                      "attention_bracketed": round(attn_ms, 4), "attention_first_layer": round(attn_first, 4),
+                      "attention_later_layers": round(attn_later, 4),
                       "attention_by_cache_set": [round(x, 4) for x in by_set]},
         "host_stage_ms": round(host_stage_ms, 4),
         "attention_GBs": round(attn_gbs, 1),
         "attention_frac_of_peak": round(attn_gbs / PEAK_HBM_GBS, 4),
-        "attention_TFLOPs": round(flops / (attn_ms * 1e-3) / 1e12, 2),
-        "attention_frac_of_mfma_peak": round(flops / (attn_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "attention_TFLOPs": round(flops / (attn_b2b * 1e-3) / 1e12, 2),
+        "attention_frac_of_mfma_peak": round(flops / (attn_b2b * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
         "bound": "mfma" if flops / nbytes["attention"] > RIDGE_FLOP_PER_BYTE else "hbm",
         "bytes": nbytes,
         "flops": flops,

@@ -36,9 +36,8 @@ struct AttnParams {
   const int2* items;
   const int32_t* n_items;  // [0]: list length, [1]: prompt items at its head
   int32_t* ticket;         // next decode item of a persistent launch (zeroed by the plan kernel)
-  // Split rows of a listed step: per (row, item head group), the count of its splits that have written their
-  // partials (zeroed by the plan kernel); the last to arrive merges them and puts the count back to zero. Null: the
-  // partials are merged by splitk_merge_kernel after the launch.
+  // Split rows (listed steps only): per (row, item head group), the count of its splits that have written their
+  // partials (zeroed by the plan kernel); the last to arrive merges them and puts the count back to zero.
   int32_t* merge_count;
   // Packed keys only: a row's context keys, seen unmasked before the row's own keys (prefill_item's CTX).
   const char* ctx_k;  // [Tc, Hkv, DQK]
