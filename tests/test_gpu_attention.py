@@ -229,14 +229,20 @@ def test_long_rows_split_over_keys(cuda, dtype):
     check(out, dense_expected(qs, kf, vf, 1 / math.sqrt(128)), dtype)
 
 
-@pytest.mark.parametrize("lens, hp", [((300, 1500, 256), 2), ((30_000, 30_000, 2), 1)], ids=["pairs", "one-head"])
-def test_split_rows_merge_the_same_bits_every_call(cuda, lens, hp):
+@pytest.mark.parametrize("lens, hp, shape, dtype", [
+    ((300, 1500, 256), 2, (32, 8, 128), torch.bfloat16),
+    ((30_000, 30_000, 2), 1, (32, 8, 128), torch.bfloat16),
+    ((9_000, 12_000, 3), 1, (8, 2, 64), torch.float16),
+], ids=["pairs", "one-head", "one-head-d64-fp16"])
+def test_split_rows_merge_the_same_bits_every_call(cuda, lens, hp, shape, dtype):
     """A split row is merged in the decode launch by whichever of its splits counts in last, from partials that the
     other splits, on any XCD, wrote through to memory. The merge reads them in split order, so every call gives the
     same bits whatever the order of arrival, and a stale partial would show as a difference. Eight calls on one
     step (256 rows of 300-1500 keys on pair items; two rows of 30,000 keys in 118 splits of 256 keys on one-head
-    items, eight batches of the merge) must agree bit for bit, and the first with the fp32 oracle."""
+    items, eight batches of the merge; three fp16 rows of 64-wide heads) must agree bit for bit, and the first with
+    the fp32 oracle."""
     lo, hi, rows = lens
+    heads, kv_heads, dim = shape
     bs = 16
     gen = torch.Generator().manual_seed(11)
     ctx_lens = torch.randint(lo, hi + 1, (rows,), generator=gen).tolist()
@@ -246,9 +252,9 @@ def test_split_rows_merge_the_same_bits_every_call(cuda, lens, hp):
         k = -(-n // bs)
         tables.append(list(range(at, at + k)) + [-1] * (width - k))
         at += k
-    b = MI355XAttention(32, 128, 1 / math.sqrt(128), 8)
-    qs, kf, vf, kn, vn, kc, vc, slots = paged_step([n - 1 for n in ctx_lens], [1] * rows, tables, at, heads=32,
-                                                   kv_heads=8, dim=128, bs=bs, device=cuda, dtype=torch.bfloat16)
+    b = MI355XAttention(heads, dim, 1 / math.sqrt(dim), kv_heads)
+    qs, kf, vf, kn, vn, kc, vc, slots = paged_step([n - 1 for n in ctx_lens], [1] * rows, tables, at, heads=heads,
+                                                   kv_heads=kv_heads, dim=dim, bs=bs, device=cuda, dtype=dtype)
     b.store_kvcache(kn, vn, kc, vc, slots)
     ctx = Context(context_lens=torch.tensor(ctx_lens, dtype=torch.int32, device=cuda),
                   block_tables=torch.tensor(tables, dtype=torch.int32, device=cuda))
@@ -261,7 +267,7 @@ def test_split_rows_merge_the_same_bits_every_call(cuda, lens, hp):
     assert info["kv_heads_per_item"] == hp and info["splitk_merge"] and info["max_splits"] > 1, info
     for i, o in enumerate(outs[1:], 1):
         assert torch.equal(o, outs[0]), f"call {i} differs from the first"
-    check(outs[0], dense_expected(qs, kf, vf, 1 / math.sqrt(128)), torch.bfloat16)
+    check(outs[0], dense_expected(qs, kf, vf, 1 / math.sqrt(dim)), dtype)
 
 
 def test_zero_length_rows_give_zeros(cuda):
