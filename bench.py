@@ -443,7 +443,7 @@ def traffic_of(name: str):
 
 def traffic_source(name: str):
     """Where ``roofline.traffic`` comes from: counters can only be read under the profiler, so it is the committed
-    summary of a profiling run (its own box and lease), not this run; its op time is given beside it."""
+    summary of a profiling run (its own machine and session), not this run; its op time is given beside it."""
     f = ROOT / "profiles" / f"traffic_{name}.json"
     if not f.exists():
         return None
@@ -451,7 +451,7 @@ def traffic_source(name: str):
     return {"file": f"profiles/traffic_{name}.json", "measured": "rocprofv3 FETCH_SIZE + WRITE_SIZE over the op's "
             "kernels in a profiling run, scaled by the same counters' reading for a 1 GiB copy",
             "op_span_us_in_that_run": j.get("rocprof_op_span_us_median_later_layers"),
-            "full_bench_attention_us_in_that_lease": j.get("lease_full_bench_attention_us")}
+            "full_bench_attention_us_in_that_session": j.get("session_full_bench_attention_us")}
 
 
 def main():

@@ -2,8 +2,8 @@
 
 This package restates, on the CPU, the algorithms of lean-vLLM's attention path so that the HIP kernels can
 be checked against them. Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg
-may import it, and only as the checker or the timed CPU baseline -- never as the product path. The product
-(``lean-vllm_amd/lvattn``) never imports anything from here.
+may import it, and only as the reference results to compare against or the timed CPU baseline -- never as the
+product path. The product (``lean-vllm_amd/lvattn``) never imports anything from here.
 
 Modules:
 - ``pack``: ragged-batch packing (``lean_vllm/engine/model_runner.py:51-63,349-464``), a vectorised numpy
