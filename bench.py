@@ -223,9 +223,12 @@ def measure(name: str, steps: int, warmup: int, seed: int, dev, layers: int | No
         ctx = step()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
-    # The per-layer breakdown: a few more steps with events around the pack and each layer's store and attention.
+    # The per-layer breakdown: a few more steps with events around the pack and each layer's store and attention,
+    # behind one step without them (so that the GPU is busy when they are queued, as in the timed steps, and no
+    # host time between two launches lands between their events).
     n_ev = min(steps, 5)
     ev = [((event(), event()), [(event(), event(), event()) for _ in range(layers)]) for _ in range(n_ev)]
+    step()
     for i in range(n_ev):
         step(ev[i])
     torch.cuda.synchronize()
