@@ -233,14 +233,15 @@ def test_long_rows_split_over_keys(cuda, dtype):
     ((300, 1500, 256), 2, (32, 8, 128), torch.bfloat16),
     ((30_000, 30_000, 2), 1, (32, 8, 128), torch.bfloat16),
     ((9_000, 12_000, 3), 1, (8, 2, 64), torch.float16),
-], ids=["pairs", "one-head", "one-head-d64-fp16"])
+    ((12_000, 12_000, 8), 2, (6, 2, 128), torch.bfloat16),
+], ids=["pairs", "one-head", "one-head-d64-fp16", "pairs-group3"])
 def test_split_rows_merge_the_same_bits_every_call(cuda, lens, hp, shape, dtype):
     """A split row is merged in the decode launch by whichever of its splits counts in last, from partials that the
     other splits, on any XCD, wrote through to memory. The merge reads them in split order, so every call gives the
     same bits whatever the order of arrival, and a stale partial would show as a difference. Eight calls on one
     step (256 rows of 300-1500 keys on pair items; two rows of 30,000 keys in 118 splits of 256 keys on one-head
-    items, eight batches of the merge; three fp16 rows of 64-wide heads) must agree bit for bit, and the first with
-    the fp32 oracle."""
+    items, eight batches of the merge; three fp16 rows of 64-wide heads; eight rows whose kv pairs each serve three
+    query-head groups of one head) must agree bit for bit, and the first with the fp32 oracle."""
     lo, hi, rows = lens
     heads, kv_heads, dim = shape
     bs = 16
