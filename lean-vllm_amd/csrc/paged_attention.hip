@@ -1027,6 +1027,9 @@ static StepKind step_kind(int32_t num_rows, bool has_cu_q, int32_t max_seqlen_q,
 
 // A launch counts its work-items (workgroups x 256) in 32 bits: the step's largest grid must stay below that.
 static int check_grids(const Shape& s, int32_t num_rows, int32_t num_heads, int32_t num_kv_heads) {
+  // Split rows are merged through the work list's counters: a step without the list must not split.
+  LV_REQUIRE(s.max_splits == 1 || s.merges > 0, "paged_attention: %d rows split over %d items without a work list",
+             num_rows, s.max_splits);
   const int64_t prompt = (int64_t)s.max_prompt_items * num_kv_heads;
   const int64_t decode = std::max<int64_t>(s.max_decode_items, (int64_t)num_rows * s.max_splits) * num_heads;
   LV_REQUIRE((prompt + decode) * 256 < ((int64_t)1 << 32),

@@ -380,12 +380,27 @@ def test_decode_of_more_rows_than_the_planner_holds(cuda):
     b.store_kvcache(kn, vn, kc, vc, slots)
     ctx = Context(context_lens=torch.tensor(lens, dtype=torch.int32, device=cuda),
                   block_tables=torch.tensor(tables, dtype=torch.int32, device=cuda))
+    b.launch_trace = []
     out = b.decode(torch.cat(qs), kc, vc, ctx)
     torch.cuda.synchronize()
+    info = b.launch_trace[-1]
+    assert info["decode_kernel"] == "decode_grid" and info["max_splits"] == 1, info
     math_ = A.TorchMath(H, 64, SCALE, HKV)
     want = A.decode_in_row_chunks(math_, torch.cat(qs).cpu(), kc.cpu(), vc.cpu(), ctx.context_lens.cpu(),
                                   ctx.block_tables.cpu(), rows_per_chunk=500)
     check(out, want, torch.bfloat16)
+
+
+def test_a_step_past_the_work_list_never_splits_its_rows():
+    """Split rows are merged through the work list's counters, so a decode step of more rows than the list holds
+    must not split them, whatever its contexts: the route of 5000 rows of up to 128K keys keeps one item per row
+    (lv_paged_attention_launch_info, the call's own route)."""
+    from lvattn import _capi
+
+    for heads, kv_heads, dim in ((32, 8, 128), (8, 1, 64), (64, 4, 128)):
+        info = _capi.launch_info(5000, 5000, heads, kv_heads, dim, 16, dim, 0, 1, 131072, 0, 0, 0,
+                                 _capi.DTYPES[torch.bfloat16])
+        assert info["decode_kernel"] == "decode_grid" and info["max_splits"] == 1, (heads, kv_heads, info)
 
 
 def test_a_decoder_step_whose_rows_all_carry_drafts(cuda):
