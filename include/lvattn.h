@@ -104,8 +104,8 @@ int lv_store_latents(const void* latent, int64_t latent_stride_t, int32_t num_to
  * Key length of row b: seqlens_k[b] if seqlens_k is non-NULL, else cu_seqlens_k[b+1] - cu_seqlens_k[b].
  * Query j of a row with lq queries and lk keys sees keys 0 .. lk-lq+j (bottom-right causal).
  * A row with no keys gets a zero output.
- * max_seqlen_k bounds every row's key length (block-table width * block_size will do); it sizes the split-K grid
- * so a captured graph needs no length read back. num_tokens is T (it sizes the work list).
+ * max_seqlen_k (at most 2^30) bounds every row's key length (block-table width * block_size will do); it sizes the
+ * split-K grid so a captured graph needs no length read back. num_tokens is T (it sizes the work list).
  * workspace: caller-owned device memory of at least lv_paged_attention_workspace_bytes(...) bytes for the same
  * arguments; its contents need no initialisation.
  * schedule (a step with prompt rows): LV_SCHEDULE_OVERLAP runs the prompt tiles on part of the CUs beside the

@@ -626,9 +626,11 @@ static Shape plan_shape(int32_t rows, int32_t tokens, int32_t hq, int32_t hkv, i
   s.split = (int32_t)split;
   s.max_splits = (int32_t)((keys + split - 1) / split);
   const int qp = kPrefillRows / (group > 0 ? group : 1);
-  s.max_prompt_items = listed ? (tokens + qp - 1) / qp + rows : 0;
-  s.max_decode_items = listed ? rows * s.max_splits : 0;
-  s.max_items = s.max_prompt_items + s.max_decode_items;
+  // In 64 bits, saturated: a count past INT32_MAX is far past what one launch holds (check_grids refuses it).
+  auto sat = [](int64_t x) { return (int32_t)std::min<int64_t>(x, INT32_MAX); };
+  s.max_prompt_items = listed ? sat(((int64_t)tokens + qp - 1) / qp + rows) : 0;
+  s.max_decode_items = listed ? sat((int64_t)rows * s.max_splits) : 0;
+  s.max_items = sat((int64_t)s.max_prompt_items + s.max_decode_items);
   size_t off = 0;
   s.items_off = off;
   off += (size_t)s.max_items * sizeof(int2);
@@ -1008,7 +1010,8 @@ static int check_shape(int32_t num_rows, int32_t num_tokens, int32_t num_heads, 
              block_size, kTile);
   LV_REQUIRE(has_cu_q || num_tokens == num_rows, "paged_attention: without cu_seqlens_q, T (%d) must equal B (%d)",
              num_tokens, num_rows);
-  LV_REQUIRE(max_seqlen_k >= 0, "paged_attention: negative max_seqlen_k");
+  LV_REQUIRE(max_seqlen_k >= 0 && max_seqlen_k <= (1 << 30), "paged_attention: max_seqlen_k %d is negative or above "
+             "2^30 keys", max_seqlen_k);
   LV_REQUIRE(!(has_cu_q && max_seqlen_q > 1) || num_rows <= kPlanMaxRows,
              "paged_attention: a step with prompts holds at most %d rows, got %d", kPlanMaxRows, num_rows);
   return LV_OK;
@@ -1170,7 +1173,9 @@ using namespace lv;
 extern "C" size_t lv_paged_attention_workspace_bytes(int32_t num_rows, int32_t num_tokens, int32_t num_heads,
                                                      int32_t num_kv_heads, int32_t head_dim, int32_t max_seqlen_k,
                                                      int32_t decode_only) {
-  if (num_rows <= 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads) return 0;
+  if (num_rows <= 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads || max_seqlen_k < 0 ||
+      max_seqlen_k > (1 << 30))
+    return 0;
   const bool mixed = decode_only == 0;
   const bool listed = mixed || num_rows <= kPlanMaxRows;
   return plan_shape(num_rows, num_tokens, num_heads, num_kv_heads, head_dim, max_seqlen_k, listed).bytes;

@@ -70,16 +70,28 @@ static int64_t varlen_qtiles(int dqk, int dv, int group, int max_seqlen_q) {
   else if (dqk == 192 && dv == 192) rows = VarlenCfg<192, 192>::kRows;
   if (rows == 0 || group > rows) return 0;
   const int qp = rows / group;
-  return (max_seqlen_q + qp - 1) / qp;
+  return ((int64_t)max_seqlen_q + qp - 1) / qp;
+}
+
+// Threads per workgroup for a (q.k, v) width pair; 0 for unsupported widths.
+static int varlen_threads(int dqk, int dv) {
+  if (dqk == 64 && dv == 64) return 64 * VarlenCfg<64, 64>::kWaves;
+  if (dqk == 128 && dv == 128) return 64 * VarlenCfg<128, 128>::kWaves;
+  if (dqk == 192 && dv == 128) return 64 * VarlenCfg<192, 128>::kWaves;
+  if (dqk == 192 && dv == 192) return 64 * VarlenCfg<192, 192>::kWaves;
+  return 0;
+}
+
+// Workgroups of a launch over `groups` (kv head, row) groups of `qtiles` query tiles: each XCD gets a whole number
+// of virtual groups, ceil(virtual groups / 8) times their query tiles.
+static int64_t varlen_grid(int64_t groups, int64_t qtiles) {
+  const int S = xcds_per_group((int)std::min<int64_t>(groups, kXcds));
+  return (groups * S + kXcds - 1) / kXcds * ((qtiles + S - 1) / S) * kXcds;
 }
 
 template <typename T, int DQK, int DV>
 static void launch_one(const AttnParams& p, int qtiles, hipStream_t st) {
-  // Each XCD gets a whole number of virtual groups: ceil(virtual groups / 8) times their query tiles.
-  const int64_t groups = (int64_t)p.rows * p.hkv;
-  const int S = xcds_per_group((int)std::min<int64_t>(groups, kXcds));
-  const int64_t per_xcd = (groups * S + kXcds - 1) / kXcds * ((qtiles + S - 1) / S);
-  const dim3 grid(per_xcd * kXcds), block(64 * VarlenCfg<DQK, DV>::kWaves);
+  const dim3 grid((uint32_t)varlen_grid((int64_t)p.rows * p.hkv, qtiles)), block(64 * VarlenCfg<DQK, DV>::kWaves);
   if (p.cu_ctx)
     hipLaunchKernelGGL((varlen_kernel<T, DQK, DV, true>), grid, block, 0, st, p, qtiles);
   else
@@ -179,8 +191,11 @@ static int varlen_attention(const void* q, int64_t q_stride_t, int64_t q_stride_
   const int64_t qtiles = varlen_qtiles(head_dim_qk, head_dim_v, p.group, max_seqlen_q);
   LV_REQUIRE(qtiles > 0, "varlen_attention: head dims (q.k %d, v %d) are not (64, 64), (128, 128), (192, 128) or "
              "(192, 192)", head_dim_qk, head_dim_v);
-  LV_REQUIRE((((int64_t)num_rows * num_kv_heads + kXcds - 1) / kXcds) * qtiles * kXcds < ((int64_t)1 << 31),
-             "varlen_attention: grid too large");
+  // A launch counts its work-items (workgroups x threads) in 32 bits.
+  const int64_t wgs = varlen_grid((int64_t)num_rows * num_kv_heads, qtiles);
+  LV_REQUIRE(wgs * varlen_threads(head_dim_qk, head_dim_v) < ((int64_t)1 << 32),
+             "varlen_attention: %d rows x %d kv heads x %lld query tiles need %lld workgroups, more than one launch "
+             "holds", num_rows, num_kv_heads, (long long)qtiles, (long long)wgs);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   return dtype == LV_DTYPE_BF16 ? launch_varlen<BF16>(p, head_dim_qk, head_dim_v, (int)qtiles, st)
                                 : launch_varlen<F16>(p, head_dim_qk, head_dim_v, (int)qtiles, st);

@@ -73,7 +73,8 @@ def test_the_static_workspace_refuses_a_step_that_needs_more():
     non-null pointers: the call returns before using them.)"""
     # Split-K keeps a step's partials under 9 MiB at any context length; a step of 2^25 prompt tokens over one kv
     # head needs a work list of 2M items (16.8 MB) and still fits one launch.
-    assert _capi.query("lv_paged_attention_workspace_bytes", 4096, 4096, 32, 8, 128, (1 << 31) - 1, 1) < 9 << 20
+    assert _capi.query("lv_paged_attention_workspace_bytes", 4096, 4096, 32, 8, 128, 1 << 30, 1) < 9 << 20
+    assert _capi.query("lv_paged_attention_workspace_bytes", 4096, 4096, 32, 8, 128, (1 << 30) + 1, 1) == 0
     tokens = 1 << 25
     need = _capi.query("lv_paged_attention_workspace_bytes", 4096, tokens, 8, 1, 128, 1 << 20, 0)
     assert need > 16 << 20
@@ -97,6 +98,14 @@ def test_the_launch_query_checks_its_shape_before_touching_the_gpu():
     assert info["decode_kernel"] == info["prompt_kernel"] == "none"
 
 
+def test_a_key_bound_past_2_30_is_refused():
+    """max_seqlen_k sizes the split-K grid in 32-bit counts: a bound above 2^30 keys is refused by the call (and sizes
+    no workspace) before the GPU is touched."""
+    with pytest.raises(_capi.LvError, match="max_seqlen_k 1073741825 is negative or above 2\\^30 keys"):
+        _capi.call("lv_paged_attention", 16, 0, 0, 16, 16, 0, 0, 0, 256, 16, 0, None, 16, None, 5000, 5000, 32, 8, 128,
+                   1.0, 1, (1 << 30) + 1, 16, 0, 0, 256, 1 << 40, 0, 0, 0, 0, None)
+
+
 def test_a_step_too_large_for_one_launch_is_refused():
     """A step whose prompt grid would pass the 32-bit work-item count of one launch is refused with a message, by
     the call and by the launch query alike, before anything touches the GPU (fake non-null pointers)."""
@@ -106,3 +115,16 @@ def test_a_step_too_large_for_one_launch_is_refused():
     with pytest.raises(_capi.LvError, match="more than one launch holds"):
         _capi.call("lv_paged_attention", 16, 0, 0, 16, 16, 0, 0, 0, 256, 16, 0, 16, None, 16, 4096, tokens, 32, 8, 128,
                    1.0, 1 << 20, 1 << 20, 16, 0, 0, 256, 1 << 40, 0, 0, 0, 0, None)
+
+
+def test_a_varlen_call_too_large_for_one_launch_is_refused():
+    """Attention over packed keys counts workgroups x threads against the same 32-bit limit: one row of up to
+    2^31 - 1 queries over 8 kv heads needs 134M workgroups of 256 threads, refused before the GPU is touched (fake
+    non-null pointers); both entry points share the check."""
+    q_max = (1 << 31) - 1
+    with pytest.raises(_capi.LvError, match="need 134217728 workgroups, more than one launch holds"):
+        _capi.call("lv_varlen_attention", 16, 0, 0, 16, 0, 0, 16, 0, 0, 16, 16, 1, 8, 8, 128, 128, 1.0, 1, q_max, 16,
+                   0, 0, None, 0, 0, 0, None)
+    with pytest.raises(_capi.LvError, match="more than one launch holds"):
+        _capi.call("lv_varlen_context_attention", 16, 0, 0, 16, 0, 0, 16, 0, 0, 16, 16, 16, 0, 0, 16, 0, 0, 16, 1, 16,
+                   16, 192, 128, 1.0, q_max, 16, 0, 0, None, 0, 0, 0, None)
