@@ -45,6 +45,11 @@ const char* last_error();
 
 inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
+// A launch counts the work-items along each grid dimension (workgroups x threads along it) in 32 bits.
+inline bool fits_one_launch(int64_t workgroups, int64_t threads) {
+  return workgroups >= 0 && workgroups * threads < ((int64_t)1 << 32);
+}
+
 // ---------------------------------------------------------------------------------------------------------
 // Vector types and element conversion.
 

@@ -97,6 +97,8 @@ extern "C" int lv_merge_attn_states(void* out, int64_t out_stride_t, int64_t out
              "merge_attn_states: bad sizes T=%d H=%d D=%d", num_tokens, num_heads, head_dim);
   if (num_tokens == 0) return LV_OK;
   LV_REQUIRE(out && o_a && lse_a && o_b && lse_b, "merge_attn_states: null pointer");
+  LV_REQUIRE(fits_one_launch(num_tokens, 64) && num_heads < 65536,
+             "merge_attn_states: %d tokens x %d heads need a grid larger than one launch holds", num_tokens, num_heads);
   const dim3 grid(num_tokens, num_heads);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int64_t e = 2;
@@ -108,15 +110,15 @@ extern "C" int lv_merge_attn_states(void* out, int64_t out_stride_t, int64_t out
     const int lpr = head_dim / 8;
     const int rpb = 256 / lpr;
     const int64_t rows = (int64_t)num_tokens * num_heads;
-    LV_REQUIRE(rows < ((int64_t)1 << 31), "merge_attn_states: too many rows");
-    const int blocks = (int)((rows + rpb - 1) / rpb);
+    const int64_t blocks = (rows + rpb - 1) / rpb;
+    LV_REQUIRE(rows < ((int64_t)1 << 31) && fits_one_launch(blocks, rpb * lpr), "merge_attn_states: too many rows");
     if (dtype == LV_DTYPE_BF16)
-      hipLaunchKernelGGL(merge_states_vec_kernel<BF16>, dim3(blocks), dim3(rpb * lpr), 0, s, (char*)out,
+      hipLaunchKernelGGL(merge_states_vec_kernel<BF16>, dim3((uint32_t)blocks), dim3(rpb * lpr), 0, s, (char*)out,
                          out_stride_t * e, out_stride_h * e, (const char*)o_a, oa_stride_t * e, oa_stride_h * e,
                          lse_a, lsea_stride_t, lsea_stride_h, (const char*)o_b, ob_stride_t * e, ob_stride_h * e,
                          lse_b, lseb_stride_t, lseb_stride_h, (int32_t)rows, num_heads, lpr);
     else
-      hipLaunchKernelGGL(merge_states_vec_kernel<F16>, dim3(blocks), dim3(rpb * lpr), 0, s, (char*)out,
+      hipLaunchKernelGGL(merge_states_vec_kernel<F16>, dim3((uint32_t)blocks), dim3(rpb * lpr), 0, s, (char*)out,
                          out_stride_t * e, out_stride_h * e, (const char*)o_a, oa_stride_t * e, oa_stride_h * e,
                          lse_a, lsea_stride_t, lsea_stride_h, (const char*)o_b, ob_stride_t * e, ob_stride_h * e,
                          lse_b, lseb_stride_t, lseb_stride_h, (int32_t)rows, num_heads, lpr);

@@ -708,9 +708,11 @@ extern "C" int lv_mla_decode(const void* q, int64_t q_stride_t, int64_t q_stride
   LV_REQUIRE(workspace_bytes >= s.bytes && (s.bytes == 0 || workspace),
              "mla_decode: workspace of %zu bytes given, %zu needed", workspace_bytes, s.bytes);
   LV_REQUIRE(aligned(workspace, 256), "mla_decode: workspace must be 256-byte aligned");
-  LV_REQUIRE((int64_t)num_rows * s.max_splits < ((int64_t)1 << 31) &&
+  LV_REQUIRE(fits_one_launch((int64_t)num_rows * s.max_splits, 256) &&
+                 fits_one_launch((int64_t)num_rows * queries_per_row, 64) &&
                  (int64_t)queries_per_row * ((num_heads + 15) / 16) < 65536,
-             "mla_decode: launch grid too large");
+             "mla_decode: %d rows x %d queries x %d splits need a grid larger than one launch holds", num_rows,
+             queries_per_row, s.max_splits);
 
   MlaParams p{};
   p.q = (const char*)q;

@@ -1035,7 +1035,7 @@ static int check_grids(const Shape& s, int32_t num_rows, int32_t num_heads, int3
              num_rows, s.max_splits);
   const int64_t prompt = (int64_t)s.max_prompt_items * num_kv_heads;
   const int64_t decode = std::max<int64_t>(s.max_decode_items, (int64_t)num_rows * s.max_splits) * num_heads;
-  LV_REQUIRE((prompt + decode) * 256 < ((int64_t)1 << 32),
+  LV_REQUIRE(fits_one_launch(prompt + decode, 256),
              "paged_attention: the step needs %lld + %lld workgroups, more than one launch holds", (long long)prompt,
              (long long)decode);
   return LV_OK;

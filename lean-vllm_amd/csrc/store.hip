@@ -138,9 +138,12 @@ extern "C" int lv_store_kvcache(const void* key, const void* value, int64_t key_
   const int32_t ppr = (int32_t)(row_bytes / vec);
   const int threads = ppr * 2 >= 256 ? 256 : ((ppr * 2 + 63) / 64) * 64;
   const int shares = (ppr * 2 + threads - 1) / threads;
+  const int64_t blocks = ((int64_t)num_tokens + kStoreTokens - 1) / kStoreTokens;
+  LV_REQUIRE(fits_one_launch(blocks, threads), "store_kvcache: %d tokens need a grid larger than one launch holds",
+             num_tokens);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
 #define LV_STORE_LAUNCH(V)                                                                                     \
-  hipLaunchKernelGGL(store_kv_kernel<V>, dim3((num_tokens + kStoreTokens - 1) / kStoreTokens, shares),       \
+  hipLaunchKernelGGL(store_kv_kernel<V>, dim3((uint32_t)blocks, shares),                                      \
                      dim3(threads), 0,                                                                         \
                      s, (const char*)key, (const char*)value, key_stride_t * eb, value_stride_t * eb, pph, ppr,  \
                      (char*)k_cache, (char*)v_cache, cache_stride_block * eb, cache_stride_token * eb,           \
@@ -168,6 +171,8 @@ extern "C" int lv_store_latents(const void* latent, int64_t latent_stride_t, int
   const int64_t row = (int64_t)dim * eb;
   const int vec = piece_bytes({row, latent_stride_t * eb}, {latent, cache});
   const int32_t pieces = (int32_t)(row / vec);
+  LV_REQUIRE(fits_one_launch(num_tokens, 128) && (pieces + 127) / 128 < 65536,
+             "store_latents: %d tokens of %d bytes need a grid larger than one launch holds", num_tokens, (int)row);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
 #define LV_LATENT_LAUNCH(V)                                                                                    \
   hipLaunchKernelGGL(store_latent_kernel<V>, dim3(num_tokens, (pieces + 127) / 128), dim3(128), 0, s,          \

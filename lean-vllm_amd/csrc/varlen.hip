@@ -191,9 +191,8 @@ static int varlen_attention(const void* q, int64_t q_stride_t, int64_t q_stride_
   const int64_t qtiles = varlen_qtiles(head_dim_qk, head_dim_v, p.group, max_seqlen_q);
   LV_REQUIRE(qtiles > 0, "varlen_attention: head dims (q.k %d, v %d) are not (64, 64), (128, 128), (192, 128) or "
              "(192, 192)", head_dim_qk, head_dim_v);
-  // A launch counts its work-items (workgroups x threads) in 32 bits.
   const int64_t wgs = varlen_grid((int64_t)num_rows * num_kv_heads, qtiles);
-  LV_REQUIRE(wgs * varlen_threads(head_dim_qk, head_dim_v) < ((int64_t)1 << 32),
+  LV_REQUIRE(fits_one_launch(wgs, varlen_threads(head_dim_qk, head_dim_v)),
              "varlen_attention: %d rows x %d kv heads x %lld query tiles need %lld workgroups, more than one launch "
              "holds", num_rows, num_kv_heads, (long long)qtiles, (long long)wgs);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);

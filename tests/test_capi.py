@@ -98,6 +98,20 @@ def test_the_launch_query_checks_its_shape_before_touching_the_gpu():
     assert info["decode_kernel"] == info["prompt_kernel"] == "none"
 
 
+def test_stores_and_merges_too_large_for_one_launch_are_refused():
+    """Every launch counts the work-items along a grid dimension in 32 bits: a scatter of 2^31 - 1 tokens, a latent
+    scatter of 2^25 tokens and a merge of 2^26 token rows are refused with a message before the GPU is touched (fake
+    non-null, 16-byte-aligned pointers)."""
+    big = (1 << 31) - 1
+    with pytest.raises(_capi.LvError, match="store_kvcache: 2147483647 tokens need a grid larger than one launch"):
+        _capi.call("lv_store_kvcache", 16, 16, 1024, 1024, big, 8, 128, 16, 16, 16 * 1024, 1024, 128, 16, 16, 2, None)
+    with pytest.raises(_capi.LvError, match="store_latents: 33554432 tokens of 1152 bytes need a grid larger"):
+        _capi.call("lv_store_latents", 16, 576, 1 << 25, 576, 16, 16, 2, None)
+    with pytest.raises(_capi.LvError, match="merge_attn_states: 67108864 tokens x 1 heads need a grid larger"):
+        _capi.call("lv_merge_attn_states", 16, 128, 128, 16, 128, 128, 16, 1, 1, 16, 128, 128, 16, 1, 1, 1 << 26, 1,
+                   128, 0, None)
+
+
 def test_a_key_bound_past_2_30_is_refused():
     """max_seqlen_k sizes the split-K grid in 32-bit counts: a bound above 2^30 keys is refused by the call (and sizes
     no workspace) before the GPU is touched."""
