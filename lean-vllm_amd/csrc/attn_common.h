@@ -394,7 +394,7 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
 #pragma unroll
             for (int qq = 1; qq < TP; ++qq) page = q == qq ? pg[qq] : page;
             const char* base = (isk ? p.k_cache : p.v_cache) + (int64_t)page * p.c_sb + kvh * (isk ? p.c_sh : p.v_sh);
-            const uint32_t off = (uint32_t)((min(key, last) - q * BS) * (int)(isk ? p.c_st : p.v_st) + chunk * 16);
+            const uint32_t off = __umul24(min(key, last) - q * BS, (uint32_t)(isk ? p.c_st : p.v_st)) + chunk * 16;
             lds_dma16<false>(base, off, lds_addr(stage + 64 * 8 * j));  // tiles other query tiles read again
           }
         }
@@ -430,7 +430,7 @@ __device__ void prefill_item(const AttnParams& p, int row, int qtile, int kvh, c
           const int kkey = slot / KJ, vkey = slot / VJ;
           const int key = isk ? kkey : vkey;
           const int chunk = isk ? min(slot - kkey * KJ, KCH - 1) : min(slot - vkey * VJ, VCH - 1);
-          const uint32_t off = (uint32_t)(min(key, last) * (int)(isk ? kst : vst) + chunk * 16);
+          const uint32_t off = __umul24(min(key, last), (uint32_t)(isk ? kst : vst)) + chunk * 16;
           lds_dma16<false>(isk ? kb : vb, off, lds_addr(stage + 64 * 8 * j));  // tiles other query tiles read again
         }
       }

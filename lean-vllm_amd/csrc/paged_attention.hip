@@ -1078,8 +1078,9 @@ static int paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h
                  (out_stride_h * 2) % 16 == 0 && (cache_stride_block * 2) % 16 == 0 &&
                  (cache_stride_token * 2) % 16 == 0 && (cache_stride_head * 2) % 16 == 0,
              "paged_attention: tensors and their strides must be 16-byte aligned");
-  // A decode lane addresses its rows inside a 16-token tile with 32-bit byte offsets.
-  LV_REQUIRE(cache_stride_token >= 0 && (int64_t)kTile * cache_stride_token * 2 < (int64_t)1 << 30,
+  // Lanes address their rows inside a 16-token decode tile or a 64-key prompt tile with 32-bit byte offsets, the
+  // prompt tile's as 24-bit products (key row times token stride).
+  LV_REQUIRE(cache_stride_token >= 0 && (int64_t)kPrefillKeys * cache_stride_token * 2 < (int64_t)1 << 30,
              "paged_attention: cache token stride %lld is negative or too large", (long long)cache_stride_token);
   LV_REQUIRE(scale > 0.f, "paged_attention: the softmax scale must be positive, got %g", (double)scale);
   const StepKind kind = step_kind(num_rows, cu_seqlens_q != nullptr, max_seqlen_q, schedule, prompt_workgroups, flags);

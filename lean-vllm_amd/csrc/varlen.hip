@@ -145,8 +145,16 @@ static int varlen_attention(const void* q, int64_t q_stride_t, int64_t q_stride_
                  (v_stride_t * 2) % 16 == 0 && (v_stride_h * 2) % 16 == 0 && (out_stride_t * 2) % 8 == 0 &&
                  (out_stride_h * 2) % 8 == 0,
              "varlen_attention: tensors and their strides must be 16-byte aligned");
+  // Lanes address the rows of a 64-key tile with 32-bit byte offsets, as 24-bit products (key row times token
+  // stride).
+  auto row_stride_ok = [](int64_t st) { return st >= 0 && (int64_t)kPrefillKeys * st * 2 < ((int64_t)1 << 30); };
+  LV_REQUIRE(row_stride_ok(k_stride_t) && row_stride_ok(v_stride_t), "varlen_attention: key token stride %lld or "
+             "value token stride %lld is negative or too large", (long long)k_stride_t, (long long)v_stride_t);
   if (cu_seqlens_ctx) {
     LV_REQUIRE(ctx_k && ctx_v, "varlen_context_attention: null context key or value pointer");
+    LV_REQUIRE(row_stride_ok(ctx_k_stride_t) && row_stride_ok(ctx_v_stride_t), "varlen_context_attention: context "
+               "token stride %lld or %lld is negative or too large", (long long)ctx_k_stride_t,
+               (long long)ctx_v_stride_t);
     LV_REQUIRE(aligned(ctx_k, 16) && aligned(ctx_v, 16) && (ctx_k_stride_t * 2) % 16 == 0 &&
                    (ctx_k_stride_h * 2) % 16 == 0 && (ctx_v_stride_t * 2) % 16 == 0 &&
                    (ctx_v_stride_h * 2) % 16 == 0,

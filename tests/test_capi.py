@@ -142,3 +142,19 @@ def test_a_varlen_call_too_large_for_one_launch_is_refused():
     with pytest.raises(_capi.LvError, match="more than one launch holds"):
         _capi.call("lv_varlen_context_attention", 16, 0, 0, 16, 0, 0, 16, 0, 0, 16, 16, 16, 0, 0, 16, 0, 0, 16, 1, 16,
                    16, 192, 128, 1.0, q_max, 16, 0, 0, None, 0, 0, 0, None)
+
+
+def test_token_strides_too_large_for_the_tile_offsets_are_refused():
+    """Lanes address the rows of a 64-key tile with 32-bit offsets, computed as 24-bit products of key row and token
+    stride: a cache or packed-key token stride of 2^23 elements (64 rows span 2^30 bytes) is refused by paged
+    attention and by both packed-key entry points before the GPU is touched (fake non-null pointers)."""
+    st = 1 << 23
+    with pytest.raises(_capi.LvError, match="cache token stride 8388608 is negative or too large"):
+        _capi.call("lv_paged_attention", 16, 0, 0, 16, 16, 0, st, 0, 256, 16, 0, None, 16, None, 1, 1, 32, 8, 128,
+                   1.0, 1, 1024, 16, 0, 0, 256, 1 << 40, 0, 0, 0, 0, None)
+    with pytest.raises(_capi.LvError, match="key token stride 8388608 or value token stride 0 is negative or too"):
+        _capi.call("lv_varlen_attention", 16, 0, 0, 16, st, 0, 16, 0, 0, 16, 16, 1, 8, 8, 128, 128, 1.0, 1, 16, 16,
+                   0, 0, None, 0, 0, 0, None)
+    with pytest.raises(_capi.LvError, match="context token stride 0 or 8388608 is negative or too large"):
+        _capi.call("lv_varlen_context_attention", 16, 0, 0, 16, 0, 0, 16, 0, 0, 16, 16, 16, 0, 0, 16, st, 0, 16, 1, 16,
+                   16, 192, 128, 1.0, 16, 16, 0, 0, None, 0, 0, 0, None)
