@@ -99,7 +99,8 @@ int lv_store_latents(const void* latent, int64_t latent_stride_t, int32_t num_to
  * math of TorchAttention.decode/prefill, lean_vllm/attention/torch_backend.py:62-103).
  *
  * q: [T, Hq, D] (strides q_stride_t, q_stride_h; unit dim stride). out: same shape, own strides.
- * Caches as lv_store_kvcache. block_tables: [B, *] int32 with row stride table_stride.
+ * Caches as lv_store_kvcache, with 64 * cache_stride_token * 2 below 2^30 (a token row under 16 MiB).
+ * block_tables: [B, *] int32 with row stride table_stride.
  * cu_seqlens_q: [B+1], or NULL for one query per row (decode; T == B).
  * Key length of row b: seqlens_k[b] if seqlens_k is non-NULL, else cu_seqlens_k[b+1] - cu_seqlens_k[b].
  * Query j of a row with lq queries and lk keys sees keys 0 .. lk-lq+j (bottom-right causal).
@@ -205,7 +206,8 @@ int lv_paged_attention_static(const void* q, int64_t q_stride_t, int64_t q_strid
  * and varlen_with_lse, lean_vllm/attention/torch_backend.py:62-91): the warmup prefill and MLA prefill chunks.
  *
  * q: [T, Hq, head_dim_qk], k: [Tk, Hkv, head_dim_qk], v: [Tk, Hkv, head_dim_v], each with its own token and head
- * strides (elements) and unit dim stride; rows given by cu_seqlens_q / cu_seqlens_k [num_rows + 1] (device).
+ * strides (elements) and unit dim stride, 64 * token stride * 2 below 2^30; rows given by cu_seqlens_q /
+ * cu_seqlens_k [num_rows + 1] (device).
  * causal != 0: query j of a row with lq queries and lk keys sees keys 0 .. lk - lq + j; else all of its row's keys.
  * out: [T, Hq, head_dim_v]. lse (optional, may be NULL): fp32 [T, Hq] natural log-sum-exp of each query row's
  * scaled scores (-inf for a row with no keys). max_seqlen_q bounds every row's query count (it sizes the grid).
@@ -223,7 +225,8 @@ int lv_varlen_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h, c
  * attention, computed as one softmax per query over [context keys; new keys] with no partial outputs.
  *
  * As lv_varlen_attention with causal = 1, plus each row's context keys ctx_k: [Tc, Hkv, head_dim_qk], ctx_v:
- * [Tc, Hkv, head_dim_v] (token and head strides in elements, unit dim stride), rows given by cu_seqlens_ctx
+ * [Tc, Hkv, head_dim_v] (token and head strides in elements, token strides bounded as k's, unit dim stride), rows
+ * given by cu_seqlens_ctx
  * [num_rows + 1] (device; a row may have none). Every query of a row sees all of its context keys, then its own
  * keys under the causal mask. lse (optional) is over both. No workspace. */
 int lv_varlen_context_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k,
