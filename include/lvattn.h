@@ -226,9 +226,8 @@ int lv_varlen_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h, c
  *
  * As lv_varlen_attention with causal = 1, plus each row's context keys ctx_k: [Tc, Hkv, head_dim_qk], ctx_v:
  * [Tc, Hkv, head_dim_v] (token and head strides in elements, token strides bounded as k's, unit dim stride), rows
- * given by cu_seqlens_ctx
- * [num_rows + 1] (device; a row may have none). Every query of a row sees all of its context keys, then its own
- * keys under the causal mask. lse (optional) is over both. No workspace. */
+ * given by cu_seqlens_ctx [num_rows + 1] (device; a row may have none). Every query of a row sees all of its
+ * context keys, then its own keys under the causal mask. lse (optional) is over both. No workspace. */
 int lv_varlen_context_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k,
                                 int64_t k_stride_t, int64_t k_stride_h, const void* v, int64_t v_stride_t,
                                 int64_t v_stride_h, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
