@@ -17,15 +17,20 @@ def randn(*shape, gen, device, dtype):
 
 
 def paged_step(num_cached, num_new, tables, nblocks, *, heads, kv_heads, dim, bs, device, dtype, seed=0,
-               layout="NHD", fill=0.0):
+               layout="NHD", fill=0.0, token_stride=None):
     """A step whose rows have ``num_cached`` keys already in the cache and ``num_new`` new ones.
 
     Returns (q_list, k_full, v_full, k_new, v_new, k_cache, v_cache, slot_mapping): the cache holds every prefix
-    key; the new keys are NOT yet stored (``slot_mapping`` says where they go).
+    key; the new keys are NOT yet stored (``slot_mapping`` says where they go). ``token_stride`` (NHD only): the
+    caches are views whose token rows lie that many elements apart.
     """
     gen = torch.Generator()
     gen.manual_seed(seed)
-    if layout == "NHD":
+    if token_stride is not None:
+        assert layout == "NHD" and token_stride >= kv_heads * dim
+        k_cache, v_cache = (torch.full((nblocks * bs, token_stride), fill, dtype=dtype, device=device)
+                            [:, :kv_heads * dim].view(nblocks, bs, kv_heads, dim) for _ in range(2))
+    elif layout == "NHD":
         k_cache = torch.full((nblocks, bs, kv_heads, dim), fill, dtype=dtype, device=device)
         v_cache = torch.full((nblocks, bs, kv_heads, dim), fill, dtype=dtype, device=device)
     else:  # (block, head, token, dim) underneath, seen as (block, token, head, dim)

@@ -179,6 +179,35 @@ def test_an_hnd_cache_stores_and_attends_as_an_nhd_one(case):
     torch.testing.assert_close(hnd, nhd, atol=0, rtol=0)
 
 
+# Token rows 2^23 - 8 elements (16 MiB) apart: a 64-key tile spans just under 2^30 bytes, the largest token stride
+# the library accepts.
+WIDE_STRIDE = (1 << 23) - 8
+
+
+@pytest.mark.parametrize("bs", [16, 64])
+def test_token_rows_at_the_largest_accepted_stride(cuda, bs):
+    """Caches whose token rows lie 16 MiB apart: the prompt tiles' 24-bit row offsets and the decode tiles' 32-bit
+    ones reach their largest values. A chunk on a prefix beside two decode rows gives the same bits as with packed
+    caches and matches the dense oracle; pages of 16 keys take the swizzled stage, pages of 64 the padded one."""
+    dtype, dim = torch.bfloat16, 128
+    b = MI355XAttention(H, dim, SCALE, HKV)
+    num_cached, num_new = [100, 70, 5], [40, 1, 1]
+    per = [-(-(c + n) // bs) for c, n in zip(num_cached, num_new)]
+    starts = [sum(per[:i]) for i in range(len(per))]
+    tables = [list(range(s0, s0 + k)) + [-1] * (max(per) - k) for s0, k in zip(starts, per)]
+    outs = []
+    for stride in (None, WIDE_STRIDE):
+        qs, kf, vf, kn, vn, kc, vc, slots = paged_step(num_cached, num_new, tables, sum(per), heads=H, kv_heads=HKV,
+                                                       dim=dim, bs=bs, device=cuda, dtype=dtype, token_stride=stride)
+        assert stride is None or kc.stride(1) == vc.stride(1) == stride
+        b.store_kvcache(kn, vn, kc, vc, slots)
+        outs.append(b.forward(torch.cat(qs), kn, vn, kc, vc, context_for(num_cached, num_new, tables, cuda)))
+        torch.cuda.synchronize()
+        del kc, vc
+    assert torch.equal(outs[0], outs[1])
+    check(outs[1], dense_expected(qs, kf, vf, SCALE), dtype)
+
+
 def test_low_precision_no_worse_than_naive(cuda):
     """tests/test_attention_backends.py:705-753: bf16 error against fp32 at most twice naive bf16 arithmetic's."""
     b = MI355XAttention(H, 64, SCALE, HKV)

@@ -270,6 +270,54 @@ def test_prefill_with_context_writes_into_a_strided_out(cuda):
     assert torch.equal(wide[..., :vd], want) and (wide[..., vd:] == 3.0).all()
 
 
+# Token rows 2^23 - 8 elements (16 MiB) apart: a 64-key tile spans just under 2^30 bytes, the largest token stride
+# the library accepts.
+WIDE_STRIDE = (1 << 23) - 8
+
+
+def widen(x):
+    """The same values with token rows WIDE_STRIDE elements apart."""
+    t, h, d = x.shape
+    w = torch.empty(t, WIDE_STRIDE, dtype=x.dtype, device=x.device)[:, :h * d].view(t, h, d)
+    w.copy_(x)
+    assert w.stride(0) == WIDE_STRIDE
+    return w
+
+
+def test_packed_keys_at_the_largest_accepted_stride(cuda):
+    """Keys, values and context keys whose token rows lie 16 MiB apart: the 24-bit row offsets of the tiles reach
+    their largest values. MLA prefill's widths over context keys, and causal varlen_with_lse, give the same bits as
+    with packed tensors; the context call also matches the dense oracle."""
+    dtype, heads, qk, vd = torch.bfloat16, 16, 192, 128
+    gen = torch.Generator().manual_seed(7)
+    lens_q, lens_c = [70, 5], [65, 3]
+    q = rnd(sum(lens_q), heads, qk, gen=gen, dtype=dtype, device=cuda)
+    k = rnd(sum(lens_q), heads, qk, gen=gen, dtype=dtype, device=cuda)
+    v = rnd(sum(lens_q), heads, vd, gen=gen, dtype=dtype, device=cuda)
+    kc = rnd(sum(lens_c), heads, qk, gen=gen, dtype=dtype, device=cuda)
+    vc = rnd(sum(lens_c), heads, vd, gen=gen, dtype=dtype, device=cuda)
+    cu_q, cu_c = cumulative(lens_q, cuda), cumulative(lens_c, cuda)
+    b = MI355XAttention(heads, qk, SCALE, heads)
+    wk, wv, wkc, wvc = widen(k), widen(v), widen(kc), widen(vc)
+    out, lse = b.prefill_with_context(q, k, v, kc, vc, cu_q, cu_c, max(lens_q), want_lse=True)
+    w_out, w_lse = b.prefill_with_context(q, wk, wv, wkc, wvc, cu_q, cu_c, max(lens_q), want_lse=True)
+    o, ls = b.varlen_with_lse(q, k, v, cu_q, cu_q, max(lens_q), max(lens_q), True)
+    w_o, w_ls = b.varlen_with_lse(q, wk, wv, cu_q, cu_q, max(lens_q), max(lens_q), True)
+    torch.cuda.synchronize()
+    assert torch.equal(w_out, out) and torch.equal(w_lse, lse)
+    assert torch.equal(w_o, o) and torch.equal(w_ls, ls)
+    qs, ks, vs = [], [], []
+    oq = oc = 0
+    for nq, nc in zip(lens_q, lens_c):
+        qs.append(q[oq:oq + nq])
+        ks.append(torch.cat([kc[oc:oc + nc], k[oq:oq + nq]]))
+        vs.append(torch.cat([vc[oc:oc + nc], v[oq:oq + nq]]))
+        oq, oc = oq + nq, oc + nc
+    want, want_lse = dense_rows(qs, ks, vs, True)
+    torch.testing.assert_close(w_out.float().cpu(), want, **TOL[dtype])
+    torch.testing.assert_close(w_lse.cpu(), want_lse, **TOL[dtype])
+
+
 @pytest.mark.parametrize("factor", [6, 40])
 @pytest.mark.parametrize("causal", [True, False], ids=["causal", "unmasked"])
 @pytest.mark.parametrize("dtype, dim", CASES, ids=IDS)
