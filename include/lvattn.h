@@ -153,7 +153,7 @@ int lv_paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h, co
 #define LV_KERNEL_NONE 0
 #define LV_KERNEL_DECODE_LIST 1    /* one workgroup per decode item of the work list */
 #define LV_KERNEL_DECODE_BESIDE 2  /* persistent grid taking decode items by ticket, beside prompt_overlap */
-#define LV_KERNEL_DECODE_GRID 3    /* one workgroup per (row, split, kv head, head group); no work list (> 4096 rows) */
+#define LV_KERNEL_DECODE_GRID 3    /* one workgroup per (row, kv head, head group), unsplit; no work list (> 4096 rows) */
 #define LV_KERNEL_PROMPT_LIST 4    /* one workgroup per prompt item, on the whole GPU */
 #define LV_KERNEL_PROMPT_OVERLAP 5 /* persistent prompt workgroups on part of the CUs, beside the decode items */
 #define LV_KERNEL_MIXED_SMALL 6    /* prompt and decode items of a small mixed step in one launch */

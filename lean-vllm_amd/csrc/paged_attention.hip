@@ -515,7 +515,8 @@ __global__ __launch_bounds__(256, 2) void mixed_small_kernel(AttnParams p, int32
   }
 }
 
-// Decode of more rows than the planner holds: blockIdx.x is (row, split), blockIdx.y the query-head group.
+// Decode of more rows than the planner holds: blockIdx.x is (row, split), blockIdx.y the query-head group. Such a
+// step is planned unsplit (max_splits 1): a split row's partials need the merge counters of a work list.
 template <typename T, int D, int GS, int HP>
 __global__ __launch_bounds__(256) void decode_grid_kernel(AttnParams p) {
   __shared__ __attribute__((aligned(16))) char smem[SmemBytes<D, GS, HP>::kDecode];
