@@ -60,10 +60,11 @@ __device__ inline int key_len(const AttnParams& p, int row) {
 // that cross it. DQK: q.k width; DV: value width.
 // The row max, in at most two passes over the item's tiles:
 // - held (the first pass; bf16 only, whose P operands hold the fp32 range): taken from the item's first tile and
-//   held, so later tiles compute no max and never rescale. Every query row sees its first tile's keys (key 0, or the context keys, come first), so on ordinary
-//   data a row's first-tile max sits within a few log2 units of its final one. After the last tile every row sum
-//   must be finite and below kHeldLimit (all probabilities <= 2^kHeldSlack); otherwise (scores that rose far above
-//   a row's first tile, or non-finite ones) the workgroup makes the second pass;
+//   held, so later tiles compute no max and never rescale. Every query row sees its first tile's keys (key 0, or
+//   the context keys, come first), so on ordinary data a row's first-tile max sits within a few log2 units of its
+//   final one. After the last tile every row sum must be finite and below kHeldLimit (all probabilities <=
+//   2^kHeldSlack); otherwise (scores that rose far above a row's first tile, or non-finite ones) the workgroup
+//   makes the second pass;
 // - running (the second pass): replaced only when a tile raises it by more than kRescaleSlack (log2 units), so
 //   rescaling the accumulators is rare and probabilities stay <= 2^kRescaleSlack.
 

@@ -56,10 +56,10 @@ struct MlaParams {
 
 // ---------------------------------------------------------------------------------------------------------
 // Split schedule: latents move from HBM straight into LDS (global_load_lds_dwordx4), a ring of kMlaSplitStages
-// 16-latent stages with all but one in flight while one is consumed; no registers stage data. Each wave computes the stage's
-// whole S^T (16 latents x 16 heads, K = 576) from LDS, then O^T for its 128 output dims with MFMA 16x16x16 whose
-// V^T operands come from one transposing LDS read each. One unfenced barrier per stage; every wait on the stage
-// loads is an explicit vmcnt.
+// 16-latent stages with all but one in flight while one is consumed; no registers stage data. Each wave computes
+// the stage's whole S^T (16 latents x 16 heads, K = 576) from LDS, then O^T for its 128 output dims with MFMA
+// 16x16x16 whose V^T operands come from one transposing LDS read each. One unfenced barrier per stage; every wait
+// on the stage loads is an explicit vmcnt.
 
 constexpr int kDmaTile = 16;                            // latents per stage
 constexpr int kDmaRowSlots = kLatChunks + 2;            // 16-byte slots per LDS row (two pad slots: pitch 1184 B)
@@ -389,7 +389,8 @@ __global__ __launch_bounds__(256) void mla_run_kernel(MlaParams p) {
   cons = prod;
 
   // This wave's loads j = wave + 4 i (i < 5) of a stage's 19: slot 64 j + lane is 16-byte chunk `part` of row r
-  // (latent or head) of the stage. Slots 74 r + 72 and 74 r + 73 of row r are LDS padding, filled with copies of chunk 71.
+  // (latent or head) of the stage. Slots 74 r + 72 and 74 r + 73 of row r are LDS padding, filled with copies of
+  // chunk 71.
   int lrow[5], lpart[5];
 #pragma unroll
   for (int i = 0; i < 5; ++i) {
