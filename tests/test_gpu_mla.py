@@ -90,7 +90,8 @@ def test_mla_decode_of_many_ragged_rows(cuda, queries):
     check_mla(cuda, torch.bfloat16, 64, lens, tables, queries=queries, heads=16, seed=7)
 
 
-def test_mla_decode_of_more_units_than_the_runs_hold(cuda):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_mla_decode_of_more_units_than_the_runs_hold(cuda, dtype):
     """8200 rows of one query and 16 heads: more (row, query, head tile) units than the balanced runs' in-kernel
     scan holds, so the split schedule (one workgroup per row and split, then the split merge) serves a page size
     that is a multiple of 16; rows of 1 to 300 latents, checked against TorchMath.mla_decode slice by slice."""
@@ -107,8 +108,8 @@ def test_mla_decode_of_more_units_than_the_runs_hold(cuda):
         n = int(need[r])
         bt[r, :n] = perm[at:at + n].to(torch.int32)
         at += n
-    cache = (torch.randn(at, bs, LATENT, generator=gen) * 0.5).to(torch.bfloat16)
-    q = torch.randn(rows, heads, LATENT, generator=gen).to(torch.bfloat16)
+    cache = (torch.randn(at, bs, LATENT, generator=gen) * 0.5).to(dtype)
+    q = torch.randn(rows, heads, LATENT, generator=gen).to(dtype)
     ctx = Context(context_lens=lens.to(torch.int32).to(cuda), block_tables=bt.to(cuda))
     out = MI355XAttention(heads, LATENT, SCALE, heads).mla_decode(q.to(cuda), cache.to(cuda), VDIM, ctx)
     torch.cuda.synchronize()
@@ -117,7 +118,7 @@ def test_mla_decode_of_more_units_than_the_runs_hold(cuda):
         sl = slice(r0, min(r0 + 1024, rows))
         sub = A.context(context_lens=lens[sl].to(torch.int32), block_tables=bt[sl])
         want = math_.mla_decode(q[sl], cache, VDIM, sub)
-        torch.testing.assert_close(out[sl].float().cpu(), want, **TOL[torch.bfloat16])
+        torch.testing.assert_close(out[sl].float().cpu(), want, **TOL[dtype])
 
 
 def test_mla_rows_with_no_latents_give_zeros(cuda):

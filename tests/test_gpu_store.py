@@ -37,20 +37,22 @@ def test_store_matches_the_oracle_bit_for_bit(cuda, dtype, layout):
 
 
 @pytest.mark.parametrize("heads,dim,dtype", [(1, 2, torch.float16), (1, 4, torch.float16), (3, 64, torch.bfloat16),
-                                             (16, 128, torch.bfloat16), (5, 24, torch.float32)])
+                                             (16, 128, torch.bfloat16), (5, 24, torch.float32), (3, 7, torch.uint8),
+                                             (3, 1, torch.float16)])
 @pytest.mark.parametrize("tokens", [1, 2, 3, 5, 7, 41])
 def test_store_row_widths_and_token_tails(cuda, heads, dim, dtype, tokens):
     """Rows of one or two pieces (fewer copying threads than a workgroup's four tokens), rows spread over two thread
-    shares (16 x 128 bf16 = 4 KB per token), and token counts that leave a last workgroup short: bit-exact."""
+    shares (16 x 128 bf16 = 4 KB per token), token counts that leave a last workgroup short, and rows whose widths
+    allow only 1- or 2-byte pieces (7 one-byte elements per head; one fp16 element per head): bit-exact."""
     bs, blocks = 16, 4
     gen = torch.Generator().manual_seed(tokens * 100 + dim)
-    key = (torch.randn(tokens, heads, dim, generator=gen) * 3).to(dtype)
-    value = (torch.randn(tokens, heads, dim, generator=gen) * 3).to(dtype)
+    key, value = ((torch.randn(tokens, heads, dim, generator=gen) * 3).to(dtype) if dtype.is_floating_point else
+                  torch.randint(0, 256, (tokens, heads, dim), generator=gen).to(dtype) for _ in range(2))
     slots = torch.randperm(blocks * bs, generator=gen)[:tokens].to(torch.int32)
     if tokens > 2:
         slots[tokens // 2] = -1
-    kc = torch.full((blocks, bs, heads, dim), 7.0, dtype=dtype)
-    vc = torch.full((blocks, bs, heads, dim), -7.0, dtype=dtype)
+    kc = torch.full((blocks, bs, heads, dim), 7, dtype=dtype)
+    vc = torch.full((blocks, bs, heads, dim), 9 if dtype == torch.uint8 else -7, dtype=dtype)
     want_k, want_v = kc.clone(), vc.clone()
     S.store_kvcache(key, value, want_k, want_v, slots)
     dk, dv = kc.to(cuda), vc.to(cuda)
@@ -59,13 +61,16 @@ def test_store_row_widths_and_token_tails(cuda, heads, dim, dtype, tokens):
     assert torch.equal(dk.cpu(), want_k) and torch.equal(dv.cpu(), want_v)
 
 
-@pytest.mark.parametrize("dim,dtype", [(576, torch.bfloat16), (4, torch.float16), (1152, torch.bfloat16)])
+@pytest.mark.parametrize("dim,dtype", [(576, torch.bfloat16), (4, torch.float16), (1152, torch.bfloat16),
+                                       (5, torch.uint8), (1, torch.float16), (2, torch.float16)])
 def test_store_latent_widths(cuda, dim, dtype):
-    """Latents of 576 (one thread share), 4 (one piece) and 1152 elements (two shares of 128 threads)."""
+    """Latents of 576 (one thread share), 4 (one piece) and 1152 elements (two shares of 128 threads), and rows of
+    5, 2 and 4 bytes (1-, 2- and 4-byte pieces)."""
     gen = torch.Generator().manual_seed(dim)
-    latent = torch.randn(9, dim, generator=gen).to(dtype)
+    latent = (torch.randn(9, dim, generator=gen).to(dtype) if dtype.is_floating_point else
+              torch.randint(0, 256, (9, dim), generator=gen).to(dtype))
     slots = torch.tensor([5, -1, 0, 63, 17, -1, 40, 2, 33], dtype=torch.int32)
-    cache = torch.full((2, 32, dim), 7.0, dtype=dtype)
+    cache = torch.full((2, 32, dim), 7, dtype=dtype)
     want = cache.clone()
     S.store_latents(latent, want, slots.tolist())
     got = cache.to(cuda)
