@@ -156,14 +156,16 @@ def test_a_small_mixed_step_in_one_launch(cuda, monkeypatch, dtype, dim, group, 
 
 
 @pytest.mark.parametrize("bs", [16, 32, 48, 64])
+@pytest.mark.parametrize("group", ["g1", "g2", "g4"])
 @pytest.mark.parametrize("dim", [64, 128])
 @pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
-def test_a_small_mixed_step_of_kv_head_pairs_in_one_launch(cuda, monkeypatch, dtype, dim, bs):
-    """The Qwen3-0.6B step's shape (16 query heads over 8 kv heads; 30 decode rows of up to 2048 keys beside two
-    chunks): enough decode items for kv-head pairs, still one launch."""
+def test_a_small_mixed_step_of_kv_head_pairs_in_one_launch(cuda, monkeypatch, dtype, dim, group, bs):
+    """The Qwen3-0.6B step's rows (30 decode rows of up to 2048 keys beside two chunks) over 8 kv heads: enough
+    decode items for kv-head pairs, still one launch."""
+    heads, kv = GROUPS[group]
     dec = _lens(30, 64, 2048, seed=4)
     num_cached, num_new = [0, 256] + [n - 1 for n in dec], [512, 384] + [1] * len(dec)
-    out, info, rows = _run(cuda, dtype, dim, bs, 16, 8, num_cached, num_new, B.SCHEDULE_OVERLAP, monkeypatch,
+    out, info, rows = _run(cuda, dtype, dim, bs, heads, kv, num_cached, num_new, B.SCHEDULE_OVERLAP, monkeypatch,
                            seed=4)
     _route(info, decode_kernel="mixed_small", prompt_kernel="mixed_small", kv_heads_per_item=2)
     _check(out, rows, dtype)
